@@ -1,0 +1,114 @@
+"""ctypes binding of ``libcfa.so`` (the C ABI declared in include/cudaforge_amd.h).
+
+The library is loaded from the package directory only (it is built in-tree by
+``cudaforge_amd._build``).  There is no fallback: if the library is missing,
+every entry point raises ``RuntimeError`` naming the build command.
+
+Error mapping follows the reference's pybind layer: a C-ABI ``CFA_ERR_ARG`` is
+the ``std::invalid_argument`` of ``csrc/src/scheduler/speculative.cpp:58-62``
+and surfaces as ``ValueError``; ``CFA_ERR_HIP`` surfaces as ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcfa.so")
+
+CFA_OK = 0
+CFA_ERR_ARG = -1
+CFA_ERR_HIP = -2
+
+CFA_INPUT_PROBS = 0
+CFA_INPUT_LOGITS = 1
+
+CFA_MODE_CPP = 0
+CFA_MODE_PYTHON = 1
+CFA_MODE_GREEDY = 2
+
+_i = ctypes.c_int
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+_p = ctypes.c_void_p
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_dp = ctypes.POINTER(ctypes.c_double)
+_ip = ctypes.POINTER(ctypes.c_int)
+
+# name -> (restype, argtypes); every symbol the header declares.
+SIGNATURES: dict[str, tuple] = {
+    "cfa_last_error": (ctypes.c_char_p, []),
+    "cfa_version": (_i, []),
+    "cfa_chain_verify_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
+    "cfa_chain_verify": (
+        _i,
+        [_p, _i64, _i64, _p, _i64, _i64, _i, _p, _p, _i, _i, _i, _f, _f, _i, _i32,
+         _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p],
+    ),
+    "cfa_rng_create": (_p, [_u64]),
+    "cfa_rng_destroy": (None, [_p]),
+    "cfa_rng_peek": (_i, [_p, _i, _f32p]),
+    "cfa_rng_advance": (_i, [_p, _i]),
+    "cfa_profile_enable": (_i, [_i]),
+    "cfa_profile_reset": (_i, []),
+    "cfa_profile_query": (_i, [ctypes.c_char_p, _ip, _dp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libcfa.so (once) and declare every entry point's signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build the HIP library with "
+                    "`python -m cudaforge_amd._build` (there is no CPU fallback)")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    msg = load().cfa_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    """Raise the Python exception that corresponds to a C-ABI return code."""
+    if rc == CFA_OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if rc == CFA_ERR_ARG:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def profile_enable(on: bool) -> None:
+    check(load().cfa_profile_enable(1 if on else 0), "cfa_profile_enable")
+
+
+def profile_reset() -> None:
+    check(load().cfa_profile_reset(), "cfa_profile_reset")
+
+
+def profile_query(kernel: str) -> tuple[int, float]:
+    """(launch count, summed duration in ms) of `kernel` since the last reset."""
+    n = ctypes.c_int(0)
+    ms = ctypes.c_double(0.0)
+    check(load().cfa_profile_query(kernel.encode(), ctypes.byref(n), ctypes.byref(ms)),
+          "cfa_profile_query")
+    return n.value, ms.value

@@ -1,0 +1,152 @@
+"""Tensor-level entry points of the verification path (PyTorch-ROCm host side).
+
+Each function validates shapes, dtypes, devices and strides on the host,
+allocates outputs and workspace with torch's caching allocator, and calls one
+C-ABI entry point of ``libcfa.so`` on torch's current HIP stream.  Nothing here
+computes on the CPU: without the HIP library every call raises.
+
+Reference semantics (paths inside Bahaa-Labs/CUDAForge):
+  chain_verify, mode="cpp"     csrc/src/scheduler/speculative.cpp:50-103
+  chain_verify, mode="greedy"  csrc/src/scheduler/speculative.cpp:105-150
+  chain_verify, mode="python"  cudaforge/speculative.py:152-195
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_MODES = {"cpp": _lib.CFA_MODE_CPP, "python": _lib.CFA_MODE_PYTHON, "greedy": _lib.CFA_MODE_GREEDY}
+_KINDS = {"probs": _lib.CFA_INPUT_PROBS, "logits": _lib.CFA_INPUT_LOGITS}
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require_cuda(name: str, t: torch.Tensor, dtype: torch.dtype, device=None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a HIP device tensor (got {t.device})")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype} (got {t.dtype})")
+
+
+@dataclass
+class ChainVerifyOutput:
+    """Per-sequence results of one chain verification (all int32 device tensors).
+
+    accept_len   [B]      accepted draft tokens (python mode: the batch-wide n)
+    tokens       [B, K+1] accepted drafts then the final token, -1 padded
+    num_emitted  [B]      valid entries of ``tokens``
+    final        [B]      the resampled or bonus token (final_token)
+    eos          [B]      end_of_sequence flag (cpp / greedy modes)
+    target_probs / draft_probs  the fp32 probabilities the decisions used, when
+                          ``return_probs`` was set
+    """
+
+    accept_len: torch.Tensor
+    tokens: torch.Tensor
+    num_emitted: torch.Tensor
+    final: torch.Tensor
+    eos: torch.Tensor
+    target_probs: Optional[torch.Tensor] = None
+    draft_probs: Optional[torch.Tensor] = None
+
+
+def chain_workspace_bytes(B: int, K: int, V: int, input_kind: str = "logits",
+                          mode: str = "cpp") -> int:
+    return int(_lib.load().cfa_chain_verify_workspace_size(B, K, V, _KINDS[input_kind],
+                                                            _MODES[mode]))
+
+
+def chain_verify(target: torch.Tensor, draft: Optional[torch.Tensor],
+                 draft_tokens: torch.Tensor, uniforms: Optional[torch.Tensor], *,
+                 input_kind: str = "logits", temperature: float = 1.0, top_p: float = 1.0,
+                 mode: str = "cpp", eos_token_id: int = -1, return_probs: bool = False,
+                 workspace: Optional[torch.Tensor] = None) -> ChainVerifyOutput:
+    """Verify B chains of K draft tokens in one pass over the logits.
+
+    target [B, K+1, V] fp32 and draft [B, K, V] fp32 (None in greedy mode) may be
+    strided views (the last dimension must be contiguous); draft_tokens [B, K]
+    int32; uniforms [B, K+1] fp32 in [0, 1) (None in greedy mode).
+
+    input_kind "logits": probabilities are softmax(row / temperature), fused
+    into the kernel; "probs": rows are probabilities (temperature unused).
+    """
+    if mode not in _MODES:
+        raise ValueError(f"mode must be one of {sorted(_MODES)}")
+    if input_kind not in _KINDS:
+        raise ValueError(f"input_kind must be one of {sorted(_KINDS)}")
+    _require_cuda("target", target, torch.float32)
+    dev = target.device
+    if target.dim() != 3:
+        raise ValueError("target must be [B, K+1, V]")
+    B, K1, V = target.shape
+    K = K1 - 1
+    if B <= 0 or V <= 0 or K < 0:
+        raise ValueError("target must be [B, K+1, V] with B, V > 0")
+    if target.stride(2) != 1:
+        raise ValueError("target's vocabulary dimension must be contiguous")
+    _require_cuda("draft_tokens", draft_tokens, torch.int32, dev)
+    if tuple(draft_tokens.shape) != (B, K):
+        raise ValueError(f"draft_tokens must be [B, K] = [{B}, {K}]")
+    draft_tokens = draft_tokens.contiguous()
+    greedy = mode == "greedy"
+    if not greedy:
+        if draft is None or uniforms is None:
+            raise ValueError("draft and uniforms are required outside greedy mode")
+        _require_cuda("draft", draft, torch.float32, dev)
+        if tuple(draft.shape) != (B, K, V):
+            raise ValueError("Incompatible draft and target tensor dimensions in SpeculativeEngine.")
+        if K > 0 and draft.stride(2) != 1:
+            raise ValueError("draft's vocabulary dimension must be contiguous")
+        _require_cuda("uniforms", uniforms, torch.float32, dev)
+        if tuple(uniforms.shape) != (B, K + 1):
+            raise ValueError(f"uniforms must be [B, K+1] = [{B}, {K + 1}]")
+        uniforms = uniforms.contiguous()
+    if input_kind == "logits" and not temperature > 0.0:
+        raise ValueError("temperature must be > 0")
+
+    lib = _lib.load()
+    ws_need = int(lib.cfa_chain_verify_workspace_size(B, K, V, _KINDS[input_kind], _MODES[mode]))
+    if workspace is None or workspace.numel() < ws_need:
+        workspace = torch.empty(max(ws_need, 1), dtype=torch.uint8, device=dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    out = ChainVerifyOutput(
+        accept_len=torch.empty(B, **i32), tokens=torch.empty(B, K + 1, **i32),
+        num_emitted=torch.empty(B, **i32), final=torch.empty(B, **i32),
+        eos=torch.empty(B, **i32))
+    if return_probs:
+        out.target_probs = torch.empty(B, K + 1, V, dtype=torch.float32, device=dev)
+        if not greedy and K > 0:
+            out.draft_probs = torch.empty(B, K, V, dtype=torch.float32, device=dev)
+    d_sb = d_sk = 0
+    if draft is not None and not greedy:
+        d_sb, d_sk = draft.stride(0), draft.stride(1)
+        if K == 0:
+            d_sb = d_sk = V
+    with torch.cuda.device(dev):
+        rc = lib.cfa_chain_verify(
+            target.data_ptr(), target.stride(0), target.stride(1),
+            None if greedy or draft is None else draft.data_ptr(), d_sb, d_sk,
+            _KINDS[input_kind], draft_tokens.data_ptr(),
+            None if uniforms is None else uniforms.data_ptr(),
+            B, K, V, ctypes.c_float(temperature), ctypes.c_float(top_p), _MODES[mode],
+            int(eos_token_id), out.accept_len.data_ptr(), out.tokens.data_ptr(),
+            out.num_emitted.data_ptr(), out.final.data_ptr(), out.eos.data_ptr(),
+            _ptr(out.target_probs), _ptr(out.draft_probs), workspace.data_ptr(),
+            workspace.numel(), _stream_ptr(dev))
+    _lib.check(rc, "cfa_chain_verify")
+    return out

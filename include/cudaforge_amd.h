@@ -1,0 +1,136 @@
+/*
+ * cudaforge_amd.h -- C ABI of the MI355X (gfx950) speculative-decoding
+ * verification library (libcfa.so).
+ *
+ * Every entry point takes plain pointers and sizes.  Pointers named as device
+ * buffers are HIP device addresses (e.g. torch.Tensor.data_ptr()); `stream` is
+ * a hipStream_t (NULL = default stream) and all device work is enqueued on it
+ * in order, without host synchronisation.  The library allocates no device
+ * memory: scratch space is the caller's `workspace`.
+ *
+ * Errors: every function returns CFA_OK (0) or a negative code; the message
+ * of the calling thread's last failure is available from cfa_last_error().
+ * CFA_ERR_ARG corresponds to the std::invalid_argument the reference throws
+ * (surfaced by its pybind layer as ValueError); CFA_ERR_HIP is a HIP runtime
+ * failure.  No C++ exception crosses this boundary.
+ *
+ * Reference interfaces replaced (paths inside Bahaa-Labs/CUDAForge):
+ *   cudaforge/speculative.py:27-217            SpeculativeEngine.step (python)
+ *   csrc/include/cudaforge/scheduler/speculative.h:14-88, bound at
+ *   csrc/bindings/pybind_module.cpp:196-239    SpeculativeEngine (C++)
+ *   csrc/include/cudaforge/memory/paged_kv_cache.h:81-94
+ *                                              KVCacheBatchDescriptor layout
+ */
+#ifndef CUDAFORGE_AMD_H
+#define CUDAFORGE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CFA_OK 0
+#define CFA_ERR_ARG (-1)
+#define CFA_ERR_HIP (-2)
+
+/* input_kind */
+#define CFA_INPUT_PROBS 0  /* rows are probabilities (the C++ engine's input) */
+#define CFA_INPUT_LOGITS 1 /* rows are logits; softmax(logits / T) is fused */
+
+/* mode */
+#define CFA_MODE_CPP 0    /* per-row rules of speculative.cpp:50-103 */
+#define CFA_MODE_PYTHON 1 /* batch lock-step rules of speculative.py:152-195 */
+#define CFA_MODE_GREEDY 2 /* speculative.cpp:105-150 */
+
+/* Message of this thread's last failed call ("" if none). */
+const char *cfa_last_error(void);
+
+/* Library ABI version (major * 100 + minor). */
+int cfa_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Chain verification.
+ *
+ * Replaces SpeculativeEngine::verify_candidates / verify_candidates_greedy
+ * (speculative.h:56-68, speculative.cpp:50-150; pybind names at
+ * pybind_module.cpp:229-235) for B sequences at once, and the acceptance
+ * phase of cudaforge/speculative.py:152-195.
+ *
+ *   target   [B, K+1, V] fp32, row (b,i) at target + b*t_stride_b + i*t_stride_k
+ *   draft    [B, K,   V] fp32, row (b,i) at draft  + b*d_stride_b + i*d_stride_k
+ *            (unused in greedy mode)
+ *   input_kind  CFA_INPUT_PROBS or CFA_INPUT_LOGITS (softmax of row / temperature)
+ *   draft_tokens [B, K] int32 (token ids in [0, V); an id outside that range
+ *            is rejected with probability 0 and never dereferenced)
+ *   uniforms [B, K+1] fp32 in [0, 1):
+ *     CFA_MODE_CPP: the draws the reference takes from its mt19937, in order
+ *       (one per acceptance test, then one for the resample / bonus draw);
+ *     CFA_MODE_PYTHON: columns 0..K-1 replace torch.rand_like at
+ *       speculative.py:161, column K drives the resample / bonus draw.
+ *   top_p    nucleus threshold of the python-mode bonus draw (speculative.py:67-81)
+ *   eos_token_id  (< 0: none) CFA_MODE_CPP / GREEDY only
+ *
+ * Outputs (device, int32):
+ *   out_accept_len  [B]    accepted draft tokens (the reference's num_accepted;
+ *                          python mode: the batch-wide count n, speculative.py:166)
+ *   out_tokens      [B, K+1] accepted drafts then the final token, -1 padded
+ *   out_num_emitted [B]    valid entries of out_tokens
+ *   out_final       [B]    final_token (resample or bonus draw)
+ *   out_eos         [B]    end_of_sequence
+ *   out_target_probs / out_draft_probs (optional, may be NULL): contiguous
+ *     [B,K+1,V] / [B,K,V] copies of the probabilities the decisions used.
+ *
+ * The resample / bonus draw reproduces the reference's sequential fp32 inverse
+ * CDF (speculative.cpp:11-48) bit for bit.
+ */
+size_t cfa_chain_verify_workspace_size(int B, int K, int V, int input_kind, int mode);
+
+int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t t_stride_k,
+                     const float *draft, int64_t d_stride_b, int64_t d_stride_k,
+                     int input_kind, const int32_t *draft_tokens, const float *uniforms,
+                     int B, int K, int V, float temperature, float top_p, int mode,
+                     int32_t eos_token_id, int32_t *out_accept_len, int32_t *out_tokens,
+                     int32_t *out_num_emitted, int32_t *out_final, int32_t *out_eos,
+                     float *out_target_probs, float *out_draft_probs, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Host uniform stream of the compatibility engine.
+ *
+ * The reference's SpeculativeEngine owns a std::mt19937 seeded with rng_seed
+ * (speculative.h:83, speculative.cpp:8-9) and draws
+ * std::uniform_real_distribution<float>(0, 1) once per acceptance test and once
+ * per final draw (speculative.cpp:13-14, 64, 72).  These calls keep that
+ * stream on the host so that SpeculativeEngine(config) produces the same
+ * tokens as the reference for the same seed; the verification itself runs on
+ * the GPU through cfa_chain_verify.
+ */
+typedef struct cfa_rng cfa_rng;
+
+cfa_rng *cfa_rng_create(uint64_t seed);
+void cfa_rng_destroy(cfa_rng *rng);
+/* Copy the next n draws into out without consuming them. */
+int cfa_rng_peek(const cfa_rng *rng, int n, float *out);
+/* Consume n draws. */
+int cfa_rng_advance(cfa_rng *rng, int n);
+
+/* ---------------------------------------------------------------------------
+ * Kernel timing (no counterpart in the reference; its speculative path only
+ * reads host perf_counter around phases, cudaforge/speculative.py:107-147).
+ *
+ * When enabled, every kernel launch of this library is bracketed by two
+ * hipEvents on the stream it runs on.  cfa_profile_query() synchronises on
+ * the recorded events and returns the launch count and summed duration of one
+ * kernel name (e.g. "chain_stats"); cfa_profile_reset() drops the records.
+ */
+int cfa_profile_enable(int on);
+int cfa_profile_reset(void);
+int cfa_profile_query(const char *kernel, int *count, double *total_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUDAFORGE_AMD_H */

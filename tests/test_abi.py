@@ -1,0 +1,98 @@
+"""CPU tier: the C-ABI library loads and exports every declared entry point,
+its host-only parts (the reference's uniform stream) match the golden stream,
+and host-side validation raises before any device work."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from cudaforge_amd import _lib
+from tests import helpers as H
+
+HEADER_DIR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+
+
+def declared_functions():
+    names = []
+    for fn in sorted(os.listdir(HEADER_DIR)):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(HEADER_DIR, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(cfa_[a-z0-9_]+)\s*\(", text):
+            names.append(m.group(1))
+    return sorted(set(names))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "cfa_chain_verify" in names and "cfa_last_error" in names
+
+
+@pytest.mark.parametrize("name", declared_functions())
+def test_library_exports_declared_symbol(name):
+    lib = _lib.load()
+    assert hasattr(lib, name), f"libcfa.so does not export {name}"
+    assert name in _lib.SIGNATURES, f"cudaforge_amd._lib has no signature for {name}"
+
+
+def test_rng_stream_matches_reference_stream():
+    lib = _lib.load()
+    seeds, draws = H.mt_stream()
+    for s, row in zip(seeds, draws):
+        r = lib.cfa_rng_create(ctypes.c_uint64(int(s)))
+        out = np.zeros(1000, np.float32)
+        assert lib.cfa_rng_peek(r, 600, out.ctypes.data_as(_lib._f32p)) == 0
+        assert lib.cfa_rng_advance(r, 600) == 0
+        assert lib.cfa_rng_peek(r, 400, out[600:].ctypes.data_as(_lib._f32p)) == 0
+        lib.cfa_rng_destroy(r)
+        np.testing.assert_array_equal(out, row[:1000])
+
+
+def test_argument_errors_map_to_valueerror():
+    lib = _lib.load()
+    rc = lib.cfa_chain_verify(None, 0, 0, None, 0, 0, 1, None, None, 0, 1, 10,
+                              ctypes.c_float(1.0), ctypes.c_float(1.0), 0, -1,
+                              None, None, None, None, None, None, None, None, 0, None)
+    assert rc == _lib.CFA_ERR_ARG
+    with pytest.raises(ValueError):
+        _lib.check(rc, "cfa_chain_verify")
+    assert "positive" in _lib.last_error()
+
+
+def test_host_validation_rejects_cpu_tensors():
+    from cudaforge_amd.verify import chain_verify
+
+    t = torch.zeros(2, 3, 8)
+    with pytest.raises(ValueError):
+        chain_verify(t, torch.zeros(2, 2, 8), torch.zeros(2, 2, dtype=torch.int32),
+                     torch.zeros(2, 3))
+
+
+def test_compat_engine_dimension_errors_match_reference_message():
+    from cudaforge_amd import SpeculativeConfig, SpeculativeEngine
+
+    eng = SpeculativeEngine(SpeculativeConfig())
+    with pytest.raises(ValueError, match="Incompatible draft and target"):
+        eng.verify_candidates([1, 2], [[0.5, 0.5]], [[0.5, 0.5]] * 3, 0)
+    with pytest.raises(ValueError, match="Incompatible draft and target"):
+        eng.verify_candidates([1], [[0.5, 0.5]], [[0.5, 0.5]], 0)
+    with pytest.raises(ValueError):
+        eng.verify_candidates([5], [[0.5, 0.5]], [[0.5, 0.5]] * 2, 0)  # id >= V
+
+
+def test_compat_config_defaults_and_no_reseed():
+    from cudaforge_amd import SpeculativeConfig, SpeculativeEngine
+
+    c = SpeculativeConfig()
+    assert (c.gamma, c.temperature, c.top_p, c.rng_seed) == (5, 1.0, 1.0, 42)
+    eng = SpeculativeEngine(c)
+    c2 = SpeculativeConfig(gamma=3, rng_seed=7)
+    eng.set_config(c2)
+    assert eng.get_config().gamma == 3
+    seeds, draws = H.mt_stream()
+    idx = list(seeds).index(42)
+    np.testing.assert_array_equal(eng._peek(8), draws[idx][:8])  # still seeded with 42
