@@ -62,15 +62,19 @@ __device__ __forceinline__ const float *row_ptr(const Args &a, int b, int j) {
                   : a.drf + (long long)b * a.d_sb + (long long)(j - a.K - 1) * a.d_sk;
 }
 
-// A row's probabilities: stored probs, or logits with (max, 1/S).
+// A row's probabilities: stored probs, or logits with (max, 1/S).  load()
+// only reads memory and eval() does the arithmetic, so seq::run can keep the
+// next block's loads in flight while it sweeps the current one.
 struct Dist {
   const float *p;
   float M, invS, c;
   int logits;
-  __device__ __forceinline__ float operator()(long long i) const {
-    const float v = p[i];
+  using Raw = float;
+  __device__ __forceinline__ Raw load(long long i) const { return p[i]; }
+  __device__ __forceinline__ float eval(Raw v) const {
     return logits ? __builtin_amdgcn_exp2f((v - M) * c) * invS : v;
   }
+  __device__ __forceinline__ float operator()(long long i) const { return eval(load(i)); }
 };
 
 // (max, 1/S) of row r from the stats partials, combined in a fixed order.
@@ -352,26 +356,36 @@ __global__ __launch_bounds__(64) void decide_kernel(Args a) {
 
 struct XResid {  // max(0, t_i - d_i)            (speculative.cpp:33)
   Dist t, d;
-  __device__ __forceinline__ float operator()(long long i) const { return relu_ref(t(i) - d(i)); }
+  using Raw = float2;
+  __device__ __forceinline__ Raw load(long long i) const { return make_float2(t.load(i), d.load(i)); }
+  __device__ __forceinline__ float eval(Raw v) const { return relu_ref(t.eval(v.x) - d.eval(v.y)); }
 };
 struct XResidNorm {  // max(0, t_i - d_i) / sum    (speculative.cpp:44)
   Dist t, d;
   float S;
-  __device__ __forceinline__ float operator()(long long i) const { return relu_ref(t(i) - d(i)) / S; }
+  using Raw = float2;
+  __device__ __forceinline__ Raw load(long long i) const { return make_float2(t.load(i), d.load(i)); }
+  __device__ __forceinline__ float eval(Raw v) const {
+    return relu_ref(t.eval(v.x) - d.eval(v.y)) / S;
+  }
 };
 struct XKeep {  // top-p kept probabilities (speculative.py:67-83)
   Dist t;
   float vstar;
-  __device__ __forceinline__ float operator()(long long i) const {
-    const float p = t(i);
+  using Raw = float;
+  __device__ __forceinline__ Raw load(long long i) const { return t.load(i); }
+  __device__ __forceinline__ float eval(Raw v) const {
+    const float p = t.eval(v);
     return (p >= vstar) ? p : 0.0f;
   }
 };
 struct XKeepNorm {
   Dist t;
   float vstar, S;
-  __device__ __forceinline__ float operator()(long long i) const {
-    const float p = t(i);
+  using Raw = float;
+  __device__ __forceinline__ Raw load(long long i) const { return t.load(i); }
+  __device__ __forceinline__ float eval(Raw v) const {
+    const float p = t.eval(v);
     return ((p >= vstar) ? p : 0.0f) / S;
   }
 };

@@ -23,13 +23,16 @@
 // Algorithm (one work-group per row).  Elements are staged in blocks of
 // NT*16; thread t owns a tile of 16 consecutive elements.  An approximate
 // prefix (exact block entry + fp32 tile sums) guesses each tile's region; the
-// tile is quantised to that region's grid, giving the integer increment
-// (twice: for even and odd entry parity, which differ only at ties).  One wave
-// then walks the block: runs of tiles whose guess equals the region of the
-// exact running sum, and whose total keeps it inside the region, are applied
-// with one integer prefix sum; any other tile is replayed serially from LDS.
-// Every applied increment is validated against the exact running sum, so a
-// wrong guess costs time, never correctness.
+// tile is quantised to that region's grid, giving its integer increment for
+// an even and for an odd entry parity (they differ only through ties).  A
+// tile is thus a function parity -> increment; the exit parity follows from
+// the increment, so two tiles compose into one such function (an associative
+// operation, `compose`).  One wave then walks the block: runs of tiles whose
+// guess equals the region of the exact running sum, and whose composed
+// increment keeps it inside the region, are applied with one composition
+// scan; any other tile is replayed serially.  Every applied increment is
+// validated against the exact running sum, so a wrong guess costs time,
+// never correctness.
 #pragma once
 
 #include "common.hpp"
@@ -41,6 +44,11 @@ constexpr int kRegionMin = -126;
 constexpr uint32_t kUnitsTop = 1u << 24;  // 2^(r+1) / g_r
 constexpr uint32_t kSat = 1u << 25;       // saturated (certainly invalid) units
 constexpr uint32_t kBad = 0xFFFFFFFFu;    // tile/wave marker: replay serially
+constexpr int kAnyRegion = 0x7fff;        // an all-zero tile fits every region
+// Slack on the region guess.  The guess need not be rigorous (the walk checks
+// every applied increment against the exact running value); the slack only
+// trades guesses near a power of two for serial replays.
+constexpr float kDelta = 1.0f / 65536.0f;
 
 // Region index of s >= 0 (see above).  Zero and subnormals fall in -126.
 CFA_HD int region_of(float s) {
@@ -107,15 +115,25 @@ CFA_HD void quantize_tile(const float *x, int len, int r, uint32_t &I0, uint32_t
   I1 = b;
 }
 
-// Apply a run increment I (valid for the parity it was computed for) to the
-// exact value s in region r; returns false when the run would leave the
-// region (the caller then replays serially).
-CFA_HD bool apply_units(float &s, int r, uint32_t I) {
-  uint32_t a = units_of(s, r);
-  if (I > kUnitsTop || a + I > kUnitsTop) return false;
-  s = value_of(a + I, r);
-  return true;
+// A run of elements inside one region as a function of the entry parity:
+// e / o = grid units added when the running value enters with an even / odd
+// unit count.  e == kBad marks an invalid run.
+struct Inc {
+  uint32_t e, o;
+};
+
+CFA_HD Inc inc_identity() { return Inc{0u, 0u}; }
+
+// A then B: B sees the parity A leaves behind.
+CFA_HD Inc compose(Inc A, Inc B) {
+  Inc C;
+  C.e = sat_add(A.e, (A.e & 1u) ? B.o : B.e);
+  C.o = sat_add(A.o, ((1u + A.o) & 1u) ? B.o : B.e);
+  return C;
 }
+
+// Units added by f when entered at unit count a.
+CFA_HD uint32_t inc_at(Inc f, uint32_t a) { return (a & 1u) ? f.o : f.e; }
 
 }  // namespace seq
 }  // namespace cfa
@@ -124,7 +142,6 @@ CFA_HD bool apply_units(float &s, int r, uint32_t I) {
 namespace cfa {
 namespace seq {
 
-constexpr float kDelta = 1.0f / 2048.0f;  // slack on the region guess
 
 // LDS working set of one exact pass; NT threads, 16 elements per tile.
 template <int NT>
@@ -132,24 +149,27 @@ struct Shared {
   static constexpr int kTile = 16;
   static constexpr int kWaves = NT / 64;
   static constexpr int kBlock = NT * kTile;
-  float x[kBlock];          // staged elements of the current block
-  uint32_t tI[NT];          // tile increment (grid units) or kBad
-  int16_t treg[NT];         // tile region guess
-  uint32_t wI[kWaves];      // wave increment or kBad
-  int16_t wreg[kWaves];     // wave region
-  float wscan[kWaves];      // block scan scratch
-  float s;                  // exact running value at the current block entry
-  long long found;          // first index with r <= s_i, or -1
+  alignas(16) float x[kBlock];  // staged elements of the current block
+  Inc tI[NT];                   // tile function (e == kBad: replay serially)
+  int16_t treg[NT];             // tile region guess
+  Inc wI[kWaves];               // wave function or kBad
+  int16_t wreg[kWaves];         // wave region
+  float wscan[kWaves];          // block scan scratch
+  float s;                      // exact running value at the current block entry
+  long long found;              // first index with r <= s_i, or -1
 };
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 
-__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+// Inclusive scan of tile functions across the wave (lane order).
+__device__ __forceinline__ Inc wave_incl_compose(Inc v) {
   const int lane = lane_id();
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
-    uint32_t o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
+    Inc o;
+    o.e = __shfl_up(v.e, d, 64);
+    o.o = __shfl_up(v.o, d, 64);
+    if (lane >= d) v = compose(o, v);
   }
   return v;
 }
@@ -164,48 +184,61 @@ __device__ __forceinline__ float wave_incl_scan_f32(float v) {
   return v;
 }
 
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-  return v;
-}
-
 // Number of consecutive set bits starting at bit 0.
 __device__ __forceinline__ int trailing_ones(unsigned long long m) {
   unsigned long long inv = ~m;
   return inv ? (int)__builtin_ctzll(inv) : 64;
 }
 
-// Serial replay of one 16-element tile from LDS (all lanes redundantly).
+// Serial replay of one 16-element tile (all lanes redundantly; the four
+// 16-byte LDS reads are broadcasts and are issued before the dependent adds).
 template <int NT>
 __device__ long long serial_tile(const Shared<NT> &sh, int tile, float &s, bool cdf, float r,
                                  long long blk0) {
-  const float *x = sh.x + tile * Shared<NT>::kTile;
-  for (int k = 0; k < Shared<NT>::kTile; ++k) {
-    s = s + x[k];
-    if (cdf && r <= s) return blk0 + (long long)tile * Shared<NT>::kTile + k;
+  const float4 *x4 = reinterpret_cast<const float4 *>(sh.x + tile * Shared<NT>::kTile);
+  float x[16];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float4 q = x4[k];
+    x[4 * k] = q.x;
+    x[4 * k + 1] = q.y;
+    x[4 * k + 2] = q.z;
+    x[4 * k + 3] = q.w;
   }
-  return -1;
+  long long hit = -1;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const float t = s + x[k];
+    if (hit < 0) {
+      s = t;
+      if (cdf && r <= s) hit = blk0 + (long long)tile * Shared<NT>::kTile + k;
+    }
+  }
+  return hit;
 }
 
-// Walk the 64 tiles of wave w from exact value s (wave 0 executes).
-template <int NT>
-__device__ long long tile_sweep(const Shared<NT> &sh, int w, float &s, bool cdf, float r,
-                                long long blk0) {
+// Walk `count` items (tiles of one wave, or the waves of a block) from the
+// exact value s.  item(i) returns (function, region guess); descend(i, s)
+// replays item i exactly from s (updating s) and returns a CDF hit or -1.
+template <class Item, class Descend>
+__device__ long long walk(int count, float &s, bool cdf, float r, const Item &item,
+                          const Descend &descend) {
   const int lane = lane_id();
   int t = 0;
-  while (t < 64) {
+  while (t < count) {
     const int rs = region_of(s);
     const uint32_t a = units_of(s, rs);
     const int ti = t + lane;
     bool vin = false;
-    uint32_t I = 0;
-    if (ti < 64) {
-      uint32_t v = sh.tI[w * 64 + ti];
-      vin = (v != kBad) && ((int)sh.treg[w * 64 + ti] == rs);
-      I = vin ? v : 0u;
+    Inc f = inc_identity();
+    if (ti < count) {
+      int reg;
+      const Inc v = item(ti, reg);
+      vin = (v.e != kBad) && (reg == rs || reg == kAnyRegion);
+      if (vin) f = v;
     }
-    const uint32_t inc = wave_incl_scan_u32(I);
+    const Inc incl = wave_incl_compose(f);
+    const uint32_t inc = inc_at(incl, a);
     const bool ok = vin && (a + inc <= kUnitsTop);
     const int nvalid = trailing_ones(__ballot(ok));
     if (cdf) {
@@ -213,9 +246,9 @@ __device__ long long tile_sweep(const Shared<NT> &sh, int w, float &s, bool cdf,
       const unsigned long long hm = __ballot(hit);
       if (hm) {
         const int h = (int)__builtin_ctzll(hm);
-        const uint32_t ex = __shfl(inc - I, h, 64);
-        s = value_of(a + ex, rs);
-        return serial_tile(sh, w * 64 + t + h, s, cdf, r, blk0);
+        const uint32_t prev = __shfl(inc, h > 0 ? h - 1 : 0, 64);
+        s = value_of(a + (h > 0 ? prev : 0u), rs);
+        return descend(t + h, s);
       }
     }
     if (nvalid > 0) {
@@ -224,8 +257,8 @@ __device__ long long tile_sweep(const Shared<NT> &sh, int w, float &s, bool cdf,
       t += nvalid;
       continue;
     }
-    const long long f = serial_tile(sh, w * 64 + t, s, cdf, r, blk0);
-    if (f >= 0) return f;
+    const long long f2 = descend(t, s);
+    if (f2 >= 0) return f2;
     ++t;
   }
   return -1;
@@ -235,46 +268,25 @@ __device__ long long tile_sweep(const Shared<NT> &sh, int w, float &s, bool cdf,
 template <int NT>
 __device__ void sweep_block(Shared<NT> &sh, long long blk0, bool cdf, float r) {
   constexpr int NW = Shared<NT>::kWaves;
-  const int lane = lane_id();
   float s = sh.s;
-  long long found = -1;
-  int w = 0;
-  while (w < NW) {
-    const int rs = region_of(s);
-    const uint32_t a = units_of(s, rs);
-    const int wi = w + lane;
-    bool vin = false;
-    uint32_t I = 0;
-    if (wi < NW) {
-      uint32_t v = sh.wI[wi];
-      vin = (v != kBad) && ((int)sh.wreg[wi] == rs);
-      I = vin ? v : 0u;
-    }
-    const uint32_t inc = wave_incl_scan_u32(I);
-    const bool ok = vin && (a + inc <= kUnitsTop);
-    const int nvalid = trailing_ones(__ballot(ok));
-    if (cdf) {
-      const bool hit = (lane < nvalid) && (r <= value_of(a + inc, rs));
-      const unsigned long long hm = __ballot(hit);
-      if (hm) {
-        const int h = (int)__builtin_ctzll(hm);
-        const uint32_t ex = __shfl(inc - I, h, 64);
-        s = value_of(a + ex, rs);
-        found = tile_sweep(sh, w + h, s, cdf, r, blk0);
-        break;
-      }
-    }
-    if (nvalid > 0) {
-      const uint32_t tot = __shfl(inc, nvalid - 1, 64);
-      s = value_of(a + tot, rs);
-      w += nvalid;
-      continue;
-    }
-    found = tile_sweep(sh, w, s, cdf, r, blk0);
-    if (found >= 0) break;
-    ++w;
-  }
-  if (lane == 0) {
+  auto tile_desc = [&](int w) {
+    return [&sh, w, cdf, r, blk0](int i, float &ss) -> long long {
+      return serial_tile(sh, w * 64 + i, ss, cdf, r, blk0);
+    };
+  };
+  auto wave_item = [&sh](int i, int &reg) -> Inc {
+    reg = sh.wreg[i];
+    return sh.wI[i];
+  };
+  auto wave_desc = [&](int w, float &ss) -> long long {
+    auto tile_item = [&sh, w](int i, int &reg) -> Inc {
+      reg = sh.treg[w * 64 + i];
+      return sh.tI[w * 64 + i];
+    };
+    return walk(64, ss, cdf, r, tile_item, tile_desc(w));
+  };
+  const long long found = walk(NW, s, cdf, r, wave_item, wave_desc);
+  if (lane_id() == 0) {
     sh.s = s;
     if (found >= 0) sh.found = found;
   }
@@ -282,57 +294,85 @@ __device__ void sweep_block(Shared<NT> &sh, long long blk0, bool cdf, float r) {
 
 // Exact left-to-right fp32 accumulation of xf(0..n-1) (all NT threads call).
 // sum mode: returns s_{n-1}.  cdf mode: *idx = first i with r <= s_i, or -1.
+// XF provides Raw load(i) (memory only) and float eval(Raw): the loads of
+// block k+1 are issued before block k is swept and evaluated only at the top
+// of the next iteration, so memory latency overlaps the serial sweep.
 template <int NT, class XF>
 __device__ float run(const XF &xf, long long n, bool cdf, float r, Shared<NT> &sh,
                      long long *idx) {
   constexpr int TILE = Shared<NT>::kTile;
   constexpr int BLK = Shared<NT>::kBlock;
-  constexpr int NW = Shared<NT>::kWaves;
   const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (tid == 0) {
     sh.s = 0.0f;
     sh.found = -1;
   }
+  typename XF::Raw raw[TILE];
+#pragma unroll
+  for (int j = 0; j < TILE; ++j) {
+    const long long i = (long long)j * NT + tid;
+    if (i < n) raw[j] = xf.load(i);
+  }
   __syncthreads();
   for (long long blk0 = 0; blk0 < n; blk0 += BLK) {
-#pragma unroll 4
+#pragma unroll
     for (int j = 0; j < TILE; ++j) {
       const int m = j * NT + tid;
-      const long long i = blk0 + m;
-      sh.x[m] = (i < n) ? xf(i) : 0.0f;
+      sh.x[m] = (blk0 + m < n) ? xf.eval(raw[j]) : 0.0f;
     }
     __syncthreads();
+    const long long nb = blk0 + BLK;
+    if (nb < n) {
+#pragma unroll
+      for (int j = 0; j < TILE; ++j) {
+        const long long i = nb + (long long)j * NT + tid;
+        if (i < n) raw[j] = xf.load(i);
+      }
+    }
     const float s_blk = sh.s;
     float v[TILE];
+    const float4 *x4 = reinterpret_cast<const float4 *>(sh.x + tid * TILE);
+#pragma unroll
+    for (int k = 0; k < TILE / 4; ++k) {
+      const float4 q = x4[k];
+      v[4 * k] = q.x;
+      v[4 * k + 1] = q.y;
+      v[4 * k + 2] = q.z;
+      v[4 * k + 3] = q.w;
+    }
     float A = 0.0f;
 #pragma unroll
-    for (int k = 0; k < TILE; ++k) {
-      v[k] = sh.x[tid * TILE + k];
-      A += v[k];
-    }
+    for (int k = 0; k < TILE; ++k) A += v[k];
     const float incl = wave_incl_scan_f32(A);
     if (lane == 63) sh.wscan[wave] = incl;
     __syncthreads();
     float wpre = 0.0f;
     for (int q = 0; q < wave; ++q) wpre += sh.wscan[q];
     const float E = s_blk + (wpre + (incl - A));
-    const int r_lo = region_of(E * (1.0f - kDelta));
+    int r_lo = region_of(E * (1.0f - kDelta));
     const int r_hi = region_of((E + A) * (1.0f + kDelta));
     bool ok = (r_lo == r_hi);
-    uint32_t I0 = kBad, I1 = kBad;
-    if (ok) {
-      quantize_tile(v, TILE, r_lo, I0, I1);
-      ok = (I0 == I1) && (I0 <= kUnitsTop);
+    Inc f{kBad, kBad};
+    if (A == 0.0f) {  // x >= 0: every element is zero, the identity in any region
+      ok = true;
+      r_lo = kAnyRegion;
+      f = inc_identity();
+    } else if (ok) {
+      quantize_tile(v, TILE, r_lo, f.e, f.o);
+      ok = (f.e <= kUnitsTop) && (f.o <= kUnitsTop);
+      if (!ok) f = Inc{kBad, kBad};
     }
-    sh.tI[tid] = ok ? I0 : kBad;
+    sh.tI[tid] = f;
     sh.treg[tid] = (int16_t)r_lo;
     const unsigned long long okm = __ballot(ok);
-    const int r0 = __shfl(r_lo, 0, 64);
-    const unsigned long long same = __ballot(r_lo == r0);
-    const uint32_t tot = wave_sum_u32(ok ? I0 : 0u);
-    if (lane == 0) {
+    // the wave's region: that of its first tile with a region (all-zero waves: any)
+    const unsigned long long real = __ballot(r_lo != kAnyRegion);
+    const int r0 = real ? __shfl(r_lo, (int)__builtin_ctzll(real), 64) : kAnyRegion;
+    const unsigned long long same = __ballot(r_lo == r0 || r_lo == kAnyRegion);
+    const Inc wtot = wave_incl_compose(ok ? f : inc_identity());
+    if (lane == 63) {
       const bool uni = (okm == ~0ull) && (same == ~0ull);
-      sh.wI[wave] = uni ? (tot < kSat ? tot : kSat) : kBad;
+      sh.wI[wave] = uni ? wtot : Inc{kBad, kBad};
       sh.wreg[wave] = (int16_t)r0;
     }
     __syncthreads();
@@ -343,7 +383,6 @@ __device__ float run(const XF &xf, long long n, bool cdf, float r, Shared<NT> &s
   const float out = sh.s;
   if (idx) *idx = sh.found;
   __syncthreads();
-  (void)NW;
   return out;
 }
 

@@ -14,9 +14,9 @@ struct Emu {
   int nt, tile, nw;
   float delta;
   std::vector<float> x;      // staged block
-  std::vector<uint32_t> tI;  // per tile
+  std::vector<Inc> tI;  // per tile
   std::vector<int> treg;
-  std::vector<uint32_t> wI;
+  std::vector<Inc> wI;
   std::vector<int> wreg;
   long long serial_tiles = 0;
 
@@ -29,35 +29,37 @@ struct Emu {
     return -1;
   }
 
-  // generic run walker over items [first, first+count) with per-item (I, reg)
-  template <class GetI, class GetReg, class OnHit, class OnBad>
-  long long walk(int count, float &s, bool cdf, float r, GetI getI, GetReg getReg, OnHit onhit,
-                 OnBad onbad) {
+  // the device walk: up to 64 items per step, composed in lane order, the
+  // valid prefix applied at once; an invalid first item is descended into
+  template <class GetI, class GetReg, class Descend>
+  long long walk(int count, float &s, bool cdf, float r, GetI getI, GetReg getReg,
+                 Descend descend) {
     int t = 0;
     while (t < count) {
       int rs = region_of(s);
       uint32_t a = units_of(s, rs);
-      // longest valid prefix from t
-      uint32_t inc = 0;
+      Inc acc = inc_identity();
       int nvalid = 0;
       for (int L = t; L < count && L - t < 64; ++L) {
-        uint32_t v = getI(L);
-        bool vin = v != kBad && getReg(L) == rs;
+        Inc v = getI(L);
+        bool vin = v.e != kBad && (getReg(L) == rs || getReg(L) == kAnyRegion);
         if (!vin) break;
-        if (a + inc + v > kUnitsTop) break;
-        if (cdf && r <= value_of(a + inc + v, rs)) {
-          s = value_of(a + inc, rs);
-          return onhit(L, s);
+        Inc nxt = compose(acc, v);
+        uint32_t inc = inc_at(nxt, a);
+        if (a + inc > kUnitsTop) break;
+        if (cdf && r <= value_of(a + inc, rs)) {
+          s = value_of(a + inc_at(acc, a), rs);
+          return descend(L, s);
         }
-        inc += v;
+        acc = nxt;
         ++nvalid;
       }
       if (nvalid > 0) {
-        s = value_of(a + inc, rs);
+        s = value_of(a + inc_at(acc, a), rs);
         t += nvalid;
         continue;
       }
-      long long f = onbad(t, s);
+      long long f = descend(t, s);
       if (f >= 0) return f;
       ++t;
     }
@@ -67,14 +69,12 @@ struct Emu {
   long long tile_sweep(int w, float &s, bool cdf, float r, long long blk0) {
     return walk(
         64, s, cdf, r, [&](int L) { return tI[w * 64 + L]; }, [&](int L) { return treg[w * 64 + L]; },
-        [&](int L, float &ss) { return serial_tile(w * 64 + L, ss, cdf, r, blk0); },
         [&](int L, float &ss) { return serial_tile(w * 64 + L, ss, cdf, r, blk0); });
   }
 
   long long sweep_block(float &s, bool cdf, float r, long long blk0) {
     return walk(
         nw, s, cdf, r, [&](int L) { return wI[L]; }, [&](int L) { return wreg[L]; },
-        [&](int L, float &ss) { return tile_sweep(L, ss, cdf, r, blk0); },
         [&](int L, float &ss) { return tile_sweep(L, ss, cdf, r, blk0); });
   }
 };
@@ -87,7 +87,7 @@ extern "C" int emu_seq(const float *xin, long long n, int cdf, float r, int nt, 
   e.nt = nt;
   e.tile = 16;
   e.nw = nt / 64;
-  e.delta = delta;
+  e.delta = delta > 0.0f ? delta : kDelta;
   const int blk = nt * 16;
   e.x.resize(blk);
   e.tI.resize(nt);
@@ -123,24 +123,33 @@ extern "C" int emu_seq(const float *xin, long long n, int cdf, float r, int nt, 
       int rlo = region_of(E * (1.0f - delta));
       int rhi = region_of((E + A[t]) * (1.0f + delta));
       bool ok = rlo == rhi;
-      uint32_t I0 = kBad, I1 = kBad;
-      if (ok) {
-        quantize_tile(&e.x[(size_t)t * 16], 16, rlo, I0, I1);
-        ok = (I0 == I1) && I0 <= kUnitsTop;
+      Inc f{kBad, kBad};
+      if (A[t] == 0.0f) {
+        ok = true;
+        rlo = kAnyRegion;
+        f = inc_identity();
+      } else if (ok) {
+        quantize_tile(&e.x[(size_t)t * 16], 16, rlo, f.e, f.o);
+        ok = f.e <= kUnitsTop && f.o <= kUnitsTop;
+        if (!ok) f = Inc{kBad, kBad};
       }
-      e.tI[t] = ok ? I0 : kBad;
+      e.tI[t] = f;
       e.treg[t] = rlo;
     }
     for (int w = 0; w < e.nw; ++w) {
       bool uni = true;
-      uint32_t tot = 0;
+      Inc tot = inc_identity();
+      int r0 = kAnyRegion;
+      for (int l = 0; l < 64; ++l)
+        if (e.treg[w * 64 + l] != kAnyRegion) { r0 = e.treg[w * 64 + l]; break; }
       for (int l = 0; l < 64; ++l) {
-        uint32_t v = e.tI[w * 64 + l];
-        if (v == kBad || e.treg[w * 64 + l] != e.treg[w * 64]) uni = false;
-        else tot += v;
+        Inc v = e.tI[w * 64 + l];
+        int rg = e.treg[w * 64 + l];
+        if (v.e == kBad || (rg != r0 && rg != kAnyRegion)) uni = false;
+        else tot = compose(tot, v);
       }
-      e.wI[w] = uni ? (tot < kSat ? tot : kSat) : kBad;
-      e.wreg[w] = e.treg[w * 64];
+      e.wI[w] = uni ? tot : Inc{kBad, kBad};
+      e.wreg[w] = r0;
     }
     found = e.sweep_block(s, cdf != 0, r, blk0);
   }

@@ -31,7 +31,7 @@ def emu():
         x = np.ascontiguousarray(x, np.float32)
         s, i, ns = ctypes.c_float(), ctypes.c_longlong(), ctypes.c_longlong()
         L.emu_seq(x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), x.size, cdf,
-                  np.float32(r), nt, np.float32(1 / 2048), ctypes.byref(s), ctypes.byref(i),
+                  np.float32(r), nt, np.float32(0.0), ctypes.byref(s), ctypes.byref(i),
                   ctypes.byref(ns))
         return np.float32(s.value), i.value
     return run
