@@ -33,6 +33,30 @@ namespace chain {
 
 enum Kind : int { kNone = 0, kResid = 1, kPlain = 2, kPyBonus = 3 };
 
+// Exact multi-work-group sampler state (per sequence b).
+constexpr int kMwNT = 256;                  // threads per chunk work-group
+constexpr int kMwTile = 16;                 // elements per thread (one tile)
+constexpr int kMwChunk = kMwNT * kMwTile;   // 4096 elements per chunk
+constexpr int kMwMaxBad = 64;               // cached serial tiles per row and pass
+constexpr int kMwMaxNC = 1024;              // chunks per row (V <= 4M)
+struct MwJob {  // what sequence b still has to draw
+  int kind, row, n, eos_acc;
+  float u;
+  int pad[3];
+};
+struct MwRes {  // per sequence: residual sum, fallback flag, drawn index
+  float S;
+  int fallback, idx, pad;
+};
+struct MwRec {  // a run's function of the entry parity and its region guess
+  uint32_t e, o;
+  int reg, pad;
+};
+struct MwBad {  // a tile the walk will probably replay serially, with its values
+  int tile, pad[3];
+  float x[kMwTile];
+};
+
 struct Args {
   const float *tgt;
   long long t_sb, t_sk;
@@ -54,6 +78,16 @@ struct Args {
   float2 *apart; // [G*2] (max prob, index as bits) per (wg, row slot)
   int4 *dec;     // [B] {n_b, kind, row, eos_accepted}
   float *ufin;   // [B]
+  // exact multi-work-group sampler (see "mw" below)
+  int vec;                // rows are 16-byte aligned with V % 4 == 0
+  int NC;                 // chunks per row
+  MwJob *jobs;            // [B]
+  MwRes *res;             // [B]
+  float *csum_x, *csum_t; // [B, NC] approximate chunk sums
+  MwRec *crec;            // [2, B, NC]   chunk functions, per pass
+  MwRec *trec;            // [2, B, NC*256] tile functions, per pass
+  int *badcnt;            // [2, B]
+  MwBad *bad;             // [2, B, kMwMaxBad]
   int32_t *out_accept_len, *out_tokens, *out_num_emitted, *out_final, *out_eos;
 };
 
@@ -425,65 +459,416 @@ __device__ float topp_threshold(const Dist &t, int V, float top_p, double *red) 
   return u2f(hi);
 }
 
+// ---------------------------------------------------------------------------
+// plan: the draw each sequence still needs (python mode applies the batch
+// lock-step rule n = min_b n_b of speculative.py:166 here).
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void plan_kernel(Args a) {
+  __shared__ int nmin;
+  const int K = a.K;
+  if (threadIdx.x == 0) nmin = K;
+  __syncthreads();
+  if (a.mode == CFA_MODE_PYTHON) {
+    int local = K;
+    for (int q = threadIdx.x; q < a.B; q += blockDim.x) local = min(local, a.dec[q].x);
+    atomicMin(&nmin, local);
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < a.B; b += blockDim.x) {
+    const int4 dj = a.dec[b];
+    MwJob j;
+    j.n = dj.x;
+    j.kind = dj.y;
+    j.row = dj.z;
+    j.eos_acc = dj.w;
+    j.u = a.ufin[b];
+    j.pad[0] = j.pad[1] = j.pad[2] = 0;
+    if (a.mode == CFA_MODE_PYTHON) {
+      j.n = nmin;
+      j.kind = (nmin < K) ? kResid : kPyBonus;
+      j.row = (nmin < K) ? nmin : K;
+      j.eos_acc = 0;
+    }
+    a.jobs[b] = j;
+    a.res[b] = MwRes{0.0f, 0, -1, 0};
+    a.badcnt[b] = 0;
+    a.badcnt[a.B + b] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Exact draw over all work-groups ("mw").  For each drawing sequence:
+//   sums    (grid NC x B)  approximate fp32 chunk sums of the residual and of
+//                          the target row, used only to guess regions;
+//   records (grid NC x B)  per pass: every tile quantised in its guessed
+//                          region (seqsum.hpp), composed into a chunk
+//                          function where the chunk stays in one region;
+//                          tiles that will need a serial replay are cached;
+//   walk    (grid B)       per pass: the validated hierarchical walk
+//                          (chunks, then tiles, then serial tiles) from the
+//                          exact running value, as seq::run does per block.
+// Pass 0 sums max(0, t - d) (speculative.cpp:30-35); pass 1 searches the
+// inverse CDF of max(0, t - d) / S, or of t for a bonus draw or the
+// sum <= 1e-6 fallback (speculative.cpp:11-24, 37-45, 97).
+// ---------------------------------------------------------------------------
+
+enum MwPass : int { kPassSum = 0, kPassCdf = 1 };
+
+// The element function of a (job, pass): 0 max(0,t-d), 1 max(0,t-d)/S, 2 t.
+struct MwElem {
+  Dist t, d;
+  int fn;
+  float S;
+  __device__ __forceinline__ float eval(float tv, float dv) const {
+    if (fn == 2) return t.eval(tv);
+    const float x = relu_ref(t.eval(tv) - d.eval(dv));
+    return fn == 1 ? x / S : x;
+  }
+};
+
+__device__ __forceinline__ bool mw_active(const MwJob &j, int pass) {
+  return pass == kPassSum ? j.kind == kResid : (j.kind == kResid || j.kind == kPlain);
+}
+
+__device__ MwElem mw_elem(const Args &a, int b, const MwJob &j, int pass) {
+  MwElem e;
+  e.t = make_dist(a, b, j.row);
+  e.d = e.t;
+  e.S = 1.0f;
+  if (j.kind == kResid) e.d = make_dist(a, b, a.K + 1 + j.row);
+  if (pass == kPassSum) {
+    e.fn = 0;
+  } else {
+    const MwRes r = a.res[b];
+    e.fn = (j.kind == kResid && !r.fallback) ? 1 : 2;
+    e.S = r.S;
+  }
+  return e;
+}
+
+// Raw values of 16 consecutive elements starting at i0 (zero past V).
+__device__ __forceinline__ void mw_load16(const Args &a, const float *p, long long i0, float *v) {
+  if (a.vec && i0 + kMwTile <= a.V) {
+    const float4 *p4 = reinterpret_cast<const float4 *>(p + i0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 q = p4[k];
+      v[4 * k] = q.x;
+      v[4 * k + 1] = q.y;
+      v[4 * k + 2] = q.z;
+      v[4 * k + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kMwTile; ++k) v[k] = (i0 + k < a.V) ? p[i0 + k] : 0.0f;
+  }
+}
+
+// Evaluated elements of tile `tile` of a row (zero past V).
+__device__ __forceinline__ void mw_tile_values(const Args &a, const MwElem &e, long long tile,
+                                               float *x) {
+  const long long i0 = tile * kMwTile;
+  float tv[kMwTile], dv[kMwTile];
+  mw_load16(a, e.t.p, i0, tv);
+  if (e.fn != 2)
+    mw_load16(a, e.d.p, i0, dv);
+#pragma unroll
+  for (int k = 0; k < kMwTile; ++k) x[k] = (i0 + k < a.V) ? e.eval(tv[k], e.fn != 2 ? dv[k] : 0.0f) : 0.0f;
+}
+
+// Deterministic block sum of one float per thread (kMwNT threads).
+__device__ float mw_block_sum(float v, float *red) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kMwNT / 64; ++w) t += red[w];
+  __syncthreads();
+  return t;
+}
+
+__global__ __launch_bounds__(kMwNT) void mw_sums_kernel(Args a) {
+  __shared__ float red[kMwNT / 64];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const MwJob j = a.jobs[b];
+  if (j.kind != kResid && j.kind != kPlain) return;
+  const MwElem e = mw_elem(a, b, j, kPassSum);
+  const long long tile = (long long)c * kMwNT + threadIdx.x;
+  const long long i0 = tile * kMwTile;
+  float tv[kMwTile], dv[kMwTile];
+  mw_load16(a, e.t.p, i0, tv);
+  if (j.kind == kResid) mw_load16(a, e.d.p, i0, dv);
+  float st = 0.0f, sx = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kMwTile; ++k) {
+    if (i0 + k < a.V) {
+      const float tp = e.t.eval(tv[k]);
+      st += tp;
+      if (j.kind == kResid) sx += relu_ref(tp - e.d.eval(dv[k]));
+    }
+  }
+  st = mw_block_sum(st, red);
+  sx = mw_block_sum(sx, red);
+  if (threadIdx.x == 0) {
+    a.csum_t[(long long)b * a.NC + c] = st;
+    a.csum_x[(long long)b * a.NC + c] = sx;
+  }
+}
+
+// Approximate running value at the start of chunk c: the chunk sums before
+// it, in a fixed order (one wave).
+__device__ float mw_entry_prefix(const float *csum, int c) {
+  const int lane = threadIdx.x & 63;
+  float acc = 0.0f;
+  for (int base = 0; base < c; base += 64) {
+    float v = (base + lane < c) ? csum[base + lane] : 0.0f;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    acc += v;
+  }
+  return acc;
+}
+
+__global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
+  using namespace seq;
+  __shared__ float wsum[kMwNT / 64];
+  __shared__ Inc wfun[kMwNT / 64];
+  __shared__ int wreg[kMwNT / 64], wok[kMwNT / 64];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const MwJob j = a.jobs[b];
+  if (!mw_active(j, pass)) return;
+  const MwElem e = mw_elem(a, b, j, pass);
+  const long long rowrec = ((long long)pass * a.B + b);
+  MwRec *crec = a.crec + rowrec * a.NC;
+  MwRec *trec = a.trec + rowrec * a.NC * kMwNT;
+  // approximate entry value of this chunk
+  const float *csum = (e.fn == 2 ? a.csum_t : a.csum_x) + (long long)b * a.NC;
+  float E0 = mw_entry_prefix(csum, c);
+  if (e.fn == 1) E0 = E0 / e.S;
+  // a CDF search ends before any chunk whose entry is surely past u
+  if (pass == kPassCdf && E0 * (1.0f - 1.0f / 64.0f) > j.u) {
+    if (tid == 0) crec[c] = MwRec{kBad, kBad, kAnyRegion, 1};
+    return;
+  }
+  const long long tile = (long long)c * kMwNT + tid;
+  float x[kMwTile];
+  mw_tile_values(a, e, tile, x);
+  float A = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kMwTile; ++k) A += x[k];
+  const float incl = wave_incl_scan_f32(A);
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  float wpre = 0.0f;
+  for (int q = 0; q < wave; ++q) wpre += wsum[q];
+  const float E = E0 + (wpre + (incl - A));
+  int r_lo = region_of(E * (1.0f - kDelta));
+  const int r_hi = region_of((E + A) * (1.0f + kDelta));
+  bool ok = (r_lo == r_hi);
+  Inc f{kBad, kBad};
+  if (A == 0.0f) {
+    ok = true;
+    r_lo = kAnyRegion;
+    f = inc_identity();
+  } else if (ok) {
+    uint32_t I;
+    if (quantize_tile_fast(x, kMwTile, r_lo, I))
+      f = Inc{I, I};
+    else
+      quantize_tile(x, kMwTile, r_lo, f.e, f.o);
+    ok = (f.e <= kUnitsTop) && (f.o <= kUnitsTop);
+    if (!ok) f = Inc{kBad, kBad};
+  }
+  trec[(long long)c * kMwNT + tid] = MwRec{f.e, f.o, r_lo, 0};
+  if (!ok) {  // cache the values for the walk's serial replay
+    const int slot = atomicAdd(&a.badcnt[rowrec], 1);
+    if (slot < kMwMaxBad) {
+      MwBad *dst = a.bad + rowrec * kMwMaxBad + slot;
+      dst->tile = (int)tile;
+#pragma unroll
+      for (int k = 0; k < kMwTile; ++k) dst->x[k] = x[k];
+    }
+  }
+  // the chunk's function, if every tile is valid in one region
+  const unsigned long long okm = __ballot(ok);
+  const unsigned long long real = __ballot(r_lo != kAnyRegion);
+  const int r0 = real ? (int)seq::lane_bcast((uint32_t)r_lo, (int)__builtin_ctzll(real)) : kAnyRegion;
+  const unsigned long long same = __ballot(r_lo == r0 || r_lo == kAnyRegion);
+  const Inc wtot = wave_incl_compose(ok ? f : inc_identity());
+  if (lane == 63) {
+    wfun[wave] = wtot;
+    wreg[wave] = r0;
+    wok[wave] = (okm == ~0ull) && (same == ~0ull);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    bool uni = true;
+    int reg = kAnyRegion;
+    Inc acc = inc_identity();
+    for (int w = 0; w < kMwNT / 64; ++w) {
+      if (!wok[w]) uni = false;
+      if (wreg[w] != kAnyRegion) {
+        if (reg == kAnyRegion)
+          reg = wreg[w];
+        else if (reg != wreg[w])
+          uni = false;
+      }
+      acc = compose(acc, wfun[w]);
+    }
+    crec[c] = uni ? MwRec{acc.e, acc.o, reg, 0} : MwRec{kBad, kBad, reg, 0};
+  }
+}
+
+constexpr int kMwPrefetch = 12;  // invalid chunks whose tile records are staged up front
+
+__global__ __launch_bounds__(kMwNT) void mw_walk_kernel(Args a, int pass) {
+  using namespace seq;
+  __shared__ MwRec cr[kMwMaxNC];
+  __shared__ MwRec tr[kMwPrefetch + 1][kMwNT];
+  __shared__ int pref[kMwPrefetch];
+  __shared__ MwBad bad[kMwMaxBad];
+  __shared__ int nbad, npref;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const MwJob j = a.jobs[b];
+  if (!mw_active(j, pass)) return;
+  const MwElem e = mw_elem(a, b, j, pass);
+  const long long rowrec = ((long long)pass * a.B + b);
+  const MwRec *crec = a.crec + rowrec * a.NC;
+  const MwRec *trec = a.trec + rowrec * a.NC * kMwNT;
+  for (int c = tid; c < a.NC; c += kMwNT) cr[c] = crec[c];
+  if (tid == 0) nbad = min(a.badcnt[rowrec], kMwMaxBad);
+  __syncthreads();
+  // the first kMwPrefetch chunks without a chunk function (the walk will
+  // descend into them), in order
+  if (tid < 64) {
+    int cnt = 0;
+    for (int base = 0; base < a.NC && cnt < kMwPrefetch; base += 64) {
+      const int c = base + lane;
+      const bool inv = c < a.NC && cr[c].e == kBad && cr[c].pad != 1;
+      const unsigned long long m = __ballot(inv);
+      const int before = __builtin_popcountll(m & ((1ull << lane) - 1ull));
+      if (inv && cnt + before < kMwPrefetch) pref[cnt + before] = c;
+      cnt += __builtin_popcountll(m);
+    }
+    if (tid == 0) npref = min(cnt, kMwPrefetch);
+  }
+  for (int q = tid; q < nbad; q += kMwNT) bad[q] = a.bad[rowrec * kMwMaxBad + q];
+  __syncthreads();
+  for (int q = 0; q < npref; ++q) tr[q][tid] = trec[(long long)pref[q] * kMwNT + tid];
+  __syncthreads();
+  const bool cdf = (pass == kPassCdf);
+  const float r = j.u;
+  // Every wave runs the same walk on the same data (so the work-group can
+  // synchronise inside it); thread 0 writes the result.
+  auto serial = [&](int c, int t, float &s) -> long long {
+    const long long tile = (long long)c * kMwNT + t;
+    const int q = lane < nbad ? lane : 0;
+    const unsigned long long m = __ballot(lane < nbad && bad[q].tile == (int)tile);
+    float x[kMwTile];
+    if (m) {
+      const MwBad &bt = bad[__builtin_ctzll(m)];
+#pragma unroll
+      for (int k = 0; k < kMwTile; ++k) x[k] = bt.x[k];
+    } else {
+      mw_tile_values(a, e, tile, x);
+    }
+    long long hit = -1;
+#pragma unroll
+    for (int k = 0; k < kMwTile; ++k) {
+      const float t2 = s + x[k];
+      if (hit < 0) {
+        s = t2;
+        if (cdf && r <= s) hit = tile * kMwTile + k;
+      }
+    }
+    return hit;
+  };
+  auto chunk_item = [&](int i, int &reg) -> Inc {
+    reg = cr[i].reg;
+    return Inc{cr[i].e, cr[i].o};
+  };
+  auto chunk_desc = [&](int c, float &s) -> long long {
+    int slot = kMwPrefetch;
+    for (int q = 0; q < npref; ++q)
+      if (pref[q] == c) slot = q;
+    if (slot == kMwPrefetch) {  // not staged: load now (a skipped chunk has no records)
+      __syncthreads();
+      tr[slot][tid] = (cr[c].pad == 1) ? MwRec{kBad, kBad, kAnyRegion, 1}
+                                       : trec[(long long)c * kMwNT + tid];
+      __syncthreads();
+    }
+    const MwRec *t_ = tr[slot];
+    auto tile_item = [&](int i, int &reg) -> Inc {
+      reg = t_[i].reg;
+      return Inc{t_[i].e, t_[i].o};
+    };
+    auto tile_desc = [&](int t, float &ss) -> long long { return serial(c, t, ss); };
+    return walk(kMwNT, s, cdf, r, tile_item, tile_desc);
+  };
+  float s = 0.0f;
+  const long long found = walk(a.NC, s, cdf, r, chunk_item, chunk_desc);
+  if (tid == 0) {
+    if (!cdf) {
+      a.res[b].S = s;
+      a.res[b].fallback = (s <= 1e-6f) ? 1 : 0;  // speculative.cpp:37
+    } else {
+      a.res[b].idx = (found < 0 || found >= a.V) ? a.V - 1 : (int)found;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// python-mode bonus draw (top-p filter, renormalise, draw; speculative.py:
+// 65-84): one work-group per sequence with the block-level exact replay.
+// ---------------------------------------------------------------------------
+
 constexpr int kSampleNT = 1024;
 
-__global__ __launch_bounds__(kSampleNT) void sample_kernel(Args a) {
+__global__ __launch_bounds__(kSampleNT) void pybonus_kernel(Args a) {
   __shared__ seq::Shared<kSampleNT> sh;
   __shared__ double red[kSampleNT / 64];
-  __shared__ int nmin;
-  const int b = blockIdx.x, K = a.K, V = a.V;
-  int4 dj = a.dec[b];
-  int n = dj.x, kind = dj.y, row = dj.z;
-  const int eos_acc = dj.w;
-  const float u = a.ufin[b];
-  if (a.mode == CFA_MODE_PYTHON) {  // batch lock-step: n = min_b n_b (speculative.py:166)
-    if (threadIdx.x == 0) nmin = K;
-    __syncthreads();
-    int local = K;
-    for (int q = threadIdx.x; q < a.B; q += kSampleNT) local = min(local, a.dec[q].x);
-    atomicMin(&nmin, local);
-    __syncthreads();
-    n = nmin;
-    kind = (n < K) ? kResid : kPyBonus;
-    row = (n < K) ? n : K;
-  }
-  int fin = -1;
-  if (kind != kNone) {
-    const Dist t = make_dist(a, b, row);
-    long long idx = -1;
-    if (kind == kResid) {
-      const Dist d = make_dist(a, b, K + 1 + row);
-      const float S = seq::run<kSampleNT>(XResid{t, d}, V, false, 0.0f, sh, nullptr);
-      if (S <= 1e-6f)
-        seq::run<kSampleNT>(t, V, true, u, sh, &idx);  // speculative.cpp:37-40
-      else
-        seq::run<kSampleNT>(XResidNorm{t, d, S}, V, true, u, sh, &idx);
-    } else if (kind == kPlain) {
-      seq::run<kSampleNT>(t, V, true, u, sh, &idx);  // speculative.cpp:97
-    } else {  // python bonus: top-p filter, renormalise, draw
-      const float vstar = (a.top_p < 1.0f) ? topp_threshold<kSampleNT>(t, V, a.top_p, red) : 0.0f;
-      const float S = seq::run<kSampleNT>(XKeep{t, vstar}, V, false, 0.0f, sh, nullptr);
-      if (S > 0.0f)
-        seq::run<kSampleNT>(XKeepNorm{t, vstar, S}, V, true, u, sh, &idx);
-      else
-        seq::run<kSampleNT>(XKeep{t, vstar}, V, true, u, sh, &idx);
-    }
-    fin = (idx < 0) ? V - 1 : (int)idx;
-  }
-  if (threadIdx.x <= K) {
-    const int j = threadIdx.x;
+  const int b = blockIdx.x, V = a.V;
+  const MwJob j = a.jobs[b];
+  if (j.kind != kPyBonus) return;
+  const Dist t = make_dist(a, b, j.row);
+  long long idx = -1;
+  const float vstar = (a.top_p < 1.0f) ? topp_threshold<kSampleNT>(t, V, a.top_p, red) : 0.0f;
+  const float S = seq::run<kSampleNT>(XKeep{t, vstar}, V, false, 0.0f, sh, nullptr);
+  if (S > 0.0f)
+    seq::run<kSampleNT>(XKeepNorm{t, vstar, S}, V, true, j.u, sh, &idx);
+  else
+    seq::run<kSampleNT>(XKeep{t, vstar}, V, true, j.u, sh, &idx);
+  if (threadIdx.x == 0) a.res[b].idx = (idx < 0) ? V - 1 : (int)idx;
+}
+
+// ---------------------------------------------------------------------------
+// finish: per-sequence outputs.
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(64) void finish_kernel(Args a) {
+  const int b = blockIdx.x * 64 + threadIdx.x;
+  if (b >= a.B) return;
+  const int K = a.K;
+  const MwJob j = a.jobs[b];
+  const int n = j.n, eos_acc = j.eos_acc;
+  int fin = (j.kind == kNone) ? -1 : a.res[b].idx;
+  int32_t *ot = a.out_tokens + (long long)b * (K + 1);
+  for (int q = 0; q <= K; ++q) {
     int v = -1;
-    if (j < n) v = a.tokens[(long long)b * K + j];
-    if (j == n && !eos_acc) v = fin;
-    a.out_tokens[(long long)b * (K + 1) + j] = v;
+    if (q < n) v = a.tokens[(long long)b * K + q];
+    if (q == n && !eos_acc) v = fin;
+    ot[q] = v;
   }
-  if (threadIdx.x == 0) {
-    if (eos_acc) fin = a.eos;
-    a.out_accept_len[b] = n;
-    a.out_final[b] = fin;
-    a.out_eos[b] = (a.mode == CFA_MODE_CPP) ? ((eos_acc || fin == a.eos) ? 1 : 0) : 0;
-    a.out_num_emitted[b] = eos_acc ? n : n + 1;
-  }
+  if (eos_acc) fin = a.eos;
+  a.out_accept_len[b] = n;
+  a.out_final[b] = fin;
+  a.out_eos[b] = (a.mode == CFA_MODE_CPP) ? ((eos_acc || fin == a.eos) ? 1 : 0) : 0;
+  a.out_num_emitted[b] = eos_acc ? n : n + 1;
 }
 
 // Optional: write the probabilities the verification used.
@@ -511,14 +896,43 @@ static size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
 
 static int max_groups(int R) { return std::max(R, 8192); }
 
-extern "C" size_t cfa_chain_verify_workspace_size(int B, int K, int V, int input_kind, int mode) {
-  (void)V;
-  (void)input_kind;
-  if (B <= 0 || K < 0) return 0;
+// Workspace layout (each region 256-byte aligned).
+struct WsLayout {
+  size_t part, apart, dec, ufin, jobs, res, csum_x, csum_t, crec, trec, badcnt, bad, total;
+};
+
+static WsLayout ws_layout(int B, int K, int V, int mode) {
   const int rpb = (mode == CFA_MODE_GREEDY) ? K + 1 : 2 * K + 1;
   const size_t G = (size_t)max_groups(B * rpb);
-  return align_up(G * 2 * sizeof(float2)) * 2 + align_up((size_t)B * sizeof(int4)) +
-         align_up((size_t)B * sizeof(float));
+  const size_t NC = (size_t)((V + kMwChunk - 1) / kMwChunk);
+  const bool mw = mode != CFA_MODE_GREEDY;
+  WsLayout L{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += align_up(bytes);
+    return at;
+  };
+  L.part = take(G * 2 * sizeof(float2));
+  L.apart = take(G * 2 * sizeof(float2));
+  L.dec = take((size_t)B * sizeof(int4));
+  L.ufin = take((size_t)B * sizeof(float));
+  L.jobs = take((size_t)B * sizeof(MwJob));
+  L.res = take((size_t)B * sizeof(MwRes));
+  L.csum_x = take(mw ? (size_t)B * NC * sizeof(float) : 0);
+  L.csum_t = take(mw ? (size_t)B * NC * sizeof(float) : 0);
+  L.crec = take(mw ? 2 * (size_t)B * NC * sizeof(MwRec) : 0);
+  L.trec = take(mw ? 2 * (size_t)B * NC * kMwNT * sizeof(MwRec) : 0);
+  L.badcnt = take(2 * (size_t)B * sizeof(int));
+  L.bad = take(mw ? 2 * (size_t)B * kMwMaxBad * sizeof(MwBad) : 0);
+  L.total = o;
+  return L;
+}
+
+extern "C" size_t cfa_chain_verify_workspace_size(int B, int K, int V, int input_kind, int mode) {
+  (void)input_kind;
+  if (B <= 0 || K < 0 || V <= 0) return 0;
+  return ws_layout(B, K, V, mode).total;
 }
 
 extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t t_stride_k,
@@ -533,6 +947,8 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
   clear_error();
   if (B <= 0 || K < 0 || V <= 0) return fail_arg("B and V must be positive and K >= 0");
   if (K > kMaxK - 1) return fail_arg("K must be at most 63");
+  if ((long long)V > (long long)kMwMaxNC * kMwChunk) return fail_arg("V must be at most 4194304");
+  if (B > 65535) return fail_arg("B must be at most 65535");
   if (mode != CFA_MODE_CPP && mode != CFA_MODE_PYTHON && mode != CFA_MODE_GREEDY)
     return fail_arg("mode must be CFA_MODE_CPP, CFA_MODE_PYTHON or CFA_MODE_GREEDY");
   if (input_kind != CFA_INPUT_PROBS && input_kind != CFA_INPUT_LOGITS)
@@ -589,15 +1005,22 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
   a.C = (total + G - 1) / G;
   a.G = (int)((total + a.C - 1) / a.C);
 
+  a.vec = vec ? 1 : 0;
+  a.NC = (V + kMwChunk - 1) / kMwChunk;
+  const WsLayout L = ws_layout(B, K, V, mode);
   char *ws = (char *)workspace;
-  const size_t Gmax = (size_t)max_groups(R);
-  a.part = (float2 *)ws;
-  ws += align_up(Gmax * 2 * sizeof(float2));
-  a.apart = (float2 *)ws;
-  ws += align_up(Gmax * 2 * sizeof(float2));
-  a.dec = (int4 *)ws;
-  ws += align_up((size_t)B * sizeof(int4));
-  a.ufin = (float *)ws;
+  a.part = (float2 *)(ws + L.part);
+  a.apart = (float2 *)(ws + L.apart);
+  a.dec = (int4 *)(ws + L.dec);
+  a.ufin = (float *)(ws + L.ufin);
+  a.jobs = (MwJob *)(ws + L.jobs);
+  a.res = (MwRes *)(ws + L.res);
+  a.csum_x = (float *)(ws + L.csum_x);
+  a.csum_t = (float *)(ws + L.csum_t);
+  a.crec = (MwRec *)(ws + L.crec);
+  a.trec = (MwRec *)(ws + L.trec);
+  a.badcnt = (int *)(ws + L.badcnt);
+  a.bad = (MwBad *)(ws + L.bad);
 
   hipStream_t st = (hipStream_t)stream;
   if (a.logits) {
@@ -609,8 +1032,18 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
   if (mode == CFA_MODE_GREEDY)
     CFA_LAUNCH("chain_argmax", (argmax_kernel<256>), dim3(a.G), dim3(256), 0, st, a);
   CFA_LAUNCH("chain_decide", decide_kernel, dim3(B), dim3(64), 0, st, a);
-  if (mode != CFA_MODE_GREEDY)
-    CFA_LAUNCH("chain_sample", sample_kernel, dim3(B), dim3(kSampleNT), 0, st, a);
+  if (mode != CFA_MODE_GREEDY) {
+    const dim3 cg(a.NC, B);
+    CFA_LAUNCH("chain_plan", plan_kernel, dim3(1), dim3(256), 0, st, a);
+    CFA_LAUNCH("chain_mw_sums", mw_sums_kernel, cg, dim3(kMwNT), 0, st, a);
+    CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassSum);
+    CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(kMwNT), 0, st, a, (int)kPassSum);
+    CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassCdf);
+    CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(kMwNT), 0, st, a, (int)kPassCdf);
+    if (mode == CFA_MODE_PYTHON)
+      CFA_LAUNCH("chain_pybonus", pybonus_kernel, dim3(B), dim3(kSampleNT), 0, st, a);
+    CFA_LAUNCH("chain_finish", finish_kernel, dim3((B + 63) / 64), dim3(64), 0, st, a);
+  }
   if (out_target_probs || out_draft_probs) {
     const int rows = B * a.rpb;
     const int gx = std::min(64, (V + 255) / 256);

@@ -115,6 +115,28 @@ CFA_HD void quantize_tile(const float *x, int len, int r, uint32_t &I0, uint32_t
   I1 = b;
 }
 
+// Fast path of quantize_tile: when no element of the tile is an exact tie
+// (x / g_r = n + 1/2), both parities add the same sum of round-to-nearest
+// integers.  Returns false if some element is a tie (use quantize_tile).
+CFA_HD bool quantize_tile_fast(const float *x, int len, int r, uint32_t &I) {
+  uint32_t acc = 0;
+  bool tie = false;
+  for (int k = 0; k < len; ++k) {
+    float t = ldexp_f(x[k], 23 - r);
+    t = (t < (float)kSat) ? t : (float)kSat;
+#if defined(__HIP_DEVICE_COMPILE__)
+    const float n = __builtin_rintf(t);
+    tie |= (__builtin_fabsf(t - n) == 0.5f);
+#else
+    const float n = rintf(t);
+    tie |= (fabsf(t - n) == 0.5f);
+#endif
+    acc = sat_add(acc, (uint32_t)n);
+  }
+  I = acc;
+  return !tie;
+}
+
 // A run of elements inside one region as a function of the entry parity:
 // e / o = grid units added when the running value enters with an even / odd
 // unit count.  e == kBad marks an invalid run.
@@ -161,27 +183,56 @@ struct Shared {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 
-// Inclusive scan of tile functions across the wave (lane order).
+// DPP lane moves (GFX9 encodings): row_shr:n shifts within rows of 16 lanes
+// (zero-filled), row_bcast:15 / :31 broadcast lane 15 / 31 of a row to the
+// rows selected by the row mask.  A disabled or out-of-row lane reads 0,
+// which is the identity of both scans below.
+constexpr int kDppRowShr = 0x110;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xf, true);
+}
+
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ Inc dpp_inc(Inc v) {
+  return Inc{dpp_u32<CTRL, ROWMASK>(v.e), dpp_u32<CTRL, ROWMASK>(v.o)};
+}
+
+// Inclusive scan of tile functions across the wave in lane order (DPP:
+// Hillis-Steele inside rows of 16, then the row carries).
 __device__ __forceinline__ Inc wave_incl_compose(Inc v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    Inc o;
-    o.e = __shfl_up(v.e, d, 64);
-    o.o = __shfl_up(v.o, d, 64);
-    if (lane >= d) v = compose(o, v);
-  }
+  v = compose(dpp_inc<kDppRowShr | 1, 0xf>(v), v);
+  v = compose(dpp_inc<kDppRowShr | 2, 0xf>(v), v);
+  v = compose(dpp_inc<kDppRowShr | 4, 0xf>(v), v);
+  v = compose(dpp_inc<kDppRowShr | 8, 0xf>(v), v);
+  v = compose(dpp_inc<kDppRowBcast15, 0xa>(v), v);
+  v = compose(dpp_inc<kDppRowBcast31, 0xc>(v), v);
   return v;
 }
 
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<CTRL, ROWMASK>(__float_as_uint(v)));
+}
+
+// Inclusive fp32 prefix sum across the wave (same DPP pattern; 0.0f is the
+// zero fill).
 __device__ __forceinline__ float wave_incl_scan_f32(float v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    float o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
+  v += dpp_f32<kDppRowShr | 1, 0xf>(v);
+  v += dpp_f32<kDppRowShr | 2, 0xf>(v);
+  v += dpp_f32<kDppRowShr | 4, 0xf>(v);
+  v += dpp_f32<kDppRowShr | 8, 0xf>(v);
+  v += dpp_f32<kDppRowBcast15, 0xa>(v);
+  v += dpp_f32<kDppRowBcast31, 0xc>(v);
   return v;
+}
+
+// Value of v in lane `src` (wave-uniform src).
+__device__ __forceinline__ uint32_t lane_bcast(uint32_t v, int src) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, src);
 }
 
 // Number of consecutive set bits starting at bit 0.
@@ -246,13 +297,13 @@ __device__ long long walk(int count, float &s, bool cdf, float r, const Item &it
       const unsigned long long hm = __ballot(hit);
       if (hm) {
         const int h = (int)__builtin_ctzll(hm);
-        const uint32_t prev = __shfl(inc, h > 0 ? h - 1 : 0, 64);
+        const uint32_t prev = lane_bcast(inc, h > 0 ? h - 1 : 0);
         s = value_of(a + (h > 0 ? prev : 0u), rs);
         return descend(t + h, s);
       }
     }
     if (nvalid > 0) {
-      const uint32_t tot = __shfl(inc, nvalid - 1, 64);
+      const uint32_t tot = lane_bcast(inc, nvalid - 1);
       s = value_of(a + tot, rs);
       t += nvalid;
       continue;
@@ -358,7 +409,11 @@ __device__ float run(const XF &xf, long long n, bool cdf, float r, Shared<NT> &s
       r_lo = kAnyRegion;
       f = inc_identity();
     } else if (ok) {
-      quantize_tile(v, TILE, r_lo, f.e, f.o);
+      uint32_t I;
+      if (quantize_tile_fast(v, TILE, r_lo, I))
+        f = Inc{I, I};
+      else
+        quantize_tile(v, TILE, r_lo, f.e, f.o);
       ok = (f.e <= kUnitsTop) && (f.o <= kUnitsTop);
       if (!ok) f = Inc{kBad, kBad};
     }
@@ -367,7 +422,7 @@ __device__ float run(const XF &xf, long long n, bool cdf, float r, Shared<NT> &s
     const unsigned long long okm = __ballot(ok);
     // the wave's region: that of its first tile with a region (all-zero waves: any)
     const unsigned long long real = __ballot(r_lo != kAnyRegion);
-    const int r0 = real ? __shfl(r_lo, (int)__builtin_ctzll(real), 64) : kAnyRegion;
+    const int r0 = real ? (int)seq::lane_bcast((uint32_t)r_lo, (int)__builtin_ctzll(real)) : kAnyRegion;
     const unsigned long long same = __ballot(r_lo == r0 || r_lo == kAnyRegion);
     const Inc wtot = wave_incl_compose(ok ? f : inc_identity());
     if (lane == 63) {
