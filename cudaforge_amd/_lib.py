@@ -49,6 +49,12 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _i64, _p, _i64, _i64, _i, _p, _p, _i, _i, _i, _f, _f, _i, _i32,
          _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p],
     ),
+    "cfa_tree_attention_workspace_size": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
+    "cfa_tree_attention": (
+        _i,
+        [_p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _p, _i64, _i, _i, _i, _i, _i, _f, _i, _i,
+         _p, _p, _sz, _p],
+    ),
     "cfa_rng_create": (_p, [_u64]),
     "cfa_rng_destroy": (None, [_p]),
     "cfa_rng_peek": (_i, [_p, _i, _f32p]),

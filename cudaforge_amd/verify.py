@@ -9,6 +9,8 @@ Reference semantics (paths inside Bahaa-Labs/CUDAForge):
   chain_verify, mode="cpp"     csrc/src/scheduler/speculative.cpp:50-103
   chain_verify, mode="greedy"  csrc/src/scheduler/speculative.cpp:105-150
   chain_verify, mode="python"  cudaforge/speculative.py:152-195
+  tree_attention               paged layout of csrc/src/memory/paged_kv_cache.cpp:
+                               13-21, 409-421; descriptor of paged_kv_cache.h:81-94
 """
 from __future__ import annotations
 
@@ -149,4 +151,77 @@ def chain_verify(target: torch.Tensor, draft: Optional[torch.Tensor],
             _ptr(out.target_probs), _ptr(out.draft_probs), workspace.data_ptr(),
             workspace.numel(), _stream_ptr(dev))
     _lib.check(rc, "cfa_chain_verify")
+    return out
+
+
+def tree_attention_workspace_bytes(B: int, N: int, n_q_heads: int, n_kv_heads: int,
+                                   head_dim: int, max_keys: int, num_splits: int = 0) -> int:
+    return int(_lib.load().cfa_tree_attention_workspace_size(B, N, n_q_heads, n_kv_heads,
+                                                              head_dim, max_keys, num_splits))
+
+
+def tree_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                   block_tables: torch.Tensor, ctx_lens: torch.Tensor,
+                   tree_mask: torch.Tensor, *, layer: int = 0,
+                   sm_scale: Optional[float] = None, max_keys: Optional[int] = None,
+                   num_splits: int = 0, out: Optional[torch.Tensor] = None,
+                   workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Tree-masked attention of N draft-tree nodes over a paged KV cache.
+
+    q [B, N, Hq, D] bf16; k_pool / v_pool [num_blocks, num_layers, Hkv, block_size, D]
+    bf16 (the reference's per-block layout); block_tables [B, max_blocks] int32;
+    ctx_lens [B] int32 (tokens before the tree; the tree's K/V sit at
+    ctx_len + i); tree_mask int64 [N] or [B, N] holding each node's 64-bit
+    ancestor-or-self mask.  max_keys bounds ctx_len + N on the host (computed
+    with one sync when omitted).  Returns [B, N, Hq, D] bf16.
+    """
+    _require_cuda("q", q, torch.bfloat16)
+    dev = q.device
+    if q.dim() != 4:
+        raise ValueError("q must be [B, N, Hq, D]")
+    B, N, Hq, D = q.shape
+    q = q.contiguous()
+    for name, pool in (("k_pool", k_pool), ("v_pool", v_pool)):
+        _require_cuda(name, pool, torch.bfloat16, dev)
+        if pool.dim() != 5 or not pool.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous [blocks, layers, Hkv, block_size, D] tensor")
+    if k_pool.shape != v_pool.shape:
+        raise ValueError("k_pool and v_pool must have the same shape")
+    nblk, nlayers, Hkv, bs, Dp = k_pool.shape
+    if Dp != D:
+        raise ValueError("head_dim of q and of the pools differ")
+    _require_cuda("block_tables", block_tables, torch.int32, dev)
+    if block_tables.dim() != 2 or block_tables.shape[0] != B:
+        raise ValueError("block_tables must be [B, max_blocks]")
+    block_tables = block_tables.contiguous()
+    _require_cuda("ctx_lens", ctx_lens, torch.int32, dev)
+    if tuple(ctx_lens.shape) != (B,):
+        raise ValueError("ctx_lens must be [B]")
+    ctx_lens = ctx_lens.contiguous()
+    _require_cuda("tree_mask", tree_mask, torch.int64, dev)
+    if tree_mask.dim() == 1 and tree_mask.shape[0] == N:
+        mstride = 0
+    elif tree_mask.dim() == 2 and tuple(tree_mask.shape) == (B, N):
+        mstride = N
+    else:
+        raise ValueError("tree_mask must be [N] or [B, N]")
+    tree_mask = tree_mask.contiguous()
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    if max_keys is None:
+        max_keys = int(ctx_lens.max().item()) + N
+    if out is None:
+        out = torch.empty_like(q)
+    lib = _lib.load()
+    need = int(lib.cfa_tree_attention_workspace_size(B, N, Hq, Hkv, D, max_keys, num_splits))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.cfa_tree_attention(
+            q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
+            block_tables.shape[1], ctx_lens.data_ptr(), nblk, nlayers, int(layer), bs,
+            tree_mask.data_ptr(), mstride, B, N, Hq, Hkv, D, ctypes.c_float(sm_scale),
+            int(max_keys), int(num_splits), out.data_ptr(), workspace.data_ptr(),
+            workspace.numel(), _stream_ptr(dev))
+    _lib.check(rc, "cfa_tree_attention")
     return out

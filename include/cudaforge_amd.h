@@ -63,7 +63,7 @@ int cfa_version(void);
  *            (unused in greedy mode)
  *   input_kind  CFA_INPUT_PROBS or CFA_INPUT_LOGITS (softmax of row / temperature)
  *   draft_tokens [B, K] int32 (token ids in [0, V); an id outside that range
- *            is rejected with probability 0 and never dereferenced)
+ *            is never accepted and never dereferenced)
  *   uniforms [B, K+1] fp32 in [0, 1):
  *     CFA_MODE_CPP: the draws the reference takes from its mt19937, in order
  *       (one per acceptance test, then one for the resample / bonus draw);
@@ -95,6 +95,40 @@ int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t t_stride_k
                      int32_t *out_num_emitted, int32_t *out_final, int32_t *out_eos,
                      float *out_target_probs, float *out_draft_probs, void *workspace,
                      size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Tree-masked verification attention over a paged KV cache (bf16, MFMA).
+ *
+ * No reference kernel exists (the reference's target forward recomputes the
+ * whole prefix, cudaforge/speculative.py:139-141); the arguments mirror the
+ * reference's paged-cache descriptor KVCacheBatchDescriptor
+ * (csrc/include/cudaforge/memory/paged_kv_cache.h:81-94: block_tables,
+ * context_lens, max_blocks_per_seq, block_size, num_kv_heads, head_dim, key
+ * and value pools) and its pool layout (paged_kv_cache.cpp:13-21, 409-421):
+ *   pool[block][layer][kv_head][slot][head_dim]  bf16
+ *
+ *   q        [B, N, n_q_heads, 128] bf16 -- queries of the N draft-tree nodes
+ *   block_tables [B, max_blocks_per_seq] int32, ctx_lens [B] int32
+ *   the tree's own K/V sit at positions ctx_len .. ctx_len + N - 1
+ *   tree_mask  uint64 per node (bit j: node j is an ancestor of, or is, the
+ *              node), [N] shared (stride 0) or [B, N] (stride N)
+ *   max_keys   host-side bound on ctx_len + N over the batch (plans the splits)
+ *   num_splits key-range splits (0: automatic); splits > 1 need workspace
+ *   out        [B, N, n_q_heads, 128] bf16
+ * Query (node i, head hq) attends to context positions [0, ctx_len) and to
+ * tree positions ctx_len + j with bit j of tree_mask[i]; scores scale by
+ * sm_scale; fp32 softmax and accumulation.
+ */
+size_t cfa_tree_attention_workspace_size(int B, int N, int n_q_heads, int n_kv_heads,
+                                         int head_dim, int max_keys, int num_splits);
+
+int cfa_tree_attention(const void *q, const void *k_pool, const void *v_pool,
+                       const int32_t *block_tables, int max_blocks_per_seq,
+                       const int32_t *ctx_lens, int num_blocks, int num_layers, int layer,
+                       int block_size, const uint64_t *tree_mask, int64_t tree_mask_stride_b,
+                       int B, int N, int n_q_heads, int n_kv_heads, int head_dim,
+                       float sm_scale, int max_keys, int num_splits, void *out,
+                       void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
  * Host uniform stream of the compatibility engine.

@@ -69,3 +69,35 @@ def replay(verify_one, tok, d, t, eos, stream, greedy):
         if not greedy:
             pos += draws_used(n, K, a[-1] if n else None, eos)
     return dict(accepted=acc, num_accepted=na, final=fin, eos=ef)
+
+
+def paged_pools(K, V, block_size, num_layers=1, layer=0, extra_blocks=3, seed=0):
+    """Scatter contiguous per-sequence K/V ([B][L_b, Hkv, D] lists or a
+    [B, L, Hkv, D] tensor) into a paged pool [blocks, layers, Hkv, bs, D] with
+    a random block permutation (paged_kv_cache.cpp:13-21, 409-421).
+    Returns (k_pool, v_pool, block_tables [B, max_blocks] int32); unused
+    table entries are -1, as prepare_batch_metadata leaves them
+    (paged_kv_cache.cpp:346-347)."""
+    import torch
+
+    B = len(K)
+    lens = [int(k.shape[0]) for k in K]
+    Hkv, D = K[0].shape[1], K[0].shape[2]
+    nb = [(L + block_size - 1) // block_size for L in lens]
+    total = sum(nb) + extra_blocks
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(total, generator=g)
+    kp = torch.randn(total, num_layers, Hkv, block_size, D, generator=g).to(K[0].dtype)
+    vp = torch.randn(total, num_layers, Hkv, block_size, D, generator=g).to(V[0].dtype)
+    maxb = max(nb)
+    bt = torch.full((B, maxb), -1, dtype=torch.int32)
+    nxt = 0
+    for b in range(B):
+        for p in range(nb[b]):
+            blk = int(perm[nxt])
+            nxt += 1
+            bt[b, p] = blk
+            lo, hi = p * block_size, min((p + 1) * block_size, lens[b])
+            kp[blk, layer, :, : hi - lo, :] = K[b][lo:hi].transpose(0, 1)
+            vp[blk, layer, :, : hi - lo, :] = V[b][lo:hi].transpose(0, 1)
+    return kp, vp, bt
