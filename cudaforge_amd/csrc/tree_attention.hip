@@ -77,49 +77,84 @@ __device__ __forceinline__ uint4 ld_g16(const uint16_t *p) {
   return *reinterpret_cast<const uint4 *>(p);
 }
 
-// Global staging of one 64-key tile: each thread owns two 16-byte K chunks
-// and, for V, one (key pair, 8-wide d slice).
+// LDS row of key k within a tile: the two 16-key MFMA tiles of a 32-key
+// block read keys {8g+i} and {8g+4+i}; storing key 8g + 4T + i at row
+// 16T + 4g + i makes each MFMA tile read 16 consecutive rows, which a 272-byte
+// row stride spreads over all 64 banks.
+__device__ __forceinline__ int k_row(int key) {
+  return (key & ~31) + ((key >> 2) & 1) * 16 + ((key >> 3) & 3) * 4 + (key & 3);
+}
+
+// Global staging of one 64-key tile.  K: thread t owns the 16-byte chunks
+// (key t/16, slice t%16) and (key t/16 + 32, same slice).  V: lane l of wave
+// w owns keys 2(l%32), 2(l%32)+1 at d-slice 2w + l/32, so that the transposed
+// 4-byte LDS writes of one wave hit 64 distinct banks.
 struct Stage {
   uint4 k0, k1;
   uint4 v0, v1;
 };
 
-__device__ __forceinline__ const uint16_t *kv_ptr(const Args &a, const uint16_t *pool, int b, int h,
-                                                  int pos) {
-  const int page = min(pos / a.bs, a.max_blocks - 1);
-  int blk = a.bt[(long long)b * a.max_blocks + page];
+// Element offsets (within a pool) of the tile's pages, read with uniform
+// addresses: page j of the tile covers keys [j*bs, (j+1)*bs), j < kKT / bs.
+struct Pages {
+  long long o0, o1, o2, o3;
+};
+
+__device__ __forceinline__ long long page_off(const Args &a, const int32_t *btb, int page, int h) {
+  page = min(page, a.max_blocks - 1);
+  int blk = btb[page];
   blk = min(max(blk, 0), a.num_blocks - 1);  // stay inside the pool whatever the table holds
-  const long long off = (((long long)blk * a.num_layers + a.layer) * a.Hkv + h) * a.bs + (pos % a.bs);
-  return pool + off * kD;
+  return (((long long)blk * a.num_layers + a.layer) * a.Hkv + h) * (long long)(a.bs * kD);
+}
+
+__device__ __forceinline__ Pages tile_pages(const Args &a, int b, int h, int kbase) {
+  const int32_t *btb = a.bt + (long long)b * a.max_blocks;
+  const int p0 = kbase / a.bs, last = kKT / a.bs - 1;
+  Pages pg;
+  pg.o0 = page_off(a, btb, p0, h);
+  pg.o1 = page_off(a, btb, p0 + min(1, last), h);
+  pg.o2 = page_off(a, btb, p0 + min(2, last), h);
+  pg.o3 = page_off(a, btb, p0 + min(3, last), h);
+  return pg;
+}
+
+// Offset of the row of tile-relative key `key`.
+__device__ __forceinline__ long long key_off(const Pages &pg, int bs, int key) {
+  const int j = key / bs;
+  long long o = pg.o0;
+  o = (j == 1) ? pg.o1 : o;
+  o = (j == 2) ? pg.o2 : o;
+  o = (j == 3) ? pg.o3 : o;
+  return o + (long long)((key % bs) * kD);
 }
 
 __device__ __forceinline__ void stage_load(const Args &a, int b, int h, int kbase, int nkeys,
                                            Stage &st) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint4 z = make_uint4(0, 0, 0, 0);
+  const Pages pg = tile_pages(a, b, h, kbase);
   {
-    const int key = tid >> 4, ds = tid & 15;  // chunks tid and tid + 512: keys key, key + 32
-    st.k0 = (kbase + key < nkeys) ? ld_g16(kv_ptr(a, a.kpool, b, h, kbase + key) + ds * 8) : z;
-    st.k1 = (kbase + key + 32 < nkeys) ? ld_g16(kv_ptr(a, a.kpool, b, h, kbase + key + 32) + ds * 8)
-                                       : z;
+    const int key = tid >> 4, ds = tid & 15;
+    st.k0 = (kbase + key < nkeys) ? ld_g16(a.kpool + key_off(pg, a.bs, key) + ds * 8) : z;
+    st.k1 = (kbase + key + 32 < nkeys) ? ld_g16(a.kpool + key_off(pg, a.bs, key + 32) + ds * 8) : z;
   }
   {
-    const int kp = tid >> 4, ds = tid & 15;  // keys 2kp, 2kp+1; d slice ds
-    const int k0 = kbase + 2 * kp;
-    st.v0 = (k0 < nkeys) ? ld_g16(kv_ptr(a, a.vpool, b, h, k0) + ds * 8) : z;
-    st.v1 = (k0 + 1 < nkeys) ? ld_g16(kv_ptr(a, a.vpool, b, h, k0 + 1) + ds * 8) : z;
+    const int kp = lane & 31, ds = wave * 2 + (lane >> 5);
+    const int key = 2 * kp;
+    st.v0 = (kbase + key < nkeys) ? ld_g16(a.vpool + key_off(pg, a.bs, key) + ds * 8) : z;
+    st.v1 = (kbase + key + 1 < nkeys) ? ld_g16(a.vpool + key_off(pg, a.bs, key + 1) + ds * 8) : z;
   }
 }
 
 __device__ __forceinline__ void stage_store(Smem &sm, int buf, const Stage &st) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   {
     const int key = tid >> 4, ds = tid & 15;
-    *reinterpret_cast<uint4 *>(&sm.k[buf][key * kKPad + ds * 8]) = st.k0;
-    *reinterpret_cast<uint4 *>(&sm.k[buf][(key + 32) * kKPad + ds * 8]) = st.k1;
+    *reinterpret_cast<uint4 *>(&sm.k[buf][k_row(key) * kKPad + ds * 8]) = st.k0;
+    *reinterpret_cast<uint4 *>(&sm.k[buf][k_row(key + 32) * kKPad + ds * 8]) = st.k1;
   }
   {
-    const int kp = tid >> 4, ds = tid & 15;
+    const int kp = lane & 31, ds = wave * 2 + (lane >> 5);
     const uint32_t a[4] = {st.v0.x, st.v0.y, st.v0.z, st.v0.w};
     const uint32_t c[4] = {st.v1.x, st.v1.y, st.v1.z, st.v1.w};
 #pragma unroll
@@ -197,7 +232,7 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
       for (int T = 0; T < 2; ++T) {
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) s[qt][blk][T] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        const int krow = blk * 32 + T * 4 + 8 * (col >> 2) + (col & 3);
+        const int krow = blk * 32 + T * 16 + col;  // = k_row(blk*32 + T*4 + 8*(col/4) + col%4)
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
           const bf16x8 kf = ld_bf16x8(K + krow * kKPad + kk * 32 + g * 8);
@@ -207,8 +242,10 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
         }
       }
 
-    // scale, mask, online softmax (per query column; 4 lanes g share a column)
+    // mask, online softmax in log2 units (per query column; the 4 lanes g of
+    // a column share it)
     const bool masked_tile = kbase + kKT > ctx;
+    const float c = a.scale_log2;
     bf16x8 p[kQT][2];
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
@@ -219,11 +256,11 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
         for (int T = 0; T < 2; ++T)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            float v = s[qt][blk][T][i] * a.scale_log2;
+            float v = s[qt][blk][T][i];
             if (masked_tile) {
               const int pos = kbase + blk * 32 + T * 4 + 8 * g + i;
               const int j = pos - ctx;
-              const bool vis = pos < ctx || (j < a.N && ((anc[qt] >> j) & 1ull));
+              const bool vis = pos < ctx || (j < a.N && ((anc[qt] >> (j & 63)) & 1ull));
               v = vis ? v : -INFINITY;
             }
             s[qt][blk][T][i] = v;
@@ -231,7 +268,7 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
           }
       tmax = xor_max(tmax, 16);
       tmax = xor_max(tmax, 32);
-      const float mnew = fmaxf(m[qt], tmax);
+      const float mnew = fmaxf(m[qt], tmax * c);  // c > 0: max of scaled = scaled max
       const float base = (mnew == -INFINITY) ? 0.0f : mnew;
       const float alpha = __builtin_amdgcn_exp2f(m[qt] - base);
       m[qt] = mnew;
@@ -243,7 +280,7 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
         for (int T = 0; T < 2; ++T)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(s[qt][blk][T][i] - base);
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][blk][T][i], c, -base));
             pv[T * 4 + i] = e;
             psum += e;
           }
