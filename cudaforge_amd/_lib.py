@@ -55,6 +55,10 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _p, _i64, _i, _i, _i, _i, _i, _f, _i, _i,
          _p, _p, _sz, _p],
     ),
+    "cfa_kv_commit": (
+        _i,
+        [_p, _p, _p, _i, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p],
+    ),
     "cfa_rng_create": (_p, [_u64]),
     "cfa_rng_destroy": (None, [_p]),
     "cfa_rng_peek": (_i, [_p, _i, _f32p]),

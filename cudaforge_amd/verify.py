@@ -11,6 +11,7 @@ Reference semantics (paths inside Bahaa-Labs/CUDAForge):
   chain_verify, mode="python"  cudaforge/speculative.py:152-195
   tree_attention               paged layout of csrc/src/memory/paged_kv_cache.cpp:
                                13-21, 409-421; descriptor of paged_kv_cache.h:81-94
+  kv_commit                    device half of append_tokens, paged_kv_cache.cpp:255-286
 """
 from __future__ import annotations
 
@@ -224,4 +225,48 @@ def tree_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
             int(max_keys), int(num_splits), out.data_ptr(), workspace.data_ptr(),
             workspace.numel(), _stream_ptr(dev))
     _lib.check(rc, "cfa_tree_attention")
+    return out
+
+
+@dataclass
+class KVCommitOutput:
+    new_ctx_lens: torch.Tensor  # [B] int32: ctx_lens + path_len (unchanged when rejected)
+    status: torch.Tensor        # [B] int32: 0 committed, 1 rejected (bad path or page)
+
+
+def kv_commit(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Tensor,
+              ctx_lens: torch.Tensor, paths: torch.Tensor, path_lens: torch.Tensor
+              ) -> KVCommitOutput:
+    """Move each sequence's accepted tree nodes (paths [B, P] int32, node ids
+    with the root 0 first, path_lens [B]) from slots ctx + node to ctx + j in
+    every layer and KV head of both pools (in place)."""
+    for name, pool in (("k_pool", k_pool), ("v_pool", v_pool)):
+        if not isinstance(pool, torch.Tensor) or pool.device.type != "cuda":
+            raise ValueError(f"{name} must be a HIP device tensor")
+        if pool.dim() != 5 or not pool.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous [blocks, layers, Hkv, block_size, D] tensor")
+    if k_pool.shape != v_pool.shape or k_pool.dtype != v_pool.dtype:
+        raise ValueError("k_pool and v_pool must match in shape and dtype")
+    dev = k_pool.device
+    nblk, nlayers, Hkv, bs, D = k_pool.shape
+    _require_cuda("block_tables", block_tables, torch.int32, dev)
+    B = block_tables.shape[0]
+    for name, t, shape in (("ctx_lens", ctx_lens, (B,)), ("path_lens", path_lens, (B,))):
+        _require_cuda(name, t, torch.int32, dev)
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{name} must be [B]")
+    _require_cuda("paths", paths, torch.int32, dev)
+    if paths.dim() != 2 or paths.shape[0] != B:
+        raise ValueError("paths must be [B, max_path]")
+    block_tables, ctx_lens, paths, path_lens = (t.contiguous() for t in
+                                                (block_tables, ctx_lens, paths, path_lens))
+    out = KVCommitOutput(new_ctx_lens=torch.empty(B, dtype=torch.int32, device=dev),
+                         status=torch.empty(B, dtype=torch.int32, device=dev))
+    with torch.cuda.device(dev):
+        rc = _lib.load().cfa_kv_commit(
+            k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(), block_tables.shape[1],
+            ctx_lens.data_ptr(), paths.data_ptr(), paths.shape[1], path_lens.data_ptr(), B, nblk,
+            nlayers, Hkv, bs, D, k_pool.element_size(), out.new_ctx_lens.data_ptr(),
+            out.status.data_ptr(), _stream_ptr(dev))
+    _lib.check(rc, "cfa_kv_commit")
     return out

@@ -131,6 +131,28 @@ int cfa_tree_attention(const void *q, const void *k_pool, const void *v_pool,
                        void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
+ * KV commit / compaction of an accepted draft-tree path.
+ *
+ * Device half of the reference's append_tokens(seq, L)
+ * (csrc/src/memory/paged_kv_cache.cpp:255-286; context length :359-364),
+ * which the reference performs on host metadata only: for each sequence b the
+ * accepted nodes paths[b, 0..L) (paths[b,0] = 0, strictly increasing) move
+ * from slots ctx_lens[b] + paths[b, j] to ctx_lens[b] + j, for every layer
+ * and KV head of both pools (layout pool[block][layer][kv_head][slot][dim],
+ * paged_kv_cache.cpp:13-21, 409-421).  Rows already in place are not touched.
+ * A sequence whose path is malformed or reaches an unmapped page is left
+ * unchanged and flagged (status[b] = 1).
+ *
+ *   new_ctx_lens [B] (optional): ctx_lens + L (or ctx_lens when rejected)
+ *   status       [B] (optional): 0 committed, 1 rejected
+ */
+int cfa_kv_commit(void *k_pool, void *v_pool, const int32_t *block_tables,
+                  int max_blocks_per_seq, const int32_t *ctx_lens, const int32_t *paths,
+                  int path_stride, const int32_t *path_lens, int B, int num_blocks,
+                  int num_layers, int n_kv_heads, int block_size, int head_dim, int elem_bytes,
+                  int32_t *new_ctx_lens, int32_t *status, void *stream);
+
+/* ---------------------------------------------------------------------------
  * Host uniform stream of the compatibility engine.
  *
  * The reference's SpeculativeEngine owns a std::mt19937 seeded with rng_seed
