@@ -22,6 +22,7 @@
 #include <cmath>
 
 #include "abi_internal.hpp"
+#include "dist.hpp"
 #include "seqsum.hpp"
 
 // Every fp32 expression below must round exactly as written (the oracle and
@@ -95,21 +96,6 @@ __device__ __forceinline__ const float *row_ptr(const Args &a, int b, int j) {
   return j <= a.K ? a.tgt + (long long)b * a.t_sb + (long long)j * a.t_sk
                   : a.drf + (long long)b * a.d_sb + (long long)(j - a.K - 1) * a.d_sk;
 }
-
-// A row's probabilities: stored probs, or logits with (max, 1/S).  load()
-// only reads memory and eval() does the arithmetic, so seq::run can keep the
-// next block's loads in flight while it sweeps the current one.
-struct Dist {
-  const float *p;
-  float M, invS, c;
-  int logits;
-  using Raw = float;
-  __device__ __forceinline__ Raw load(long long i) const { return p[i]; }
-  __device__ __forceinline__ float eval(Raw v) const {
-    return logits ? __builtin_amdgcn_exp2f((v - M) * c) * invS : v;
-  }
-  __device__ __forceinline__ float operator()(long long i) const { return eval(load(i)); }
-};
 
 // (max, 1/S) of row r from the stats partials, combined in a fixed order.
 __device__ float2 row_stat(const Args &a, int r) {

@@ -12,6 +12,7 @@ Reference semantics (paths inside Bahaa-Labs/CUDAForge):
   tree_attention               paged layout of csrc/src/memory/paged_kv_cache.cpp:
                                13-21, 409-421; descriptor of paged_kv_cache.h:81-94
   kv_commit                    device half of append_tokens, paged_kv_cache.cpp:255-286
+  tree_verify                  speculative.cpp:50-150 generalised to a draft tree
 """
 from __future__ import annotations
 
@@ -269,4 +270,87 @@ def kv_commit(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Te
             nlayers, Hkv, bs, D, k_pool.element_size(), out.new_ctx_lens.data_ptr(),
             out.status.data_ptr(), _stream_ptr(dev))
     _lib.check(rc, "cfa_kv_commit")
+    return out
+
+
+@dataclass
+class TreeVerifyOutput:
+    """Per-sequence results of tree verification (int32 device tensors)."""
+
+    path: torch.Tensor         # [B, N] accepted node ids from the root, -1 padded
+    path_len: torch.Tensor     # [B] 1 + accepted drafts
+    tokens: torch.Tensor       # [B, N+1] accepted draft tokens then the final token
+    num_emitted: torch.Tensor  # [B]
+    final: torch.Tensor        # [B]
+    eos: torch.Tensor          # [B]
+    status: torch.Tensor       # [B] 1 when the uniform stream ran out
+    target_probs: Optional[torch.Tensor] = None
+    draft_probs: Optional[torch.Tensor] = None
+
+
+def tree_verify(target: torch.Tensor, draft: Optional[torch.Tensor], parents: torch.Tensor,
+                node_tokens: torch.Tensor, uniforms: Optional[torch.Tensor], *,
+                input_kind: str = "logits", temperature: float = 1.0, mode: str = "cpp",
+                eos_token_id: int = -1, return_probs: bool = False) -> TreeVerifyOutput:
+    """Accept the longest root-to-leaf path of a draft tree.
+
+    target / draft [B, N, V] fp32 (rows may be strided; the vocabulary
+    dimension contiguous); parents [N] or [B, N] int32 with parents[c] < c and
+    parents[0] = -1; node_tokens [B, N] int32; uniforms [B, n_u] fp32 (cpp mode).
+    """
+    if mode not in ("cpp", "greedy"):
+        raise ValueError("mode must be 'cpp' or 'greedy'")
+    if input_kind not in _KINDS:
+        raise ValueError(f"input_kind must be one of {sorted(_KINDS)}")
+    _require_cuda("target", target, torch.float32)
+    dev = target.device
+    if target.dim() != 3 or target.stride(2) != 1:
+        raise ValueError("target must be [B, N, V] with a contiguous last dimension")
+    B, N, V = target.shape
+    greedy = mode == "greedy"
+    if not greedy:
+        if draft is None or uniforms is None:
+            raise ValueError("draft and uniforms are required in cpp mode")
+        _require_cuda("draft", draft, torch.float32, dev)
+        if tuple(draft.shape) != (B, N, V) or draft.stride(2) != 1:
+            raise ValueError("draft must be [B, N, V] with a contiguous last dimension")
+        _require_cuda("uniforms", uniforms, torch.float32, dev)
+        if uniforms.dim() != 2 or uniforms.shape[0] != B:
+            raise ValueError("uniforms must be [B, n_uniforms]")
+        uniforms = uniforms.contiguous()
+    _require_cuda("parents", parents, torch.int32, dev)
+    if parents.dim() == 1 and parents.shape[0] == N:
+        pstride = 0
+    elif parents.dim() == 2 and tuple(parents.shape) == (B, N):
+        pstride = N
+    else:
+        raise ValueError("parents must be [N] or [B, N]")
+    parents = parents.contiguous()
+    _require_cuda("node_tokens", node_tokens, torch.int32, dev)
+    if tuple(node_tokens.shape) != (B, N):
+        raise ValueError("node_tokens must be [B, N]")
+    node_tokens = node_tokens.contiguous()
+    if input_kind == "logits" and not temperature > 0.0:
+        raise ValueError("temperature must be > 0")
+    i32 = dict(dtype=torch.int32, device=dev)
+    out = TreeVerifyOutput(path=torch.empty(B, N, **i32), path_len=torch.empty(B, **i32),
+                           tokens=torch.empty(B, N + 1, **i32), num_emitted=torch.empty(B, **i32),
+                           final=torch.empty(B, **i32), eos=torch.empty(B, **i32),
+                           status=torch.empty(B, **i32))
+    if return_probs:
+        out.target_probs = torch.zeros(B, N, V, dtype=torch.float32, device=dev)
+        if not greedy:
+            out.draft_probs = torch.zeros(B, N, V, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.load().cfa_tree_verify(
+            target.data_ptr(), target.stride(0), target.stride(1),
+            None if greedy else draft.data_ptr(), 0 if greedy else draft.stride(0),
+            0 if greedy else draft.stride(1), _KINDS[input_kind], parents.data_ptr(), pstride,
+            node_tokens.data_ptr(), None if greedy else uniforms.data_ptr(),
+            0 if greedy else uniforms.shape[1], B, N, V, ctypes.c_float(temperature),
+            _MODES[mode], int(eos_token_id), out.path.data_ptr(), out.path_len.data_ptr(),
+            out.tokens.data_ptr(), out.num_emitted.data_ptr(), out.final.data_ptr(),
+            out.eos.data_ptr(), out.status.data_ptr(), _ptr(out.target_probs),
+            _ptr(out.draft_probs), _stream_ptr(dev))
+    _lib.check(rc, "cfa_tree_verify")
     return out

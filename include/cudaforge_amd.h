@@ -131,6 +131,41 @@ int cfa_tree_attention(const void *q, const void *k_pool, const void *v_pool,
                        void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
+ * Tree verification: multi-candidate rejection sampling down a draft tree,
+ * longest accepted root-to-leaf path and the resample / bonus token.
+ *
+ * Generalises SpeculativeEngine::verify_candidates / _greedy
+ * (csrc/src/scheduler/speculative.cpp:50-150; pybind names at
+ * csrc/bindings/pybind_module.cpp:229-235) from a chain of K drafts to a tree
+ * of N <= 64 nodes (parents[c] < c, node 0 = root = the last verified token);
+ * on a one-child chain it is exactly verify_candidates.
+ *
+ *   target [B, N, V] fp32: row n = target distribution after node n
+ *   draft  [B, N, V] fp32: row n = distribution node n's children were drawn
+ *          from (unused in greedy mode); probabilities or logits (input_kind)
+ *   parents    [N] shared (stride 0) or [B, N] (stride N) int32
+ *   node_tokens [B, N] int32 (the root's entry is not read)
+ *   uniforms   [B, n_uniforms]: the stream the walk consumes, one draw per
+ *              acceptance test and one for the final draw (as the reference's
+ *              mt19937 stream, speculative.cpp:64, 72, 13-14)
+ *   mode       CFA_MODE_CPP or CFA_MODE_GREEDY
+ * Outputs (int32): path [B, N] accepted node ids from the root, -1 padded;
+ * path_len [B] (1 + accepted drafts); tokens [B, N+1] accepted draft tokens
+ * then the final token; num_emitted [B]; final [B]; eos [B]; status [B]
+ * (optional; 1 when the uniform stream ran out).  out_target_probs /
+ * out_draft_probs (optional, [B, N, V]) receive the probabilities of the rows
+ * the walk visited.
+ */
+int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t t_stride_n,
+                    const float *draft, int64_t d_stride_b, int64_t d_stride_n, int input_kind,
+                    const int32_t *parents, int64_t parents_stride_b, const int32_t *node_tokens,
+                    const float *uniforms, int n_uniforms, int B, int N, int V,
+                    float temperature, int mode, int32_t eos_token_id, int32_t *out_path,
+                    int32_t *out_path_len, int32_t *out_tokens, int32_t *out_num_emitted,
+                    int32_t *out_final, int32_t *out_eos, int32_t *out_status,
+                    float *out_target_probs, float *out_draft_probs, void *stream);
+
+/* ---------------------------------------------------------------------------
  * KV commit / compaction of an accepted draft-tree path.
  *
  * Device half of the reference's append_tokens(seq, L)
