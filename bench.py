@@ -28,11 +28,15 @@ sys.path.insert(0, ROOT)
 
 METRIC = "verified tok/s (B=64,K=8,V=128k) + tree-attn/sampling HBM GB/s as % of peak"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK = 2.5e15  # dense bf16 FLOP/s
 B, K, V, T = 64, 8, 128256, 0.7
 SIGMA, NOISE = 2.0, 0.5
 NSETS = 4
 # algorithmic bytes of one step: target [B,K+1,V] + draft [B,K,V] logits, read once
 ALG_BYTES = B * (2 * K + 1) * V * 4
+# HBM bytes per chain_stats launch measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE, scaled by a plain-copy calibration (profiles/hbm_traffic_per_dispatch.md)
+STATS_TRAFFIC_BYTES = 562_217_848
 
 
 def make_inputs(dev, seed):
@@ -67,11 +71,129 @@ def cpu_baseline(tl, dl, tok, U, budget_s=12.0):
         emitted += int(out["num_emitted"].sum())
         passes += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or passes >= 50:
+        if el >= budget_s:
             break
     return {"value": emitted / el, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{passes} full passes over one B=64,K=8,V=128256 batch "
                       f"(oracle softmax + per-row verify, {el:.1f} s)"}
+
+
+def _time_launches(fn, reps, names):
+    """Run fn() reps times with per-kernel HIP events; returns avg ms per call
+    per kernel name (launches inside one call are summed)."""
+    import torch
+    from cudaforge_amd import _lib
+
+    torch.cuda.synchronize()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    out = {n: _lib.profile_query(n)[1] / reps for n in names}
+    _lib.profile_reset()
+    return out
+
+
+def tree_attention_leg(dev, reps=20):
+    """B=16, 63-node binary tree, 32 q / 8 KV heads,
+    head_dim 128, context 4096, page 16, random page table, bf16 N(0,1)."""
+    import torch
+    from cudaforge_amd import tree as Tr
+    from cudaforge_amd.verify import tree_attention, tree_attention_workspace_bytes
+
+    Bt, N, Hq, Hkv, D, bs, C = 16, 63, 32, 8, 128, 16, 4096
+    nps = (C + N + bs - 1) // bs
+    nblk = Bt * nps + 8
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    kp = torch.randn(nblk, 1, Hkv, bs, D, device=dev, generator=g).bfloat16()
+    vp = torch.randn(nblk, 1, Hkv, bs, D, device=dev, generator=g).bfloat16()
+    bt = torch.randperm(nblk, device=dev, generator=g)[: Bt * nps].int().reshape(Bt, nps)
+    q = torch.randn(Bt, N, Hq, D, device=dev, generator=g).bfloat16()
+    ctx = torch.full((Bt,), C, dtype=torch.int32, device=dev)
+    masks = Tr.ancestor_masks(Tr.binary_tree_parents(N))
+    mt = Tr.mask_tensor(masks, dev)
+    anc = int(sum(bin(int(x)).count("1") for x in masks))
+    flops = 4 * Bt * Hq * D * (N * C + anc)
+    nbytes = (Bt * Hkv * (C + N) * D * 2 * 2      # K and V rows read once
+              + 2 * q.numel() * 2 + bt.numel() * 4)  # q in, out, page table
+    out = torch.empty_like(q)
+    ws = torch.empty(tree_attention_workspace_bytes(Bt, N, Hq, Hkv, D, C + N), dtype=torch.uint8,
+                     device=dev)
+
+    def run():
+        tree_attention(q, kp, vp, bt, ctx, mt, max_keys=C + N, out=out, workspace=ws)
+
+    for _ in range(3):
+        run()
+    ms = _time_launches(run, reps, ("tree_attn", "tree_attn_merge"))
+    t = (ms["tree_attn"] + ms["tree_attn_merge"]) * 1e-3
+    return {"config": "B=16,N=63 binary tree,Hq=32,Hkv=8,d=128,ctx=4096,page=16 (BASELINE configs[2])",
+            "us": round(t * 1e6, 2), "kernels_us": {k: round(v * 1e3, 2) for k, v in ms.items()},
+            "flop": flops, "tflops": round(flops / t / 1e12, 1),
+            "mfma_frac": round(flops / t / MFMA_BF16_PEAK, 4),
+            "bytes": nbytes, "gbs": round(nbytes / t / 1e9, 1),
+            "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def tree_accept_commit_leg(dev, reps=10):
+    """B=32, 63-node binary tree, V=128256, fp32
+    target/draft logits per node (as configs[1]), node tokens drawn from the
+    parent's draft softmax, T=0.7, seeded uniforms; then the KV commit of the
+    accepted paths (32 layers x 8 KV heads x 128, bf16, page 16, ctx 1024)."""
+    import torch
+    from cudaforge_amd import tree as Tr
+    from cudaforge_amd.verify import kv_commit, tree_verify
+
+    Bt, N, Vt, L, Hkv, D, bs, C = 32, 63, 128256, 32, 8, 128, 16, 1024
+    parents = Tr.binary_tree_parents(N)
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    tl = torch.randn(Bt, N, Vt, device=dev, generator=g) * SIGMA
+    dl = tl + NOISE * torch.randn(Bt, N, Vt, device=dev, generator=g)
+    par = torch.from_numpy(parents).to(dev)
+    probs = torch.softmax(dl[:, par[1:].long()] / T, dim=-1).reshape(-1, Vt)
+    tok = torch.zeros(Bt, N, dtype=torch.int32, device=dev)
+    tok[:, 1:] = torch.multinomial(probs, 1, generator=g).reshape(Bt, N - 1).int()
+    del probs
+    U = torch.rand(Bt, N + 1, device=dev, generator=g)
+    nps = (C + N + bs - 1) // bs
+    nblk = Bt * nps
+    kp = torch.randn(nblk, L, Hkv, bs, D, device=dev, generator=g).bfloat16()
+    vp = torch.randn(nblk, L, Hkv, bs, D, device=dev, generator=g).bfloat16()
+    bt = torch.randperm(nblk, device=dev, generator=g).int().reshape(Bt, nps)
+    ctx = torch.full((Bt,), C, dtype=torch.int32, device=dev)
+
+    res = {}
+
+    def run():
+        res["tv"] = tree_verify(tl, dl, par, tok, U, input_kind="logits", temperature=T,
+                                mode="cpp")
+        res["kc"] = kv_commit(kp, vp, bt, ctx, res["tv"].path, res["tv"].path_len)
+
+    for _ in range(2):
+        run()
+    torch.cuda.synchronize()
+    plen = res["tv"].path_len.cpu().numpy()
+    path = res["tv"].path.cpu().numpy()
+    emitted = int(res["tv"].num_emitted.sum())
+    visited_nodes = int(plen.sum())  # target rows of path nodes; draft rows of non-leaf ones
+    alg_accept = (visited_nodes * 2) * Vt * 4
+    moved = int(sum(sum(1 for j in range(int(plen[b])) if path[b, j] != j) for b in range(Bt)))
+    alg_commit = moved * 2 * (L * Hkv * D * 2 * 2)  # read + write of K and V rows
+    ms = _time_launches(run, reps, ("tree_verify", "kv_commit"))
+    t_acc, t_com = ms["tree_verify"] * 1e-3, ms["kv_commit"] * 1e-3
+    return {"config": "B=32,63-node binary tree,V=128256,T=0.7; commit 32L x 8H x 128 bf16 "
+                      "(BASELINE configs[3])",
+            "accept_us": round(t_acc * 1e6, 1), "commit_us": round(t_com * 1e6, 2),
+            "mean_path_len": round(float(plen.mean()), 3),
+            "accepted_tok_s": round(emitted / (t_acc + t_com), 1),
+            "accept_alg_bytes": alg_accept,
+            "accept_gbs": round(alg_accept / t_acc / 1e9, 1),
+            "commit_moved_tokens": moved, "commit_alg_bytes": alg_commit,
+            "commit_gbs": round(alg_commit / t_com / 1e9, 1) if moved else None}
 
 
 def main() -> int:
@@ -80,6 +202,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-tree", action="store_true", help="skip the tree attention / accept legs")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy (reference for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (no multi-GPU path); "
@@ -93,6 +218,14 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": src.numel() * 4, "copies": 3}), flush=True)
+        return 0
     _lib.load()
     sets = [make_inputs(dev, 1000 + s) for s in range(NSETS)]
     ws = torch.empty(chain_workspace_bytes(B, K, V, "logits", "cpp"), dtype=torch.uint8,
@@ -163,13 +296,21 @@ def main() -> int:
                    "mean_accept_len": round(sum(emitted) / (NSETS * B) - 1, 3)},
         "roofline": {"bound": "hbm", "kernel": "chain_stats",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": STATS_TRAFFIC_BYTES},
         "kernels_ms_per_step": {k: round(v, 5) for k, v in kern.items()},
         "step_hbm_gbs": round(ALG_BYTES / (ms_per_step * 1e-3) / 1e9, 1),
         "wall_s": round(wall, 4),
     }
+    if not args.no_tree:
+        del sets
+        torch.cuda.empty_cache()
+        line["tree_attention"] = tree_attention_leg(dev)
+        torch.cuda.empty_cache()
+        line["tree_accept_commit"] = tree_accept_commit_leg(dev)
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
-        tl, dl, tok, U = sets[0]
+        tl, dl, tok, U = make_inputs(dev, 1000)
         line["cpu_baseline"] = cpu_baseline(tl, dl, tok, U)
     print(json.dumps(line), flush=True)
     return 0

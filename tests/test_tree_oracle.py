@@ -111,3 +111,60 @@ def test_kv_commit_oracle_vs_index_copy():
             want = before.clone().index_copy(0, torch.arange(ctx[b], ctx[b] + lens[b]),
                                              before[src])
             assert torch.equal(after, want)
+
+
+# --- tree acceptance oracle (orc_tree_verify) -------------------------------
+
+
+def test_tree_walk_on_chain_equals_chain_verify():
+    """On a one-child chain the tree walk is verify_candidates
+    (speculative.cpp:50-103): same accept count, final token and EOS."""
+    from tests.golden.recipes import chain_case
+
+    for seed in range(6):
+        K, V = 5, 300
+        tok, d, t, eos = chain_case(500 + seed, 4, K, V, eos_bias=(seed % 2 == 0))
+        U = np.random.default_rng(seed).random((4, K + 1)).astype(np.float32)
+        want = O.chain_verify(t, d, tok, U, eos=eos)
+        parents = T.chain_parents(K + 1)
+        for c in range(4):
+            ntok = np.concatenate([[0], tok[c]]).astype(np.int32)
+            dd = np.concatenate([d[c], np.zeros((1, V), np.float32)])
+            w = O.tree_verify(parents, ntok, t[c], dd, U[c], eos=eos)
+            assert len(w["path"]) - 1 == want["accept_len"][c]
+            assert w["final"] == want["final"][c] and int(w["eos"]) == want["eos"][c]
+
+
+def test_tree_walk_preserves_target_distribution():
+    """Multi-candidate rejection sampling emits its first token with exactly
+    the target distribution p_root when the candidates are drawn from the
+    draft distribution q (SpecInfer, Miao et al. 2023): chi-square test on a
+    3-candidate star over V = 5."""
+    rng = np.random.default_rng(123)
+    V, n = 5, 40000
+    p = np.array([0.05, 0.4, 0.1, 0.25, 0.2], np.float32)
+    q = np.array([0.3, 0.1, 0.3, 0.2, 0.1], np.float32)
+    parents = np.array([-1, 0, 0, 0], np.int32)
+    tp = np.stack([p, p, p, p])           # rows of the leaves are never sampled here
+    dp = np.stack([q, q, q, q])
+    counts = np.zeros(V)
+    cq = np.cumsum(q.astype(np.float64))
+    for _ in range(n):
+        toks = [0] + [int(np.searchsorted(cq, rng.random() * cq[-1])) for _ in range(3)]
+        U = rng.random(8).astype(np.float32)
+        w = O.tree_verify(parents, np.array(toks, np.int32), tp, dp, U)
+        first = toks[w["path"][1]] if len(w["path"]) > 1 else w["final"]
+        counts[first] += 1
+    expected = n * p.astype(np.float64)
+    chi2 = float(((counts - expected) ** 2 / expected).sum())
+    assert chi2 < 18.47, (chi2, counts / n)  # chi-square(4) 99.9% quantile
+
+
+def test_tree_walk_greedy_known_answer():
+    # root's argmax is token 2; children carry tokens 1 and 2 -> node 2 accepted;
+    # node 2 is a leaf whose argmax (token 3) is the bonus
+    parents = np.array([-1, 0, 0], np.int32)
+    tp = np.array([[0.1, 0.2, 0.6, 0.1], [0.25] * 4, [0.1, 0.1, 0.1, 0.7]], np.float32)
+    w = O.tree_verify(parents, np.array([0, 1, 2], np.int32), tp, tp, np.zeros(1, np.float32),
+                      greedy=True)
+    assert list(w["path"]) == [0, 2] and w["final"] == 3
