@@ -213,6 +213,18 @@ __device__ __forceinline__ Inc wave_incl_compose(Inc v) {
   return v;
 }
 
+// Inclusive integer prefix sum across the wave (same DPP pattern); the
+// inputs here are at most 2^25 each, so 64 of them cannot overflow.
+__device__ __forceinline__ uint32_t wave_incl_add_u32(uint32_t v) {
+  v += dpp_u32<kDppRowShr | 1, 0xf>(v);
+  v += dpp_u32<kDppRowShr | 2, 0xf>(v);
+  v += dpp_u32<kDppRowShr | 4, 0xf>(v);
+  v += dpp_u32<kDppRowShr | 8, 0xf>(v);
+  v += dpp_u32<kDppRowBcast15, 0xa>(v);
+  v += dpp_u32<kDppRowBcast31, 0xc>(v);
+  return v;
+}
+
 template <int CTRL, int ROWMASK>
 __device__ __forceinline__ float dpp_f32(float v) {
   return __uint_as_float(dpp_u32<CTRL, ROWMASK>(__float_as_uint(v)));
@@ -288,8 +300,13 @@ __device__ long long walk(int count, float &s, bool cdf, float r, const Item &it
       vin = (v.e != kBad) && (reg == rs || reg == kAnyRegion);
       if (vin) f = v;
     }
-    const Inc incl = wave_incl_compose(f);
-    const uint32_t inc = inc_at(incl, a);
+    // Without a tie-dependent item the functions are plain integers: an add
+    // scan (6 DPP adds) replaces the composition scan.
+    uint32_t inc;
+    if (__ballot(f.e != f.o) == 0ull)
+      inc = wave_incl_add_u32(f.e);
+    else
+      inc = inc_at(wave_incl_compose(f), a);
     const bool ok = vin && (a + inc <= kUnitsTop);
     const int nvalid = trailing_ones(__ballot(ok));
     if (cdf) {
