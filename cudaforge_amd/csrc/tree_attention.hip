@@ -11,19 +11,32 @@
 // been appended at positions ctx_b .. ctx_b + N - 1.
 //
 // One work-group = (split, kv head, sequence); its 8 waves hold all G*N query
-// rows (two 16-row tiles each) and share one LDS-staged 64-key K/V tile per
-// step (double-buffered, register-prefetched).  Everything is computed in the
-// transposed form
+// rows (two 16-row tiles each, Q^T in registers) and share a ring of
+// kStages LDS stages, each holding one 64-key K tile and one 64-key V tile.
+// Tiles move HBM -> LDS with direct 16-byte global_load_lds transfers (no
+// register staging), kStages - 1 tiles ahead of the tile being computed.
+// Everything is computed in the transposed form
 //   S^T = K Q^T            (MFMA A = K rows, B = Q^T columns)
 //   O^T += V^T P^T         (MFMA A = V^T rows, B = P^T columns)
-// so that each lane owns one query column throughout: the softmax of a column
-// and the rescale of its O^T column stay in registers, and the P^T operand of
-// the second product is the first product's output, converted to bf16 in
-// place.  Within a 32-key block the two 16-key MFMA tiles take keys
-// {8g+i} and {8g+4+i} (g = lane / 16, i < 4) so that lane (g, q) ends up with
-// keys 8g..8g+7 of column q, which is exactly its 8-element k-slice of P^T.
-// V is staged transposed in LDS so that the matching V^T k-slice is one
-// 16-byte read.  Splits of the key range are merged by a log-sum-exp pass.
+// so each lane owns one query column throughout: the softmax of a column and
+// the rescale of its O^T column stay in registers, and the P^T operand of the
+// second product is the first product's output converted to bf16 in place.
+// Within a 32-key block the two 16-key MFMA tiles take keys {8g+i} and
+// {8g+4+i} (g = lane / 16, i < 4), so lane (g, q) ends up with keys 8g..8g+7
+// of column q: exactly its 8-element k-slice of P^T.  The matching V^T
+// k-slice comes from two ds_read_b64_tr_b16 transposed reads of the V tile,
+// which stays in its natural [key][d] layout.
+//
+// LDS layouts (256-byte rows, 16-byte chunks XOR-swizzled so that the MFMA
+// operand reads of one wave hit distinct banks):
+//   K: row R holds key 32*(R/32) + 8*((R/4)%4) + 4*((R/16)%2) + R%4 (each
+//      16-row MFMA tile reads consecutive rows); chunk c sits at c ^ (R % 16).
+//   V: row = key; chunk c sits at c ^ 2*((key % 4) | 4*((key / 8) % 2)).
+//
+// Softmax rescaling is lazy: a column's exponent base only moves when its
+// running maximum grows by more than kRescaleSlack (log2 units), so P^T
+// entries stay below 2^kRescaleSlack and the O^T rescale is rare.  Splits of
+// the key range are merged by a log-sum-exp pass.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -31,20 +44,29 @@
 
 #include "abi_internal.hpp"
 
+#define CFA_LDS __attribute__((address_space(3)))
+
 namespace cfa {
 namespace tree {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kD = 128;           // head_dim
-constexpr int kKT = 64;           // keys per LDS tile
+constexpr int kD = 128;                       // head_dim
+constexpr int kKT = 64;                       // keys per tile
 constexpr int kWaves = 8;
-constexpr int kNT = kWaves * 64;  // threads per work-group
-constexpr int kQT = 2;            // 16-row query tiles per wave
-constexpr int kMaxRows = kWaves * kQT * 16;  // 256 query rows per work-group
-constexpr int kKPad = kD + 8;     // K row stride in LDS (bf16), breaks bank aliasing
-constexpr int kVPad = kKT + 8;    // V^T row stride in LDS (bf16)
+constexpr int kNT = kWaves * 64;              // threads per work-group
+constexpr int kQT = 2;                        // 16-row query tiles per wave
+constexpr int kMaxRows = kWaves * kQT * 16;   // 256 query rows per work-group
+constexpr int kRowBytes = kD * 2;             // one K or V row, bf16
+constexpr int kTileBytes = kKT * kRowBytes;   // 16 KiB
+constexpr int kStages = 3;                    // LDS ring depth (tiles)
+constexpr int kStageBytes = 2 * kTileBytes;   // K tile then V tile
+constexpr int kLoadsPerTile = 4;              // global_load_lds per wave per tile
+constexpr float kRescaleSlack = 8.0f;         // log2 units
+constexpr int kMaxGroups = 1024;              // 16-key groups per split (page lookup table)
+constexpr int kMaxTilesPerSplit = kMaxGroups / (kKT / 16);
 
 struct Args {
   const uint16_t *q;       // [B, N, Hq, D]
@@ -56,125 +78,133 @@ struct Args {
   long long mask_sb;
   uint16_t *out;           // [B, N, Hq, D]
   float *part_o;           // [S, B, Hkv, rows, D] unnormalised partial outputs
-  float2 *part_ml;         // [S, B, Hkv, rows] (running max in log2 units, sum)
+  float2 *part_ml;         // [S, B, Hkv, rows] (exponent base in log2 units, sum)
   int B, N, Hq, Hkv, G, rows;
   int max_blocks, num_blocks, num_layers, layer, bs;
   int splits, tiles_per_split;
   float scale_log2;        // sm_scale * log2(e)
 };
 
-struct __align__(16) Smem {
-  uint16_t k[2][kKT * kKPad];
-  uint16_t vt[2][kD * kVPad];
-};
-
-__device__ __forceinline__ bf16x8 ld_bf16x8(const uint16_t *p) {
-  const uint4 v = *reinterpret_cast<const uint4 *>(p);
-  return __builtin_bit_cast(bf16x8, v);
-}
-
 __device__ __forceinline__ uint4 ld_g16(const uint16_t *p) {
   return *reinterpret_cast<const uint4 *>(p);
 }
 
-// LDS row of key k within a tile: the two 16-key MFMA tiles of a 32-key
-// block read keys {8g+i} and {8g+4+i}; storing key 8g + 4T + i at row
-// 16T + 4g + i makes each MFMA tile read 16 consecutive rows, which a 272-byte
-// row stride spreads over all 64 banks.
-__device__ __forceinline__ int k_row(int key) {
-  return (key & ~31) + ((key >> 2) & 1) * 16 + ((key >> 3) & 3) * 4 + (key & 3);
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, expcnt 6:4, lgkmcnt 11:8, vmcnt[5:4] in 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
 }
 
-// Global staging of one 64-key tile.  K: thread t owns the 16-byte chunks
-// (key t/16, slice t%16) and (key t/16 + 32, same slice).  V: lane l of wave
-// w owns keys 2(l%32), 2(l%32)+1 at d-slice 2w + l/32, so that the transposed
-// 4-byte LDS writes of one wave hit 64 distinct banks.
-struct Stage {
-  uint4 k0, k1;
-  uint4 v0, v1;
-};
-
-// Element offsets (within a pool) of the tile's pages, read with uniform
-// addresses: page j of the tile covers keys [j*bs, (j+1)*bs), j < kKT / bs.
-struct Pages {
-  long long o0, o1, o2, o3;
-};
-
-__device__ __forceinline__ long long page_off(const Args &a, const int32_t *btb, int page, int h) {
-  page = min(page, a.max_blocks - 1);
-  int blk = btb[page];
-  blk = min(max(blk, 0), a.num_blocks - 1);  // stay inside the pool whatever the table holds
-  return (((long long)blk * a.num_layers + a.layer) * a.Hkv + h) * (long long)(a.bs * kD);
+// One 16-byte-per-lane transfer HBM -> LDS: lane i's 16 bytes at `src` land at
+// LDS byte address lds + 16 i.  Written as inline assembly so the compiler
+// neither tracks it (its alias analysis would otherwise wait for every
+// transfer before each LDS read) nor reorders it; completion is awaited with
+// wait_vmcnt and published to the other waves with block_barrier.  M0 is a
+// reserved register that the compiler sets right before each of its own uses,
+// so overwriting it here disturbs nothing.
+__device__ __forceinline__ void dma16(const void *src, CFA_LDS void *lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory");
 }
 
-__device__ __forceinline__ Pages tile_pages(const Args &a, int b, int h, int kbase) {
-  const int32_t *btb = a.bt + (long long)b * a.max_blocks;
-  const int p0 = kbase / a.bs, last = kKT / a.bs - 1;
-  Pages pg;
-  pg.o0 = page_off(a, btb, p0, h);
-  pg.o1 = page_off(a, btb, p0 + min(1, last), h);
-  pg.o2 = page_off(a, btb, p0 + min(2, last), h);
-  pg.o3 = page_off(a, btb, p0 + min(3, last), h);
-  return pg;
+// Work-group barrier without the release/acquire fences of __syncthreads
+// (those would wait for every outstanding transfer); the empty asm statements
+// keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
-// Offset of the row of tile-relative key `key`.
-__device__ __forceinline__ long long key_off(const Pages &pg, int bs, int key) {
-  const int j = key / bs;
-  long long o = pg.o0;
-  o = (j == 1) ? pg.o1 : o;
-  o = (j == 2) ? pg.o2 : o;
-  o = (j == 3) ? pg.o3 : o;
-  return o + (long long)((key % bs) * kD);
+// Key (tile-relative) held by K-tile LDS row R.
+__device__ __forceinline__ int k_key_of_row(int R) {
+  return (R & ~31) + ((R >> 2) & 3) * 8 + ((R >> 4) & 1) * 4 + (R & 3);
 }
 
-__device__ __forceinline__ void stage_load(const Args &a, int b, int h, int kbase, int nkeys,
-                                           Stage &st) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint4 z = make_uint4(0, 0, 0, 0);
-  const Pages pg = tile_pages(a, b, h, kbase);
+// Swizzle of V-tile row `key`: 2 * ((key % 4) | 4 * ((key / 8) % 2)).
+__device__ __forceinline__ int v_swz(int key) { return ((key & 3) | ((key >> 1) & 4)) << 1; }
+
+// Pool element offset of the row holding position gstart = min(16 gi,
+// nkeys - 1), the first row 16-key group gi reads.  Page index and block id
+// are clamped into the table and the pool, so a corrupt table can never send
+// a load outside the pool.
+__device__ __forceinline__ long long group_row_offset(const Args &a, const int32_t *btb, int gi,
+                                                      int nkeys, int h) {
+  const int gstart = min(gi * 16, nkeys - 1);
+  const int page = min(gstart / a.bs, a.max_blocks - 1);
+  const int blk = min(max(btb[page], 0), a.num_blocks - 1);
+  return (((long long)blk * a.num_layers + a.layer) * a.Hkv + h) * (long long)(a.bs * kD) +
+         (long long)(gstart - page * a.bs) * kD;
+}
+
+__device__ __forceinline__ long long uniform_i64(long long v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((unsigned long long)v >> 32));
+  return (long long)(((unsigned long long)hi << 32) | lo);
+}
+
+// Issue this wave's share of the tile at key kbase: two 1 KiB K transfers
+// (LDS rows 8w..8w+7) and two 1 KiB V transfers (keys 8w..8w+7).  Each
+// transfer covers four keys of one 16-key group, and a group never straddles
+// a page (block_size % 16 == 0).  Keys at or past nkeys re-read key
+// nkeys - 1: a finite, in-bounds row that the mask then hides.  gtab holds
+// the split's group row offsets (group_row_offset) from group g0 on.
+__device__ __forceinline__ void issue_tile(const Args &a, const long long *gtab, int g0, int kbase,
+                                           int nkeys, uint8_t *stage, int wave, int lane) {
+  const int sub = lane >> 4, pc = lane & 15;
   {
-    const int key = tid >> 4, ds = tid & 15;
-    st.k0 = (kbase + key < nkeys) ? ld_g16(a.kpool + key_off(pg, a.bs, key) + ds * 8) : z;
-    st.k1 = (kbase + key + 32 < nkeys) ? ld_g16(a.kpool + key_off(pg, a.bs, key + 32) + ds * 8) : z;
-  }
-  {
-    const int kp = lane & 31, ds = wave * 2 + (lane >> 5);
-    const int key = 2 * kp;
-    st.v0 = (kbase + key < nkeys) ? ld_g16(a.vpool + key_off(pg, a.bs, key) + ds * 8) : z;
-    st.v1 = (kbase + key + 1 < nkeys) ? ld_g16(a.vpool + key_off(pg, a.bs, key + 1) + ds * 8) : z;
-  }
-}
-
-__device__ __forceinline__ void stage_store(Smem &sm, int buf, const Stage &st) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  {
-    const int key = tid >> 4, ds = tid & 15;
-    *reinterpret_cast<uint4 *>(&sm.k[buf][k_row(key) * kKPad + ds * 8]) = st.k0;
-    *reinterpret_cast<uint4 *>(&sm.k[buf][k_row(key + 32) * kKPad + ds * 8]) = st.k1;
-  }
-  {
-    const int kp = lane & 31, ds = wave * 2 + (lane >> 5);
-    const uint32_t a[4] = {st.v0.x, st.v0.y, st.v0.z, st.v0.w};
-    const uint32_t c[4] = {st.v1.x, st.v1.y, st.v1.z, st.v1.w};
+    // K: the wave's rows hold keys of the tile's 16-group 2 (w / 4) + (w % 2)
+    const int gi = kbase / 16 + 2 * (wave >> 2) + (wave & 1);
+    const int gstart = min(gi * 16, nkeys - 1);
+    const uint16_t *base = a.kpool + uniform_i64(gtab[gi - g0]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // d = ds*8 + 2j (low halves) and + 1 (high halves); keys 2kp, 2kp+1
-      const uint32_t lo = (a[j] & 0xffffu) | (c[j] << 16);
-      const uint32_t hi = (a[j] >> 16) | (c[j] & 0xffff0000u);
-      *reinterpret_cast<uint32_t *>(&sm.vt[buf][(ds * 8 + 2 * j) * kVPad + 2 * kp]) = lo;
-      *reinterpret_cast<uint32_t *>(&sm.vt[buf][(ds * 8 + 2 * j + 1) * kVPad + 2 * kp]) = hi;
+    for (int j = 0; j < 2; ++j) {
+      const int R = 8 * wave + 4 * j + sub;
+      const int c = pc ^ (R & 15);
+      const int pos = min(kbase + k_key_of_row(R), nkeys - 1);
+      dma16(base + ((pos - gstart) * kD + c * 8),
+            (CFA_LDS void *)(stage + (8 * wave + 4 * j) * kRowBytes));
     }
   }
+  {
+    // V: keys 8w..8w+7, in the tile's 16-group w / 2
+    const int gi = kbase / 16 + (wave >> 1);
+    const int gstart = min(gi * 16, nkeys - 1);
+    const uint16_t *base = a.vpool + uniform_i64(gtab[gi - g0]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int key = 8 * wave + 4 * j + sub;
+      const int c = pc ^ v_swz(key);
+      const int pos = min(kbase + key, nkeys - 1);
+      dma16(base + ((pos - gstart) * kD + c * 8),
+            (CFA_LDS void *)(stage + kTileBytes + (8 * wave + 4 * j) * kRowBytes));
+    }
+  }
+}
+
+// Visibility of the 64 keys kbase.. of a tile to a query whose ancestor mask
+// (bits < N) is anc: context positions (< ctx) are all visible, tree position
+// ctx + j is visible iff bit j of anc is set, positions past the tree never.
+__device__ __forceinline__ uint64_t tile_visibility(int kbase, int ctx, uint64_t anc) {
+  const int nctx = ctx - kbase;  // context keys at the start of the tile
+  const uint64_t ctx_bits = nctx >= 64 ? ~0ull : (nctx <= 0 ? 0ull : ((1ull << nctx) - 1));
+  // tile key k is tree node k - nctx
+  const uint64_t tree_bits = nctx >= 0 ? (nctx >= 64 ? 0ull : anc << nctx)
+                                       : (-nctx >= 64 ? 0ull : anc >> -nctx);
+  return ctx_bits | tree_bits;
 }
 
 __device__ __forceinline__ float xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m, 64)); }
 __device__ __forceinline__ float xor_sum(float v, int m) { return v + __shfl_xor(v, m, 64); }
 
 __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
-  __shared__ Smem sm;
+  __shared__ __align__(16) uint8_t smem[kStages * kStageBytes];
+  __shared__ long long gtab[kMaxGroups];
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int col = lane & 15, g = lane >> 4;
   // positions past the block table are never read (ctx_lens beyond the
   // table's capacity are clamped rather than trusted)
@@ -184,8 +214,10 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
   const int ntiles = (nkeys + kKT - 1) / kKT;
   const int t0 = split * a.tiles_per_split;
   const int t1 = min(ntiles, t0 + a.tiles_per_split);
+  const int g0 = t0 * (kKT / 16);
 
   // query rows of this wave: r = node * G + head-in-group
+  const uint64_t node_bits = a.N >= 64 ? ~0ull : ((1ull << a.N) - 1);
   bf16x8 qf[kQT][4];
   uint64_t anc[kQT];
   bool qvalid[kQT];
@@ -194,7 +226,7 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
     const int r = (wave * kQT + qt) * 16 + col;
     qvalid[qt] = r < a.rows;
     const int node = qvalid[qt] ? r / a.G : 0, hg = r % a.G;
-    anc[qt] = qvalid[qt] ? a.mask[(long long)b * a.mask_sb + node] : 0ull;
+    anc[qt] = qvalid[qt] ? a.mask[(long long)b * a.mask_sb + node] & node_bits : 0ull;
     const uint16_t *qp = a.q + (((long long)b * a.N + node) * a.Hq + (long long)h * a.G + hg) * kD;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
@@ -202,6 +234,23 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
       qf[qt][kk] = __builtin_bit_cast(bf16x8, v);
     }
   }
+
+  // the split's page lookups, once
+  {
+    const int32_t *btb = a.bt + (long long)b * a.max_blocks;
+    const int ng = (t1 - t0) * (kKT / 16);
+    for (int i = tid; i < ng; i += kNT) gtab[i] = group_row_offset(a, btb, g0 + i, nkeys, h);
+  }
+  // Q and the table are in; settling every load here also tells the compiler
+  // that nothing it issued is outstanding inside the loop below
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  // prologue: the first kStages - 1 tiles go in flight
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s)
+    if (t0 + s < t1)
+      issue_tile(a, gtab, g0, (t0 + s) * kKT, nkeys, smem + s * kStageBytes, wave, lane);
 
   f32x4 o[kQT][kD / 16];
   float m[kQT], l[kQT];
@@ -213,15 +262,28 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
     for (int dt = 0; dt < kD / 16; ++dt) o[qt][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  Stage st;
-  if (t0 < t1) stage_load(a, b, h, t0 * kKT, nkeys, st);
+  // per-lane LDS byte offsets, tile-relative
+  int koff[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) koff[kk] = col * kRowBytes + (((kk * 4 + g) ^ col) << 4);
+  const int vrow = 8 * g + (col >> 2);
+  const int vh = v_swz(vrow) >> 1;
+  const int vbase = vrow * kRowBytes + ((col >> 1) & 1) * 16 + (col & 1) * 8;
+
+  const float c = a.scale_log2;
   for (int t = t0; t < t1; ++t) {
-    const int buf = (t - t0) & 1;
-    stage_store(sm, buf, st);
-    __syncthreads();
-    if (t + 1 < t1) stage_load(a, b, h, (t + 1) * kKT, nkeys, st);
-    const uint16_t *K = sm.k[buf];
-    const uint16_t *Vt = sm.vt[buf];
+    // this wave's transfers of tile t have landed once at most the later
+    // tiles' transfers are outstanding; the barrier then publishes every
+    // wave's transfers and retires the stage read during tile t - 1
+    const int later = min(kStages - 2, t1 - 1 - t);
+    if (later >= 1) wait_vmcnt<kLoadsPerTile * (kStages - 2)>();
+    else wait_vmcnt<0>();
+    block_barrier();
+    if (t + kStages - 1 < t1)
+      issue_tile(a, gtab, g0, (t + kStages - 1) * kKT, nkeys,
+                 smem + ((t - t0 + kStages - 1) % kStages) * kStageBytes, wave, lane);
+    const uint8_t *Ks = smem + ((t - t0) % kStages) * kStageBytes;
+    const uint8_t *Vs = Ks + kTileBytes;
     const int kbase = t * kKT;
 
     // S^T for the tile: s[qt][blk][T] holds keys blk*32 + T*4 + 8g + i
@@ -232,20 +294,34 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
       for (int T = 0; T < 2; ++T) {
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) s[qt][blk][T] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        const int krow = blk * 32 + T * 16 + col;  // = k_row(blk*32 + T*4 + 8*(col/4) + col%4)
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const bf16x8 kf = ld_bf16x8(K + krow * kKPad + kk * 32 + g * 8);
+          const uint4 kv =
+              *reinterpret_cast<const uint4 *>(Ks + (blk * 32 + T * 16) * kRowBytes + koff[kk]);
+          const bf16x8 kf = __builtin_bit_cast(bf16x8, kv);
 #pragma unroll
           for (int qt = 0; qt < kQT; ++qt)
             s[qt][blk][T] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[qt][kk], s[qt][blk][T], 0, 0, 0);
         }
       }
 
-    // mask, online softmax in log2 units (per query column; the 4 lanes g of
-    // a column share it)
-    const bool masked_tile = kbase + kKT > ctx;
-    const float c = a.scale_log2;
+    // mask (tiles reaching the tree only), then online softmax in log2 units
+    // (per query column; the 4 lanes g of a column share it)
+    if (kbase + kKT > ctx) {
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+        // bit k: tile key k is visible to this column; this lane's keys are
+        // blk*32 + 8g + 4T + i, i.e. bit blk*32 + 4T + i of vis >> 8g
+        const uint64_t vis = tile_visibility(kbase, ctx, anc[qt]) >> (8 * g);
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              s[qt][blk][T][i] = ((vis >> (blk * 32 + 4 * T + i)) & 1ull) ? s[qt][blk][T][i] : -INFINITY;
+      }
+    }
     bf16x8 p[kQT][2];
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
@@ -255,23 +331,19 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
 #pragma unroll
         for (int T = 0; T < 2; ++T)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float v = s[qt][blk][T][i];
-            if (masked_tile) {
-              const int pos = kbase + blk * 32 + T * 4 + 8 * g + i;
-              const int j = pos - ctx;
-              const bool vis = pos < ctx || (j < a.N && ((anc[qt] >> (j & 63)) & 1ull));
-              v = vis ? v : -INFINITY;
-            }
-            s[qt][blk][T][i] = v;
-            tmax = fmaxf(tmax, v);
-          }
+          for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[qt][blk][T][i]);
       tmax = xor_max(tmax, 16);
       tmax = xor_max(tmax, 32);
-      const float mnew = fmaxf(m[qt], tmax * c);  // c > 0: max of scaled = scaled max
-      const float base = (mnew == -INFINITY) ? 0.0f : mnew;
-      const float alpha = __builtin_amdgcn_exp2f(m[qt] - base);
-      m[qt] = mnew;
+      const float mx = tmax * c;  // c > 0: max of scaled = scaled max
+      if (mx > m[qt] + kRescaleSlack) {
+        const float alpha = __builtin_amdgcn_exp2f(m[qt] - mx);  // 0 on the first visible tile
+        m[qt] = mx;
+        l[qt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < kD / 16; ++dt) o[qt][dt] *= alpha;
+      }
+      // m is -inf only while every key so far was masked (then so is this tile)
+      const float base = (m[qt] == -INFINITY) ? 0.0f : m[qt];
       float psum = 0.0f;
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
@@ -287,19 +359,19 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) p[qt][blk][j] = (__bf16)pv[j];
       }
-      l[qt] = l[qt] * alpha + psum;
-      if (alpha != 1.0f) {
-#pragma unroll
-        for (int dt = 0; dt < kD / 16; ++dt) o[qt][dt] *= alpha;
-      }
+      l[qt] += psum;
     }
 
-    // O^T += V^T P^T
+    // O^T += V^T P^T; lane (g, col) reads V rows blk*32 + 8g + 0..7 at
+    // d = dt*16 + col through two transposed 4x16 reads
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
       for (int dt = 0; dt < kD / 16; ++dt) {
-        const bf16x8 vf = ld_bf16x8(Vt + (dt * 16 + col) * kVPad + blk * 32 + 8 * g);
+        const uint8_t *vp = Vs + blk * 32 * kRowBytes + vbase + ((dt ^ vh) << 5);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((CFA_LDS i16x4 *)vp);
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((CFA_LDS i16x4 *)(vp + 4 * kRowBytes));
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt)
           o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, p[qt][blk], o[qt][dt], 0, 0, 0);
@@ -387,6 +459,8 @@ static void split_plan(int B, int Hkv, int max_keys, int splits_req, int &splits
     const int items = std::max(1, B * Hkv);
     s = std::max(1, (cus + items - 1) / items);  // about one work-group per compute unit
   }
+  // a split covers at most kMaxTilesPerSplit tiles (its page lookups fit LDS)
+  s = std::max(s, (tiles + kMaxTilesPerSplit - 1) / kMaxTilesPerSplit);
   s = std::min(s, tiles);
   tps = (tiles + s - 1) / s;
   splits = (tiles + tps - 1) / tps;
@@ -422,7 +496,7 @@ extern "C" int cfa_tree_attention(const void *q, const void *k_pool, const void 
     return fail_arg("n_q_heads must be a positive multiple of n_kv_heads");
   const int G = n_q_heads / n_kv_heads;
   if (G * N > kMaxRows) return fail_arg("(n_q_heads / n_kv_heads) * N must be at most 256");
-  if (block_size <= 0 || kKT % block_size) return fail_arg("block_size must divide 64");
+  if (block_size <= 0 || block_size % 16) return fail_arg("block_size must be a multiple of 16");
   if (num_blocks <= 0 || num_layers <= 0 || layer < 0 || layer >= num_layers)
     return fail_arg("bad pool geometry (num_blocks, num_layers, layer)");
   if (max_keys < N) return fail_arg("max_keys must be at least N (context + tree tokens)");
