@@ -11,21 +11,28 @@
 // been appended at positions ctx_b .. ctx_b + N - 1.
 //
 // One work-group = (split, kv head, sequence); its 8 waves hold all G*N query
-// rows (two 16-row tiles each, Q^T in registers) and share a ring of
-// kStages LDS stages, each holding one 64-key K tile and one 64-key V tile.
-// Tiles move HBM -> LDS with direct 16-byte global_load_lds transfers (no
-// register staging), kStages - 1 tiles ahead of the tile being computed.
-// Everything is computed in the transposed form
-//   S^T = K Q^T            (MFMA A = K rows, B = Q^T columns)
+// rows (two 16-row tiles each, Q^T in registers, pre-scaled by
+// scale*log2(e)).  64-key K and V tiles move HBM -> LDS with direct 16-byte
+// global_load_lds transfers (no register staging) into two rings (K: 3
+// stages, V: 4), three tiles ahead of the tile being computed; the split's
+// page lookups are resolved once into an LDS table.  Everything is computed
+// in the transposed form
+//   S^T = K Q^T - b        (MFMA A = K rows, B = Q^T columns, C = -b)
 //   O^T += V^T P^T         (MFMA A = V^T rows, B = P^T columns)
+//   l   += 1^T P^T         (row sums on the MFMA unit too)
 // so each lane owns one query column throughout: the softmax of a column and
 // the rescale of its O^T column stay in registers, and the P^T operand of the
-// second product is the first product's output converted to bf16 in place.
-// Within a 32-key block the two 16-key MFMA tiles take keys {8g+i} and
-// {8g+4+i} (g = lane / 16, i < 4), so lane (g, q) ends up with keys 8g..8g+7
-// of column q: exactly its 8-element k-slice of P^T.  The matching V^T
-// k-slice comes from two ds_read_b64_tr_b16 transposed reads of the V tile,
-// which stays in its natural [key][d] layout.
+// second product is exp2 of the first product's output in bf16.  Within a
+// 32-key block the two 16-key MFMA tiles take keys {8g+i} and {8g+4+i}
+// (g = lane / 16, i < 4), so lane (g, q) ends up with keys 8g..8g+7 of
+// column q: exactly its 8-element k-slice of P^T.  The matching V^T k-slice
+// comes from two ds_read_b64_tr_b16 transposed reads of the V tile, which
+// stays in its natural [key][d] layout.
+//
+// Each tile runs as a VALU phase (mask, column maxima, exponentials) and an
+// MFMA phase (PV of this tile, QK of the next).  Waves w and w + 4 share a
+// SIMD and run one phase apart, so one's exponentials overlap the other's
+// MFMAs.
 //
 // LDS layouts (256-byte rows, 16-byte chunks XOR-swizzled so that the MFMA
 // operand reads of one wave hit distinct banks):
@@ -33,8 +40,8 @@
 //      16-row MFMA tile reads consecutive rows); chunk c sits at c ^ (R % 16).
 //   V: row = key; chunk c sits at c ^ 2*((key % 4) | 4*((key / 8) % 2)).
 //
-// Softmax rescaling is lazy: a column's exponent base only moves when its
-// running maximum grows by more than kRescaleSlack (log2 units), so P^T
+// Softmax rescaling is lazy: a column's exponent base b only moves when its
+// running maximum exceeds it by more than kRescaleSlack (log2 units), so P^T
 // entries stay below 2^kRescaleSlack and the O^T rescale is rare.  Splits of
 // the key range are merged by a log-sum-exp pass.
 #include <hip/hip_runtime.h>
@@ -61,10 +68,13 @@ constexpr int kQT = 2;                        // 16-row query tiles per wave
 constexpr int kMaxRows = kWaves * kQT * 16;   // 256 query rows per work-group
 constexpr int kRowBytes = kD * 2;             // one K or V row, bf16
 constexpr int kTileBytes = kKT * kRowBytes;   // 16 KiB
-constexpr int kStages = 3;                    // LDS ring depth (tiles)
-constexpr int kStageBytes = 2 * kTileBytes;   // K tile then V tile
+constexpr int kKStages = 3;                   // K-tile ring (tile u: stage u % 3)
+constexpr int kVStages = 4;                   // V-tile ring (read one iteration after K)
 constexpr int kLoadsPerTile = 4;              // global_load_lds per wave per tile
 constexpr float kRescaleSlack = 8.0f;         // log2 units
+#ifndef CFA_TA_SGB
+#define CFA_TA_SGB 1
+#endif
 constexpr int kMaxGroups = 1024;              // 16-key groups per split (page lookup table)
 constexpr int kMaxTilesPerSplit = kMaxGroups / (kKT / 16);
 
@@ -146,13 +156,14 @@ __device__ __forceinline__ long long uniform_i64(long long v) {
 }
 
 // Issue this wave's share of the tile at key kbase: two 1 KiB K transfers
-// (LDS rows 8w..8w+7) and two 1 KiB V transfers (keys 8w..8w+7).  Each
+// (K-tile LDS rows 8w..8w+7) and two 1 KiB V transfers (keys 8w..8w+7).  Each
 // transfer covers four keys of one 16-key group, and a group never straddles
 // a page (block_size % 16 == 0).  Keys at or past nkeys re-read key
 // nkeys - 1: a finite, in-bounds row that the mask then hides.  gtab holds
 // the split's group row offsets (group_row_offset) from group g0 on.
 __device__ __forceinline__ void issue_tile(const Args &a, const long long *gtab, int g0, int kbase,
-                                           int nkeys, uint8_t *stage, int wave, int lane) {
+                                           int nkeys, uint8_t *kdst, uint8_t *vdst, int wave,
+                                           int lane) {
   const int sub = lane >> 4, pc = lane & 15;
   {
     // K: the wave's rows hold keys of the tile's 16-group 2 (w / 4) + (w % 2)
@@ -165,7 +176,7 @@ __device__ __forceinline__ void issue_tile(const Args &a, const long long *gtab,
       const int c = pc ^ (R & 15);
       const int pos = min(kbase + k_key_of_row(R), nkeys - 1);
       dma16(base + ((pos - gstart) * kD + c * 8),
-            (CFA_LDS void *)(stage + (8 * wave + 4 * j) * kRowBytes));
+            (CFA_LDS void *)(kdst + (8 * wave + 4 * j) * kRowBytes));
     }
   }
   {
@@ -179,7 +190,7 @@ __device__ __forceinline__ void issue_tile(const Args &a, const long long *gtab,
       const int c = pc ^ v_swz(key);
       const int pos = min(kbase + key, nkeys - 1);
       dma16(base + ((pos - gstart) * kD + c * 8),
-            (CFA_LDS void *)(stage + kTileBytes + (8 * wave + 4 * j) * kRowBytes));
+            (CFA_LDS void *)(vdst + (8 * wave + 4 * j) * kRowBytes));
     }
   }
 }
@@ -197,10 +208,190 @@ __device__ __forceinline__ uint64_t tile_visibility(int kbase, int ctx, uint64_t
 }
 
 __device__ __forceinline__ float xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m, 64)); }
-__device__ __forceinline__ float xor_sum(float v, int m) { return v + __shfl_xor(v, m, 64); }
+
+// Per-wave state of the pipelined loop: 16-row query tiles qt of this wave,
+// scores of one 64-key tile s[qt][blk][T] (keys blk*32 + 8g + 4T + i) and its
+// bf16 probabilities p[qt][blk] (keys blk*32 + 8g + 0..7).
+struct Scores {
+  f32x4 s[kQT][2][2];
+};
+struct Probs {
+  bf16x8 p[kQT][2];
+};
+
+struct Lane {
+  bf16x8 qf[kQT][4];   // Q^T columns pre-scaled by scale*log2(e)
+  uint64_t anc[kQT];   // ancestor-or-self masks of the wave's columns
+  int koff[4];         // K-tile LDS byte offsets of this lane's operand reads
+  int vbase, vh;       // V-tile transposed-read offset and swizzle
+  int g;               // lane / 16
+};
+
+// S^T = K Q^T - base: the accumulators start at -b so that the products come
+// out relative to the column's exponent base.
+__device__ __forceinline__ void qk_tile(const Lane &ln, const uint8_t *Ks, const float *b,
+                                        Scores &S) {
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt)
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int T = 0; T < 2; ++T) S.s[qt][blk][T] = f32x4{-b[qt], -b[qt], -b[qt], -b[qt]};
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+        const uint4 kv =
+            *reinterpret_cast<const uint4 *>(Ks + (blk * 32 + T * 16) * kRowBytes + ln.koff[kk]);
+        const bf16x8 kf = __builtin_bit_cast(bf16x8, kv);
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt)
+          S.s[qt][blk][T] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, ln.qf[qt][kk], S.s[qt][blk][T], 0, 0, 0);
+      }
+}
+
+// Online-softmax bookkeeping of one column: b is the exponent base (log2
+// units) the scores are relative to, valid says b has been set.
+struct Softmax {
+  float b[kQT];
+  bool valid[kQT];
+};
+
+// VALU phase of tile t: mask (tiles reaching the tree), column maxima, the
+// rare rebase, and the probabilities P = exp2(S) in bf16.  S holds tile t's
+// scores relative to each column's exponent base b; the base only moves when
+// a column's maximum exceeds it by more than kRescaleSlack, which also
+// rescales O and l (they hold tiles < t, so this precedes tile t's PV).
+__device__ __forceinline__ void valu_phase(const Lane &ln, int kbase, int ctx, Scores &S,
+                                           Softmax &sm, f32x4 (&o)[kQT][kD / 16],
+                                           f32x4 (&lacc)[kQT], Probs &P) {
+  if (kbase + kKT > ctx) {
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      // bit k: tile key k is visible to this column; this lane's keys are
+      // blk*32 + 8g + 4T + i, i.e. bit blk*32 + 4T + i of vis >> 8g
+      const uint64_t vis = tile_visibility(kbase, ctx, ln.anc[qt]) >> (8 * ln.g);
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            S.s[qt][blk][T][i] =
+                ((vis >> (blk * 32 + 4 * T + i)) & 1ull) ? S.s[qt][blk][T][i] : -INFINITY;
+    }
+  }
+  float mx[kQT];
+  bool resc[kQT];
+  bool any = false;
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
+    float v = -INFINITY;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v = fmaxf(v, S.s[qt][blk][T][i]);
+    v = xor_max(v, 16);
+    mx[qt] = xor_max(v, 32);
+    resc[qt] = mx[qt] > -INFINITY && (!sm.valid[qt] || mx[qt] > kRescaleSlack);
+    any |= resc[qt];
+  }
+  if (__ballot(any) != 0) {
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      const float d = resc[qt] ? mx[qt] : 0.0f;
+      const float alpha = resc[qt] ? (sm.valid[qt] ? __builtin_amdgcn_exp2f(-d) : 0.0f) : 1.0f;
+      sm.b[qt] += d;
+      sm.valid[qt] = sm.valid[qt] || resc[qt];
+      lacc[qt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < kD / 16; ++dt) o[qt][dt] *= alpha;
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int T = 0; T < 2; ++T) S.s[qt][blk][T] -= d;
+    }
+  }
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt)
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          P.p[qt][blk][T * 4 + i] = (__bf16)__builtin_amdgcn_exp2f(S.s[qt][blk][T][i]);
+  // keep the exponentials in this phase: without a use here the compiler
+  // sinks them past the phase barrier, next to the MFMAs that read them
+  asm volatile("" ::"v"(P.p[0][0]), "v"(P.p[0][1]), "v"(P.p[1][0]), "v"(P.p[1][1]));
+}
+
+// MFMA phase of tile t: O^T += V_t^T P^T and l += 1^T P^T, then
+// S = K_{t+1} Q^T - b (tile t+1's scores; for the last tile the stage read is
+// stale and the result unused).  The QK products run k-slice outermost so
+// that eight independent accumulation chains interleave: a dependent MFMA
+// issued right behind its predecessor stalls the matrix pipe.  Lane (g, col)
+// reads V rows blk*32 + 8g + 0..7 at d = dt*16 + col through two transposed
+// 4x16 reads.
+__device__ __forceinline__ void mfma_phase(const Lane &ln, const uint8_t *Knext, const uint8_t *Vs,
+                                           const float *b, const Probs &P, Scores &S,
+                                           f32x4 (&o)[kQT][kD / 16], f32x4 (&lacc)[kQT]) {
+  bf16x8 ones;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = (__bf16)1.0f;
+  f32x4 negb[kQT];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) negb[qt] = f32x4{-b[qt], -b[qt], -b[qt], -b[qt]};
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+    for (int dt = 0; dt < kD / 16; ++dt) {
+      const uint8_t *vp = Vs + blk * 32 * kRowBytes + ln.vbase + ((dt ^ ln.vh) << 5);
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((CFA_LDS i16x4 *)vp);
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((CFA_LDS i16x4 *)(vp + 4 * kRowBytes));
+      const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt)
+        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, P.p[qt][blk], o[qt][dt], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt)
+      lacc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, P.p[qt][blk], lacc[qt], 0, 0, 0);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+        const bf16x8 kf = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const uint4 *>(Knext + (blk * 32 + T * 16) * kRowBytes + ln.koff[kk]));
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt)
+          S.s[qt][blk][T] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              kf, ln.qf[qt][kk], kk == 0 ? negb[qt] : S.s[qt][blk][T], 0, 0, 0);
+      }
+#if CFA_TA_SGB
+  // software pipeline of the operand reads: four fragments ahead, then two
+  // reads after every pair of MFMAs
+  __builtin_amdgcn_sched_group_barrier(0x0100, 8, 0);
+#pragma unroll
+  for (int j = 0; j < 34; ++j) {
+    __builtin_amdgcn_sched_group_barrier(0x0008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x0100, 2, 0);
+  }
+#endif
+}
 
 __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
-  __shared__ __align__(16) uint8_t smem[kStages * kStageBytes];
+  __shared__ __align__(16) uint8_t kring[kKStages * kTileBytes];
+  __shared__ __align__(16) uint8_t vring[kVStages * kTileBytes];
   __shared__ long long gtab[kMaxGroups];
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -216,23 +407,36 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
   const int t1 = min(ntiles, t0 + a.tiles_per_split);
   const int g0 = t0 * (kKT / 16);
 
-  // query rows of this wave: r = node * G + head-in-group
-  const uint64_t node_bits = a.N >= 64 ? ~0ull : ((1ull << a.N) - 1);
-  bf16x8 qf[kQT][4];
-  uint64_t anc[kQT];
+  // query rows of this wave: r = node * G + head-in-group; Q^T is scaled by
+  // scale*log2(e) once here so that scores come out in log2 units
+  Lane ln;
+  ln.g = g;
   bool qvalid[kQT];
+  {
+    const uint64_t node_bits = a.N >= 64 ? ~0ull : ((1ull << a.N) - 1);
 #pragma unroll
-  for (int qt = 0; qt < kQT; ++qt) {
-    const int r = (wave * kQT + qt) * 16 + col;
-    qvalid[qt] = r < a.rows;
-    const int node = qvalid[qt] ? r / a.G : 0, hg = r % a.G;
-    anc[qt] = qvalid[qt] ? a.mask[(long long)b * a.mask_sb + node] & node_bits : 0ull;
-    const uint16_t *qp = a.q + (((long long)b * a.N + node) * a.Hq + (long long)h * a.G + hg) * kD;
+    for (int qt = 0; qt < kQT; ++qt) {
+      const int r = (wave * kQT + qt) * 16 + col;
+      qvalid[qt] = r < a.rows;
+      const int node = qvalid[qt] ? r / a.G : 0, hg = r % a.G;
+      ln.anc[qt] = qvalid[qt] ? a.mask[(long long)b * a.mask_sb + node] & node_bits : 0ull;
+      const uint16_t *qp =
+          a.q + (((long long)b * a.N + node) * a.Hq + (long long)h * a.G + hg) * kD;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const uint4 v = qvalid[qt] ? ld_g16(qp + kk * 32 + g * 8) : make_uint4(0, 0, 0, 0);
-      qf[qt][kk] = __builtin_bit_cast(bf16x8, v);
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint4 v = qvalid[qt] ? ld_g16(qp + kk * 32 + g * 8) : make_uint4(0, 0, 0, 0);
+        const bf16x8 raw = __builtin_bit_cast(bf16x8, v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ln.qf[qt][kk][j] = (__bf16)((float)raw[j] * a.scale_log2);
+      }
     }
+  }
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) ln.koff[kk] = col * kRowBytes + (((kk * 4 + g) ^ col) << 4);
+  {
+    const int vrow = 8 * g + (col >> 2);
+    ln.vh = v_swz(vrow) >> 1;
+    ln.vbase = vrow * kRowBytes + ((col >> 1) & 1) * 16 + (col & 1) * 8;
   }
 
   // the split's page lookups, once
@@ -246,143 +450,78 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
   wait_vmcnt<0>();
   __syncthreads();
 
-  // prologue: the first kStages - 1 tiles go in flight
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s)
-    if (t0 + s < t1)
-      issue_tile(a, gtab, g0, (t0 + s) * kKT, nkeys, smem + s * kStageBytes, wave, lane);
-
   f32x4 o[kQT][kD / 16];
-  float m[kQT], l[kQT];
+  f32x4 lacc[kQT];
+  Softmax sm;
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt) {
-    m[qt] = -INFINITY;
-    l[qt] = 0.0f;
+    sm.b[qt] = 0.0f;
+    sm.valid[qt] = false;
+    lacc[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int dt = 0; dt < kD / 16; ++dt) o[qt][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  // per-lane LDS byte offsets, tile-relative
-  int koff[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) koff[kk] = col * kRowBytes + (((kk * 4 + g) ^ col) << 4);
-  const int vrow = 8 * g + (col >> 2);
-  const int vh = v_swz(vrow) >> 1;
-  const int vbase = vrow * kRowBytes + ((col >> 1) & 1) * 16 + (col & 1) * 8;
-
-  const float c = a.scale_log2;
-  for (int t = t0; t < t1; ++t) {
-    // this wave's transfers of tile t have landed once at most the later
-    // tiles' transfers are outstanding; the barrier then publishes every
-    // wave's transfers and retires the stage read during tile t - 1
-    const int later = min(kStages - 2, t1 - 1 - t);
-    if (later >= 1) wait_vmcnt<kLoadsPerTile * (kStages - 2)>();
+  if (t0 < t1) {
+    for (int u = t0; u < min(t0 + 3, t1); ++u)
+      issue_tile(a, gtab, g0, u * kKT, nkeys, kring + ((u - t0) % kKStages) * kTileBytes,
+                 vring + ((u - t0) % kVStages) * kTileBytes, wave, lane);
+    // tile t0 has landed once at most the other prologue tiles are in flight
+    const int later = min(t0 + 3, t1) - 1 - t0;
+    if (later >= 2) wait_vmcnt<2 * kLoadsPerTile>();
+    else if (later == 1) wait_vmcnt<kLoadsPerTile>();
     else wait_vmcnt<0>();
     block_barrier();
-    if (t + kStages - 1 < t1)
-      issue_tile(a, gtab, g0, (t + kStages - 1) * kKT, nkeys,
-                 smem + ((t - t0 + kStages - 1) % kStages) * kStageBytes, wave, lane);
-    const uint8_t *Ks = smem + ((t - t0) % kStages) * kStageBytes;
-    const uint8_t *Vs = Ks + kTileBytes;
-    const int kbase = t * kKT;
-
-    // S^T for the tile: s[qt][blk][T] holds keys blk*32 + T*4 + 8g + i
-    f32x4 s[kQT][2][2];
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-      for (int T = 0; T < 2; ++T) {
-#pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) s[qt][blk][T] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const uint4 kv =
-              *reinterpret_cast<const uint4 *>(Ks + (blk * 32 + T * 16) * kRowBytes + koff[kk]);
-          const bf16x8 kf = __builtin_bit_cast(bf16x8, kv);
-#pragma unroll
-          for (int qt = 0; qt < kQT; ++qt)
-            s[qt][blk][T] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[qt][kk], s[qt][blk][T], 0, 0, 0);
+    // Waves w and w + 4 share a SIMD.  Group 1 (waves 4..7) runs one phase
+    // behind group 0, so while one wave of a SIMD is in its VALU phase the
+    // other is in its MFMA phase.  Barrier k ties group 0's phase k to group
+    // 1's phase k - 1; group 1 takes one extra barrier first, group 0 one at
+    // the end.  Tile t+1 must be visible before barrier 2(t - t0) + 1 (the
+    // first MFMA phase reading it follows that barrier), and tile t + 3 is
+    // issued right after it: its stages last held tiles t (K) and t - 1 (V),
+    // whose last readers finished before that barrier.
+    const bool lag = wave >= kWaves / 2;
+    if (lag) block_barrier();
+    Scores S;
+    Probs P;
+    qk_tile(ln, kring, sm.b, S);
+    for (int t = t0; t < t1; ++t) {
+      const int kbase = t * kKT;
+      if (!lag) {
+        block_barrier();
+      } else {
+        if (t + 2 < t1) wait_vmcnt<kLoadsPerTile>();
+        else wait_vmcnt<0>();
+        block_barrier();
+        if (t + 3 < t1) {
+          const int u = t + 3 - t0;
+          issue_tile(a, gtab, g0, (t + 3) * kKT, nkeys, kring + (u % kKStages) * kTileBytes,
+                     vring + (u % kVStages) * kTileBytes, wave, lane);
         }
       }
-
-    // mask (tiles reaching the tree only), then online softmax in log2 units
-    // (per query column; the 4 lanes g of a column share it)
-    if (kbase + kKT > ctx) {
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        // bit k: tile key k is visible to this column; this lane's keys are
-        // blk*32 + 8g + 4T + i, i.e. bit blk*32 + 4T + i of vis >> 8g
-        const uint64_t vis = tile_visibility(kbase, ctx, anc[qt]) >> (8 * g);
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-          for (int T = 0; T < 2; ++T)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              s[qt][blk][T][i] = ((vis >> (blk * 32 + 4 * T + i)) & 1ull) ? s[qt][blk][T][i] : -INFINITY;
+      valu_phase(ln, kbase, ctx, S, sm, o, lacc, P);
+      if (!lag) {
+        if (t + 2 < t1) wait_vmcnt<kLoadsPerTile>();
+        else wait_vmcnt<0>();
+        block_barrier();
+        if (t + 3 < t1) {
+          const int u = t + 3 - t0;
+          issue_tile(a, gtab, g0, (t + 3) * kKT, nkeys, kring + (u % kKStages) * kTileBytes,
+                     vring + (u % kVStages) * kTileBytes, wave, lane);
+        }
+      } else {
+        block_barrier();
       }
+      mfma_phase(ln, kring + ((t + 1 - t0) % kKStages) * kTileBytes,
+                 vring + ((t - t0) % kVStages) * kTileBytes, sm.b, P, S, o, lacc);
     }
-    bf16x8 p[kQT][2];
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) {
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-        for (int T = 0; T < 2; ++T)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[qt][blk][T][i]);
-      tmax = xor_max(tmax, 16);
-      tmax = xor_max(tmax, 32);
-      const float mx = tmax * c;  // c > 0: max of scaled = scaled max
-      if (mx > m[qt] + kRescaleSlack) {
-        const float alpha = __builtin_amdgcn_exp2f(m[qt] - mx);  // 0 on the first visible tile
-        m[qt] = mx;
-        l[qt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < kD / 16; ++dt) o[qt][dt] *= alpha;
-      }
-      // m is -inf only while every key so far was masked (then so is this tile)
-      const float base = (m[qt] == -INFINITY) ? 0.0f : m[qt];
-      float psum = 0.0f;
-#pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
-        float pv[8];
-#pragma unroll
-        for (int T = 0; T < 2; ++T)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][blk][T][i], c, -base));
-            pv[T * 4 + i] = e;
-            psum += e;
-          }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) p[qt][blk][j] = (__bf16)pv[j];
-      }
-      l[qt] += psum;
-    }
-
-    // O^T += V^T P^T; lane (g, col) reads V rows blk*32 + 8g + 0..7 at
-    // d = dt*16 + col through two transposed 4x16 reads
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-      for (int dt = 0; dt < kD / 16; ++dt) {
-        const uint8_t *vp = Vs + blk * 32 * kRowBytes + vbase + ((dt ^ vh) << 5);
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((CFA_LDS i16x4 *)vp);
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((CFA_LDS i16x4 *)(vp + 4 * kRowBytes));
-        const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-        for (int qt = 0; qt < kQT; ++qt)
-          o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, p[qt][blk], o[qt][dt], 0, 0, 0);
-      }
+    if (!lag) block_barrier();
   }
 
-  // column sums over the 4 lanes of a query; write final or partial outputs
+  // every lane holds its column's full sum; write final or partial outputs
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt) {
-    float ls = xor_sum(l[qt], 16);
-    ls = xor_sum(ls, 32);
+    const float ls = lacc[qt][0];
     if (!qvalid[qt]) continue;
     const int r = (wave * kQT + qt) * 16 + col;
     if (a.splits == 1) {
@@ -405,42 +544,46 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
 #pragma unroll
       for (int dt = 0; dt < kD / 16; ++dt)
         *reinterpret_cast<f32x4 *>(pp + dt * 16 + 4 * g) = o[qt][dt];
-      if (g == 0) a.part_ml[prow] = make_float2(m[qt], ls);
+      if (g == 0) a.part_ml[prow] = make_float2(sm.valid[qt] ? sm.b[qt] : -INFINITY, ls);
     }
   }
 }
 
-// Log-sum-exp merge of the splits: one wave per query row, 2 d-values per lane.
+// Log-sum-exp merge of the splits: 32 threads per query row, four d-values
+// (one 16-byte load per split) per thread, eight rows per work-group.
 __global__ __launch_bounds__(256) void tree_merge_kernel(Args a) {
-  const int row_g = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const long long row_g = (long long)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int q4 = threadIdx.x & 31;
   const long long total = (long long)a.B * a.Hkv * a.rows;
   if (row_g >= total) return;
-  const int r = row_g % a.rows;
-  const int h = (row_g / a.rows) % a.Hkv;
-  const int b = row_g / (a.rows * a.Hkv);
+  const int r = (int)(row_g % a.rows);
+  const int h = (int)((row_g / a.rows) % a.Hkv);
+  const int b = (int)(row_g / ((long long)a.rows * a.Hkv));
+  const long long split_stride = (long long)a.B * a.Hkv * a.rows;  // rows per split
+  const long long prow0 = ((long long)b * a.Hkv + h) * a.rows + r;
   float M = -INFINITY;
-  for (int s = 0; s < a.splits; ++s) {
-    const long long prow = (((long long)s * a.B + b) * a.Hkv + h) * a.rows + r;
-    M = fmaxf(M, a.part_ml[prow].x);
-  }
+  for (int s = 0; s < a.splits; ++s) M = fmaxf(M, a.part_ml[prow0 + s * split_stride].x);
   const float base = (M == -INFINITY) ? 0.0f : M;
-  float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  float L = 0.0f;
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
   for (int s = 0; s < a.splits; ++s) {
-    const long long prow = (((long long)s * a.B + b) * a.Hkv + h) * a.rows + r;
+    const long long prow = prow0 + s * split_stride;
     const float2 ml = a.part_ml[prow];
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(a.part_o + prow * kD + 4 * q4);
     const float w = __builtin_amdgcn_exp2f(ml.x - base);
     L += ml.y * w;
-    const float2 ov = *reinterpret_cast<const float2 *>(a.part_o + prow * kD + 2 * lane);
-    o0 += ov.x * w;
-    o1 += ov.y * w;
+    acc += v * w;
   }
   const float inv = (L > 0.0f) ? 1.0f / L : 0.0f;
   const int node = r / a.G, hg = r % a.G;
   uint16_t *op = a.out + (((long long)b * a.N + node) * a.Hq + (long long)h * a.G + hg) * kD;
-  const uint32_t w = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(o0 * inv)) |
-                     ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(o1 * inv)) << 16);
-  *reinterpret_cast<uint32_t *>(op + 2 * lane) = w;
+  uint2 w;
+  w.x = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc[0] * inv)) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc[1] * inv)) << 16);
+  w.y = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc[2] * inv)) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc[3] * inv)) << 16);
+  *reinterpret_cast<uint2 *>(op + 4 * q4) = w;
 }
 
 }  // namespace tree
@@ -538,7 +681,7 @@ extern "C" int cfa_tree_attention(const void *q, const void *k_pool, const void 
   CFA_LAUNCH("tree_attn", tree_attn_kernel, dim3(a.splits, n_kv_heads, B), dim3(kNT), 0, st, a);
   if (a.splits > 1) {
     const long long rows = (long long)B * n_kv_heads * a.rows;
-    CFA_LAUNCH("tree_attn_merge", tree_merge_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+    CFA_LAUNCH("tree_attn_merge", tree_merge_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0,
                st, a);
   }
   return CFA_OK;
