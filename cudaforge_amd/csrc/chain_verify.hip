@@ -35,23 +35,35 @@ namespace chain {
 enum Kind : int { kNone = 0, kResid = 1, kPlain = 2, kPyBonus = 3 };
 
 // Exact multi-work-group sampler state (per sequence b).
-constexpr int kMwNT = 256;                  // threads per chunk work-group
-constexpr int kMwTile = 16;                 // elements per thread (one tile)
-constexpr int kMwChunk = kMwNT * kMwTile;   // 4096 elements per chunk
+constexpr int kMwNT = 256;                  // threads per sums / records work-group
+constexpr int kMwTile = 16;                 // elements per lane (one tile)
+constexpr int kMwChunkTiles = 64;           // tiles per chunk (one wave)
+constexpr int kMwChunk = kMwChunkTiles * kMwTile;  // 1024 elements per chunk
 constexpr int kMwMaxBad = 64;               // cached serial tiles per row and pass
-constexpr int kMwMaxNC = 1024;              // chunks per row (V <= 4M)
+constexpr int kMwMaxNC = 4096;              // chunks per row (V <= 4M)
 struct MwJob {  // what sequence b still has to draw
   int kind, row, n, eos_acc;
   float u;
+  float tM, tInvS;  // (max, 1/S) of the target row (logits input)
+  float dM, dInvS;  // and of the draft row of a residual draw
   int pad[3];
 };
 struct MwRes {  // per sequence: residual sum, fallback flag, drawn index
   float S;
   int fallback, idx, pad;
 };
-struct MwRec {  // a run's function of the entry parity and its region guess
+struct MwRec {  // a tile's function of the entry parity, its region guess, pad = 1: replay
   uint32_t e, o;
   int reg, pad;
+};
+// A chunk as run 0 (tiles [0, brk)), break tile brk (replayed serially when
+// brk_serial, otherwise run 1 starts there in another region) and run 1
+// (the rest); brk = -1: one run.  Runs are functions of the entry parity.
+struct MwChunk {
+  uint32_t e0, o0, e1, o1;
+  int reg0, reg1;
+  int brk, brk_serial;
+  int status, pad[3];
 };
 struct MwBad {  // a tile the walk will probably replay serially, with its values
   int tile, pad[3];
@@ -85,8 +97,8 @@ struct Args {
   MwJob *jobs;            // [B]
   MwRes *res;             // [B]
   float *csum_x, *csum_t; // [B, NC] approximate chunk sums
-  MwRec *crec;            // [2, B, NC]   chunk functions, per pass
-  MwRec *trec;            // [2, B, NC*256] tile functions, per pass
+  MwChunk *crec;          // [2, B, NC]   chunk structure, per pass
+  MwRec *trec;            // [2, B, NC*64] tile functions, per pass
   int *badcnt;            // [2, B]
   MwBad *bad;             // [2, B, kMwMaxBad]
   int32_t *out_accept_len, *out_tokens, *out_num_emitted, *out_final, *out_eos;
@@ -161,6 +173,15 @@ __device__ float2 block_ms(float m, float s, float c) {
   return out;
 }
 
+// Streaming 16-byte load: every logit is read once here, so the lines are
+// marked non-temporal instead of displacing cached data (on MI355X this
+// raises the pass from ~65% to ~75% of HBM peak).
+__device__ __forceinline__ float4 ld_stream4(const float4 *p) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const f32x4 q = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+  return make_float4(q[0], q[1], q[2], q[3]);
+}
+
 template <int NT, int W>
 __global__ __launch_bounds__(NT) void stats_kernel(Args a) {
   const long long total = (long long)a.B * a.rpb * a.Vw;
@@ -181,7 +202,7 @@ __global__ __launch_bounds__(NT) void stats_kernel(Args a) {
       for (; i + (U - 1) * NT < s1; i += U * NT) {
         float4 v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = p4[i + u * NT];
+        for (int u = 0; u < U; ++u) v[u] = ld_stream4(p4 + i + u * NT);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const float mx = fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w));
@@ -195,7 +216,7 @@ __global__ __launch_bounds__(NT) void stats_kernel(Args a) {
         }
       }
       for (; i < s1; i += NT) {
-        const float4 v = p4[i];
+        const float4 v = ld_stream4(p4 + i);
         const float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
         if (mx > m) {
           s *= __builtin_amdgcn_exp2f((m - mx) * c);
@@ -207,7 +228,7 @@ __global__ __launch_bounds__(NT) void stats_kernel(Args a) {
       }
     } else {
       for (long long i = s0 + threadIdx.x; i < s1; i += NT) {
-        const float v = row[i];
+        const float v = __builtin_nontemporal_load(row + i);
         if (v > m) {
           s *= __builtin_amdgcn_exp2f((m - v) * c);
           m = v;
@@ -476,6 +497,19 @@ __global__ __launch_bounds__(256) void plan_kernel(Args a) {
       j.row = (nmin < K) ? nmin : K;
       j.eos_acc = 0;
     }
+    // row statistics of the draw's rows, once for every kernel that reads them
+    j.tM = j.dM = 0.0f;
+    j.tInvS = j.dInvS = 1.0f;
+    if (a.logits && (j.kind == kResid || j.kind == kPlain)) {
+      const float2 ts = row_stat(a, b * a.rpb + j.row);
+      j.tM = ts.x;
+      j.tInvS = ts.y;
+      if (j.kind == kResid) {
+        const float2 ds = row_stat(a, b * a.rpb + K + 1 + j.row);
+        j.dM = ds.x;
+        j.dInvS = ds.y;
+      }
+    }
     a.jobs[b] = j;
     a.res[b] = MwRes{0.0f, 0, -1, 0};
     a.badcnt[b] = 0;
@@ -484,22 +518,33 @@ __global__ __launch_bounds__(256) void plan_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------------------
-// Exact draw over all work-groups ("mw").  For each drawing sequence:
-//   sums    (grid NC x B)  approximate fp32 chunk sums of the residual and of
-//                          the target row, used only to guess regions;
-//   records (grid NC x B)  per pass: every tile quantised in its guessed
-//                          region (seqsum.hpp), composed into a chunk
-//                          function where the chunk stays in one region;
-//                          tiles that will need a serial replay are cached;
-//   walk    (grid B)       per pass: the validated hierarchical walk
-//                          (chunks, then tiles, then serial tiles) from the
-//                          exact running value, as seq::run does per block.
+// Exact draw over all work-groups ("mw").  A row is cut into chunks of 1024
+// elements (64 tiles of 16, one wave per chunk).  For each drawing sequence:
+//   sums    (grid NC/4 x B)  approximate fp32 chunk sums of the residual and
+//                            of the target row, used only to guess regions;
+//   records (grid NC/4 x B)  per pass: every tile quantised in its guessed
+//                            region (seqsum.hpp); per chunk, the composed
+//                            function of the tiles before its first break
+//                            (a tile straddling a region boundary, or a
+//                            region change), the break, and the function of
+//                            the tiles after it; tiles that will need a
+//                            serial replay are cached;
+//   walk    (grid B, 1 wave) per pass: chunk 0, where the running value is
+//                            small and crosses a binade every doubling, is
+//                            replayed serially; later chunks apply their
+//                            functions from the exact running value, and a
+//                            chunk with a break costs a check, the break
+//                            tile's serial replay and a second check.  Any
+//                            check that fails (a wrong guess, a second
+//                            break, a CDF hit inside a run) falls back to the
+//                            tile-level walk of seq::walk.
 // Pass 0 sums max(0, t - d) (speculative.cpp:30-35); pass 1 searches the
 // inverse CDF of max(0, t - d) / S, or of t for a bonus draw or the
 // sum <= 1e-6 fallback (speculative.cpp:11-24, 37-45, 97).
 // ---------------------------------------------------------------------------
 
 enum MwPass : int { kPassSum = 0, kPassCdf = 1 };
+enum MwStatus : int { kChunkOk = 0, kChunkTiles = 1, kChunkSkipped = 2 };
 
 // The element function of a (job, pass): 0 max(0,t-d), 1 max(0,t-d)/S, 2 t.
 struct MwElem {
@@ -519,10 +564,18 @@ __device__ __forceinline__ bool mw_active(const MwJob &j, int pass) {
 
 __device__ MwElem mw_elem(const Args &a, int b, const MwJob &j, int pass) {
   MwElem e;
-  e.t = make_dist(a, b, j.row);
+  e.t.p = row_ptr(a, b, j.row);
+  e.t.c = a.c;
+  e.t.logits = a.logits;
+  e.t.M = j.tM;
+  e.t.invS = j.tInvS;
   e.d = e.t;
   e.S = 1.0f;
-  if (j.kind == kResid) e.d = make_dist(a, b, a.K + 1 + j.row);
+  if (j.kind == kResid) {
+    e.d.p = row_ptr(a, b, a.K + 1 + j.row);
+    e.d.M = j.dM;
+    e.d.invS = j.dInvS;
+  }
   if (pass == kPassSum) {
     e.fn = 0;
   } else {
@@ -563,28 +616,21 @@ __device__ __forceinline__ void mw_tile_values(const Args &a, const MwElem &e, l
   for (int k = 0; k < kMwTile; ++k) x[k] = (i0 + k < a.V) ? e.eval(tv[k], e.fn != 2 ? dv[k] : 0.0f) : 0.0f;
 }
 
-// Deterministic block sum of one float per thread (kMwNT threads).
-__device__ float mw_block_sum(float v, float *red) {
+__device__ __forceinline__ float wave_sum_f32(float v) {
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float t = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kMwNT / 64; ++w) t += red[w];
-  __syncthreads();
-  return t;
+  return v;
 }
 
+// One wave per chunk: chunk c = 4 * blockIdx.x + wave, lane = tile in chunk.
 __global__ __launch_bounds__(kMwNT) void mw_sums_kernel(Args a) {
-  __shared__ float red[kMwNT / 64];
-  const int c = blockIdx.x, b = blockIdx.y;
+  const int b = blockIdx.y, lane = threadIdx.x & 63;
+  const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
   const MwJob j = a.jobs[b];
   if (j.kind != kResid && j.kind != kPlain) return;
+  if (c >= a.NC) return;
   const MwElem e = mw_elem(a, b, j, kPassSum);
-  const long long tile = (long long)c * kMwNT + threadIdx.x;
-  const long long i0 = tile * kMwTile;
+  const long long i0 = ((long long)c * kMwChunkTiles + lane) * kMwTile;
   float tv[kMwTile], dv[kMwTile];
   mw_load16(a, e.t.p, i0, tv);
   if (j.kind == kResid) mw_load16(a, e.d.p, i0, dv);
@@ -597,9 +643,9 @@ __global__ __launch_bounds__(kMwNT) void mw_sums_kernel(Args a) {
       if (j.kind == kResid) sx += relu_ref(tp - e.d.eval(dv[k]));
     }
   }
-  st = mw_block_sum(st, red);
-  sx = mw_block_sum(sx, red);
-  if (threadIdx.x == 0) {
+  st = wave_sum_f32(st);
+  sx = wave_sum_f32(sx);
+  if (lane == 0) {
     a.csum_t[(long long)b * a.NC + c] = st;
     a.csum_x[(long long)b * a.NC + c] = sx;
   }
@@ -612,47 +658,56 @@ __device__ float mw_entry_prefix(const float *csum, int c) {
   float acc = 0.0f;
   for (int base = 0; base < c; base += 64) {
     float v = (base + lane < c) ? csum[base + lane] : 0.0f;
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    acc += v;
+    acc += wave_sum_f32(v);
   }
   return acc;
 }
 
+// Composition of the functions of the lanes where `in` holds (lane order).
+__device__ __forceinline__ seq::Inc wave_compose_where(bool in, seq::Inc f) {
+  using namespace seq;
+  const Inc v = in ? f : inc_identity();
+  const Inc tot = (__ballot(v.e != v.o) == 0ull) ? Inc{wave_incl_add_u32(v.e), 0u}
+                                                 : wave_incl_compose(v);
+  if (__ballot(v.e != v.o) == 0ull) {
+    const uint32_t t = lane_bcast(tot.e, 63);
+    return Inc{t, t};
+  }
+  return Inc{lane_bcast(tot.e, 63), lane_bcast(tot.o, 63)};
+}
+
 __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
   using namespace seq;
-  __shared__ float wsum[kMwNT / 64];
-  __shared__ Inc wfun[kMwNT / 64];
-  __shared__ int wreg[kMwNT / 64], wok[kMwNT / 64];
-  const int c = blockIdx.x, b = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.y, lane = threadIdx.x & 63;
+  const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
   const MwJob j = a.jobs[b];
   if (!mw_active(j, pass)) return;
+  if (c == 0 || c >= a.NC) return;  // chunk 0 is replayed serially by the walk
   const MwElem e = mw_elem(a, b, j, pass);
   const long long rowrec = ((long long)pass * a.B + b);
-  MwRec *crec = a.crec + rowrec * a.NC;
-  MwRec *trec = a.trec + rowrec * a.NC * kMwNT;
+  MwChunk *crec = a.crec + rowrec * a.NC;
+  MwRec *trec = a.trec + rowrec * a.NC * kMwChunkTiles;
   // approximate entry value of this chunk
   const float *csum = (e.fn == 2 ? a.csum_t : a.csum_x) + (long long)b * a.NC;
   float E0 = mw_entry_prefix(csum, c);
   if (e.fn == 1) E0 = E0 / e.S;
   // a CDF search ends before any chunk whose entry is surely past u
   if (pass == kPassCdf && E0 * (1.0f - 1.0f / 64.0f) > j.u) {
-    if (tid == 0) crec[c] = MwRec{kBad, kBad, kAnyRegion, 1};
+    if (lane == 0) {
+      MwChunk r{};
+      r.status = kChunkSkipped;
+      crec[c] = r;
+    }
     return;
   }
-  const long long tile = (long long)c * kMwNT + tid;
+  const long long tile = (long long)c * kMwChunkTiles + lane;
   float x[kMwTile];
   mw_tile_values(a, e, tile, x);
   float A = 0.0f;
 #pragma unroll
   for (int k = 0; k < kMwTile; ++k) A += x[k];
   const float incl = wave_incl_scan_f32(A);
-  if (lane == 63) wsum[wave] = incl;
-  __syncthreads();
-  float wpre = 0.0f;
-  for (int q = 0; q < wave; ++q) wpre += wsum[q];
-  const float E = E0 + (wpre + (incl - A));
+  const float E = E0 + (incl - A);
   int r_lo = region_of(E * (1.0f - kDelta));
   const int r_hi = region_of((E + A) * (1.0f + kDelta));
   bool ok = (r_lo == r_hi);
@@ -670,7 +725,7 @@ __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
     ok = (f.e <= kUnitsTop) && (f.o <= kUnitsTop);
     if (!ok) f = Inc{kBad, kBad};
   }
-  trec[(long long)c * kMwNT + tid] = MwRec{f.e, f.o, r_lo, 0};
+  trec[tile] = MwRec{f.e, f.o, ok ? r_lo : kAnyRegion, ok ? 0 : 1};
   if (!ok) {  // cache the values for the walk's serial replay
     const int slot = atomicAdd(&a.badcnt[rowrec], 1);
     if (slot < kMwMaxBad) {
@@ -680,79 +735,103 @@ __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
       for (int k = 0; k < kMwTile; ++k) dst->x[k] = x[k];
     }
   }
-  // the chunk's function, if every tile is valid in one region
-  const unsigned long long okm = __ballot(ok);
-  const unsigned long long real = __ballot(r_lo != kAnyRegion);
-  const int r0 = real ? (int)seq::lane_bcast((uint32_t)r_lo, (int)__builtin_ctzll(real)) : kAnyRegion;
-  const unsigned long long same = __ballot(r_lo == r0 || r_lo == kAnyRegion);
-  const Inc wtot = wave_incl_compose(ok ? f : inc_identity());
-  if (lane == 63) {
-    wfun[wave] = wtot;
-    wreg[wave] = r0;
-    wok[wave] = (okm == ~0ull) && (same == ~0ull);
+  // chunk structure: run 0, an optional break, run 1
+  const bool real = ok && r_lo != kAnyRegion;
+  const unsigned long long realm = __ballot(real);
+  const int r_first = realm ? (int)lane_bcast((uint32_t)r_lo, (int)__builtin_ctzll(realm)) : kAnyRegion;
+  const unsigned long long brkm = __ballot(!ok || (real && r_lo != r_first));
+  MwChunk rec{};
+  rec.status = kChunkOk;
+  if (brkm == 0ull) {
+    const Inc F = wave_compose_where(true, f);
+    rec.e0 = F.e;
+    rec.o0 = F.o;
+    rec.reg0 = r_first;
+    rec.brk = -1;
+  } else {
+    const int k = (int)__builtin_ctzll(brkm);
+    const bool kbad = ((__ballot(!ok) >> k) & 1ull) != 0ull;
+    const int s1 = kbad ? k + 1 : k;
+    const unsigned long long before = (k == 0) ? 0ull : (~0ull >> (64 - k));
+    const Inc F0 = wave_compose_where(lane < k, f);
+    const bool in1 = lane >= s1;
+    const unsigned long long real1 = realm & ~((s1 >= 64) ? ~0ull : ((1ull << s1) - 1ull));
+    const int r1 = real1 ? (int)lane_bcast((uint32_t)r_lo, (int)__builtin_ctzll(real1)) : kAnyRegion;
+    const bool bad1 = in1 && (!ok || (real && r_lo != r1));
+    const Inc F1 = wave_compose_where(in1, f);
+    rec.e0 = F0.e;
+    rec.o0 = F0.o;
+    rec.reg0 = (realm & before) ? r_first : kAnyRegion;
+    rec.brk = k;
+    rec.brk_serial = kbad ? 1 : 0;
+    rec.e1 = F1.e;
+    rec.o1 = F1.o;
+    rec.reg1 = r1;
+    if (__ballot(bad1) != 0ull) rec.status = kChunkTiles;
   }
-  __syncthreads();
-  if (tid == 0) {
-    bool uni = true;
-    int reg = kAnyRegion;
-    Inc acc = inc_identity();
-    for (int w = 0; w < kMwNT / 64; ++w) {
-      if (!wok[w]) uni = false;
-      if (wreg[w] != kAnyRegion) {
-        if (reg == kAnyRegion)
-          reg = wreg[w];
-        else if (reg != wreg[w])
-          uni = false;
-      }
-      acc = compose(acc, wfun[w]);
-    }
-    crec[c] = uni ? MwRec{acc.e, acc.o, reg, 0} : MwRec{kBad, kBad, reg, 0};
-  }
+  if (lane == 0) crec[c] = rec;
 }
 
-constexpr int kMwPrefetch = 12;  // invalid chunks whose tile records are staged up front
+constexpr int kMwWin = 256;  // chunk records staged in LDS at a time
 
-__global__ __launch_bounds__(kMwNT) void mw_walk_kernel(Args a, int pass) {
+__global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
   using namespace seq;
-  __shared__ MwRec cr[kMwMaxNC];
-  __shared__ MwRec tr[kMwPrefetch + 1][kMwNT];
-  __shared__ int pref[kMwPrefetch];
+  __shared__ MwChunk cr[kMwWin];
+  __shared__ MwRec tr[kMwChunkTiles];
   __shared__ MwBad bad[kMwMaxBad];
-  __shared__ int nbad, npref;
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  __shared__ __align__(16) float xs[kMwChunk];
+  const int b = blockIdx.x, lane = threadIdx.x;
   const MwJob j = a.jobs[b];
   if (!mw_active(j, pass)) return;
   const MwElem e = mw_elem(a, b, j, pass);
   const long long rowrec = ((long long)pass * a.B + b);
-  const MwRec *crec = a.crec + rowrec * a.NC;
-  const MwRec *trec = a.trec + rowrec * a.NC * kMwNT;
-  for (int c = tid; c < a.NC; c += kMwNT) cr[c] = crec[c];
-  if (tid == 0) nbad = min(a.badcnt[rowrec], kMwMaxBad);
-  __syncthreads();
-  // the first kMwPrefetch chunks without a chunk function (the walk will
-  // descend into them), in order
-  if (tid < 64) {
-    int cnt = 0;
-    for (int base = 0; base < a.NC && cnt < kMwPrefetch; base += 64) {
-      const int c = base + lane;
-      const bool inv = c < a.NC && cr[c].e == kBad && cr[c].pad != 1;
-      const unsigned long long m = __ballot(inv);
-      const int before = __builtin_popcountll(m & ((1ull << lane) - 1ull));
-      if (inv && cnt + before < kMwPrefetch) pref[cnt + before] = c;
-      cnt += __builtin_popcountll(m);
-    }
-    if (tid == 0) npref = min(cnt, kMwPrefetch);
-  }
-  for (int q = tid; q < nbad; q += kMwNT) bad[q] = a.bad[rowrec * kMwMaxBad + q];
-  __syncthreads();
-  for (int q = 0; q < npref; ++q) tr[q][tid] = trec[(long long)pref[q] * kMwNT + tid];
-  __syncthreads();
+  const MwChunk *crec = a.crec + rowrec * a.NC;
+  const MwRec *trec = a.trec + rowrec * a.NC * kMwChunkTiles;
+  const int nbad = min(a.badcnt[rowrec], kMwMaxBad);
   const bool cdf = (pass == kPassCdf);
   const float r = j.u;
-  // Every wave runs the same walk on the same data (so the work-group can
-  // synchronise inside it); thread 0 writes the result.
-  auto serial = [&](int c, int t, float &s) -> long long {
-    const long long tile = (long long)c * kMwNT + t;
+
+  // chunk 0's values, the first window of chunk records and the cached tiles
+  {
+    float x[kMwTile];
+    mw_tile_values(a, e, lane, x);
+#pragma unroll
+    for (int k = 0; k < kMwTile; k += 4)
+      *reinterpret_cast<float4 *>(&xs[lane * kMwTile + k]) = make_float4(x[k], x[k + 1], x[k + 2], x[k + 3]);
+  }
+  for (int c = 1 + lane; c < min(a.NC, 1 + kMwWin); c += 64) cr[c - 1] = crec[c];
+  for (int q = lane; q < nbad; q += 64) bad[q] = a.bad[rowrec * kMwMaxBad + q];
+  __syncthreads();
+
+  // Serial replay of a tile's 16 values from s (CDF: first hit index).  The
+  // running value never decreases (x >= 0), so the first i with r <= s_i is
+  // searched only in a tile whose last partial sum reaches r.
+  auto replay16 = [&](const float *x, long long i0, float &s) -> long long {
+    float ps[kMwTile];
+    float acc = s;
+#pragma unroll
+    for (int k = 0; k < kMwTile; ++k) {
+      acc = acc + x[k];
+      ps[k] = acc;
+    }
+    if (cdf && r <= acc) {
+      // static indices only: a dynamically indexed ps[] would live in scratch
+      int k = kMwTile - 1;
+      float sk = ps[kMwTile - 1];
+#pragma unroll
+      for (int q = kMwTile - 2; q >= 0; --q) {
+        const bool h = r <= ps[q];
+        k = h ? q : k;
+        sk = h ? ps[q] : sk;
+      }
+      s = sk;
+      return i0 + k;
+    }
+    s = acc;
+    return -1;
+  };
+  // values of tile `tile`: the cache when the records kernel stored them
+  auto serial = [&](long long tile, float &s) -> long long {
     const int q = lane < nbad ? lane : 0;
     const unsigned long long m = __ballot(lane < nbad && bad[q].tile == (int)tile);
     float x[kMwTile];
@@ -763,42 +842,113 @@ __global__ __launch_bounds__(kMwNT) void mw_walk_kernel(Args a, int pass) {
     } else {
       mw_tile_values(a, e, tile, x);
     }
-    long long hit = -1;
-#pragma unroll
-    for (int k = 0; k < kMwTile; ++k) {
-      const float t2 = s + x[k];
-      if (hit < 0) {
-        s = t2;
-        if (cdf && r <= s) hit = tile * kMwTile + k;
-      }
-    }
-    return hit;
+    return replay16(x, tile * kMwTile, s);
   };
-  auto chunk_item = [&](int i, int &reg) -> Inc {
-    reg = cr[i].reg;
-    return Inc{cr[i].e, cr[i].o};
-  };
-  auto chunk_desc = [&](int c, float &s) -> long long {
-    int slot = kMwPrefetch;
-    for (int q = 0; q < npref; ++q)
-      if (pref[q] == c) slot = q;
-    if (slot == kMwPrefetch) {  // not staged: load now (a skipped chunk has no records)
-      __syncthreads();
-      tr[slot][tid] = (cr[c].pad == 1) ? MwRec{kBad, kBad, kAnyRegion, 1}
-                                       : trec[(long long)c * kMwNT + tid];
-      __syncthreads();
-    }
-    const MwRec *t_ = tr[slot];
-    auto tile_item = [&](int i, int &reg) -> Inc {
-      reg = t_[i].reg;
-      return Inc{t_[i].e, t_[i].o};
-    };
-    auto tile_desc = [&](int t, float &ss) -> long long { return serial(c, t, ss); };
-    return walk(kMwNT, s, cdf, r, tile_item, tile_desc);
-  };
+
   float s = 0.0f;
-  const long long found = walk(a.NC, s, cdf, r, chunk_item, chunk_desc);
-  if (tid == 0) {
+  long long found = -1;
+  // chunk 0, serially (all lanes redundantly); the next tile's values are
+  // read from LDS while this tile's adds run
+  {
+    float4 cur[4], nxt[4];
+    const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cur[k] = x4[k];
+    for (int t = 0; t < kMwChunkTiles && found < 0; ++t) {
+      const int tn = (t + 1 < kMwChunkTiles) ? t + 1 : t;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) nxt[k] = x4[tn * 4 + k];
+      float x[kMwTile];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        x[4 * k] = cur[k].x;
+        x[4 * k + 1] = cur[k].y;
+        x[4 * k + 2] = cur[k].z;
+        x[4 * k + 3] = cur[k].w;
+      }
+      found = replay16(x, (long long)t * kMwTile, s);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) cur[k] = nxt[k];
+    }
+  }
+
+  // tile-level walk of chunk c from its tile t0 (records from memory)
+  auto tile_walk = [&](int c, int t0, float &ss) -> long long {
+    __syncthreads();
+    tr[lane] = trec[(long long)c * kMwChunkTiles + lane];
+    __syncthreads();
+    auto tile_item = [&](int i, int &reg) -> Inc {
+      const MwRec q = tr[t0 + i];
+      reg = q.reg;
+      return q.pad ? Inc{kBad, kBad} : Inc{q.e, q.o};
+    };
+    auto tile_desc = [&](int i, float &s2) -> long long {
+      return serial((long long)c * kMwChunkTiles + t0 + i, s2);
+    };
+    return walk(kMwChunkTiles - t0, ss, cdf, r, tile_item, tile_desc);
+  };
+  // whole chunk c from memory values, serially (a skipped chunk reached anyway)
+  auto chunk_serial = [&](int c, float &ss) -> long long {
+    for (int t = 0; t < kMwChunkTiles; ++t) {
+      const long long h = serial((long long)c * kMwChunkTiles + t, ss);
+      if (h >= 0) return h;
+    }
+    return -1;
+  };
+  // apply run function F (region reg) from ss if valid and not hit; returns
+  // false when the run has to be walked tile by tile instead
+  auto apply_run = [&](uint32_t fe, uint32_t fo, int reg, float &ss) -> bool {
+    const int rs = region_of(ss);
+    if (!(reg == rs || reg == kAnyRegion)) return false;
+    const uint32_t a0 = units_of(ss, rs);
+    const uint32_t inc = inc_at(Inc{fe, fo}, a0);
+    if (a0 + inc > kUnitsTop) return false;
+    const float v = value_of(a0 + inc, rs);
+    if (cdf && r <= v) return false;
+    ss = v;
+    return true;
+  };
+
+  for (int w0 = 1; w0 < a.NC && found < 0; w0 += kMwWin) {
+    const int cnt = min(kMwWin, a.NC - w0);
+    if (w0 > 1) {
+      __syncthreads();
+      for (int c = lane; c < cnt; c += 64) cr[c] = crec[w0 + c];
+      __syncthreads();
+    }
+    auto chunk_item = [&](int i, int &reg) -> Inc {
+      const MwChunk q = cr[i];
+      reg = q.reg0;
+      return (q.status == kChunkOk && q.brk < 0) ? Inc{q.e0, q.o0} : Inc{kBad, kBad};
+    };
+    auto chunk_desc = [&](int i, float &ss) -> long long {
+      const MwChunk q = cr[i];
+      const int c = w0 + i;
+      if (q.status == kChunkSkipped) return chunk_serial(c, ss);
+      if (q.status != kChunkOk || q.brk < 0) return tile_walk(c, 0, ss);
+      const float s0 = ss;
+      if (q.brk > 0 && !apply_run(q.e0, q.o0, q.reg0, ss)) {
+        ss = s0;
+        return tile_walk(c, 0, ss);
+      }
+      int t1 = q.brk;
+      if (q.brk_serial) {
+        const long long h = serial((long long)c * kMwChunkTiles + q.brk, ss);
+        if (h >= 0) return h;
+        ++t1;
+      }
+      if (t1 < kMwChunkTiles) {
+        const float s1 = ss;
+        if (!apply_run(q.e1, q.o1, q.reg1, ss)) {
+          ss = s1;
+          return tile_walk(c, t1, ss);
+        }
+      }
+      return -1;
+    };
+    found = walk(cnt, s, cdf, r, chunk_item, chunk_desc);
+  }
+  if (lane == 0) {
     if (!cdf) {
       a.res[b].S = s;
       a.res[b].fallback = (s <= 1e-6f) ? 1 : 0;  // speculative.cpp:37
@@ -907,8 +1057,8 @@ static WsLayout ws_layout(int B, int K, int V, int mode) {
   L.res = take((size_t)B * sizeof(MwRes));
   L.csum_x = take(mw ? (size_t)B * NC * sizeof(float) : 0);
   L.csum_t = take(mw ? (size_t)B * NC * sizeof(float) : 0);
-  L.crec = take(mw ? 2 * (size_t)B * NC * sizeof(MwRec) : 0);
-  L.trec = take(mw ? 2 * (size_t)B * NC * kMwNT * sizeof(MwRec) : 0);
+  L.crec = take(mw ? 2 * (size_t)B * NC * sizeof(MwChunk) : 0);
+  L.trec = take(mw ? 2 * (size_t)B * NC * kMwChunkTiles * sizeof(MwRec) : 0);
   L.badcnt = take(2 * (size_t)B * sizeof(int));
   L.bad = take(mw ? 2 * (size_t)B * kMwMaxBad * sizeof(MwBad) : 0);
   L.total = o;
@@ -1003,7 +1153,7 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
   a.res = (MwRes *)(ws + L.res);
   a.csum_x = (float *)(ws + L.csum_x);
   a.csum_t = (float *)(ws + L.csum_t);
-  a.crec = (MwRec *)(ws + L.crec);
+  a.crec = (MwChunk *)(ws + L.crec);
   a.trec = (MwRec *)(ws + L.trec);
   a.badcnt = (int *)(ws + L.badcnt);
   a.bad = (MwBad *)(ws + L.bad);
@@ -1019,13 +1169,13 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
     CFA_LAUNCH("chain_argmax", (argmax_kernel<256>), dim3(a.G), dim3(256), 0, st, a);
   CFA_LAUNCH("chain_decide", decide_kernel, dim3(B), dim3(64), 0, st, a);
   if (mode != CFA_MODE_GREEDY) {
-    const dim3 cg(a.NC, B);
+    const dim3 cg((a.NC + kMwNT / 64 - 1) / (kMwNT / 64), B);
     CFA_LAUNCH("chain_plan", plan_kernel, dim3(1), dim3(256), 0, st, a);
     CFA_LAUNCH("chain_mw_sums", mw_sums_kernel, cg, dim3(kMwNT), 0, st, a);
     CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassSum);
-    CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(kMwNT), 0, st, a, (int)kPassSum);
+    CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassSum);
     CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassCdf);
-    CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(kMwNT), 0, st, a, (int)kPassCdf);
+    CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassCdf);
     if (mode == CFA_MODE_PYTHON)
       CFA_LAUNCH("chain_pybonus", pybonus_kernel, dim3(B), dim3(kSampleNT), 0, st, a);
     CFA_LAUNCH("chain_finish", finish_kernel, dim3((B + 63) / 64), dim3(64), 0, st, a);
