@@ -34,9 +34,10 @@ SIGMA, NOISE = 2.0, 0.5
 NSETS = 4
 # algorithmic bytes of one step: target [B,K+1,V] + draft [B,K,V] logits, read once
 ALG_BYTES = B * (2 * K + 1) * V * 4
-# HBM bytes per chain_stats launch measured with rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE, scaled by a plain-copy calibration (profiles/hbm_traffic_per_dispatch.md)
-STATS_TRAFFIC_BYTES = 562_217_848
+# HBM bytes per chain_stats launch: reads from rocprofv3 --pmc TCC_EA0_RDREQ_{32B,64B,128B}
+# (request-size weighted, exact on a plain copy) plus WRITE_SIZE
+# (profiles/hbm_traffic_per_dispatch.md)
+STATS_TRAFFIC_BYTES = 576_649_216
 
 
 def make_inputs(dev, seed):
