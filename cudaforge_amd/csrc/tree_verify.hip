@@ -118,14 +118,44 @@ __device__ float2 row_stats(const Args &a, const float *row, Smem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float c = a.c;
   float m = -INFINITY, s = 0.0f;
-  for (int i = tid; i < a.V; i += kNT) {
-    const float v = row[i];
-    if (v > m) {
-      s *= __builtin_amdgcn_exp2f((m - v) * c);
-      m = v;
+  // one online update per group of four values: rescale once per new maximum
+  auto update = [&](float v0, float v1, float v2, float v3) {
+    const float mx = fmaxf(fmaxf(v0, v1), fmaxf(v2, v3));
+    if (mx > m) {
+      s *= __builtin_amdgcn_exp2f((m - mx) * c);
+      m = mx;
     }
     const float ms = (m == -INFINITY) ? 0.0f : m;
-    s += __builtin_amdgcn_exp2f((v - ms) * c);
+    s += __builtin_amdgcn_exp2f((v0 - ms) * c) + __builtin_amdgcn_exp2f((v1 - ms) * c) +
+         __builtin_amdgcn_exp2f((v2 - ms) * c) + __builtin_amdgcn_exp2f((v3 - ms) * c);
+  };
+  if (a.vec) {
+    // 16-byte loads, four in flight per thread
+    const float4 *p4 = reinterpret_cast<const float4 *>(row);
+    const int n4 = a.V / 4;
+    constexpr int U = 4;
+    int i = tid;
+    for (; i + (U - 1) * kNT < n4; i += U * kNT) {
+      float4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = p4[i + u * kNT];
+#pragma unroll
+      for (int u = 0; u < U; ++u) update(v[u].x, v[u].y, v[u].z, v[u].w);
+    }
+    for (; i < n4; i += kNT) {
+      const float4 v = p4[i];
+      update(v.x, v.y, v.z, v.w);
+    }
+  } else {
+    for (int i = tid; i < a.V; i += kNT) {
+      const float v = row[i];
+      if (v > m) {
+        s *= __builtin_amdgcn_exp2f((m - v) * c);
+        m = v;
+      }
+      const float ms = (m == -INFINITY) ? 0.0f : m;
+      s += __builtin_amdgcn_exp2f((v - ms) * c);
+    }
   }
   auto merge = [c](float &m1, float &s1, float m2, float s2) {
     const float M = fmaxf(m1, m2);
@@ -390,6 +420,10 @@ extern "C" int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t 
   a.out_status = out_status;
   a.probs_t = out_target_probs;
   a.probs_d = greedy ? nullptr : out_draft_probs;
+  // 16-byte vector loads need every row 16-byte aligned
+  a.vec = (V % 4 == 0) && (t_stride_b % 4 == 0) && (t_stride_n % 4 == 0) &&
+          (((uintptr_t)target & 15) == 0) &&
+          (greedy || ((d_stride_b % 4 == 0) && (d_stride_n % 4 == 0) && (((uintptr_t)draft & 15) == 0)));
   CFA_LAUNCH("tree_verify", treev::tree_verify_kernel, dim3(B), dim3(treev::kNT), 0,
              (hipStream_t)stream, a);
   return CFA_OK;
