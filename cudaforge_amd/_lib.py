@@ -6,7 +6,10 @@ every entry point raises ``RuntimeError`` naming the build command.
 
 Error mapping follows the reference's pybind layer: a C-ABI ``CFA_ERR_ARG`` is
 the ``std::invalid_argument`` of ``csrc/src/scheduler/speculative.cpp:58-62``
-and surfaces as ``ValueError``; ``CFA_ERR_HIP`` surfaces as ``RuntimeError``.
+and surfaces as ``ValueError``; ``CFA_ERR_RANGE`` is a ``std::out_of_range``
+(``IndexError``); ``CFA_ERR_OUT_OF_PAGES`` is the reference's
+``OutOfPagesException`` (a ``RuntimeError``); ``CFA_ERR_STATE`` (a
+``std::runtime_error``) and ``CFA_ERR_HIP`` surface as ``RuntimeError``.
 """
 from __future__ import annotations
 
@@ -19,6 +22,9 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcfa.so")
 CFA_OK = 0
 CFA_ERR_ARG = -1
 CFA_ERR_HIP = -2
+CFA_ERR_STATE = -3
+CFA_ERR_RANGE = -4
+CFA_ERR_OUT_OF_PAGES = -5
 
 CFA_INPUT_PROBS = 0
 CFA_INPUT_LOGITS = 1
@@ -38,6 +44,54 @@ _i32p = ctypes.POINTER(ctypes.c_int32)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _dp = ctypes.POINTER(ctypes.c_double)
 _ip = ctypes.POINTER(ctypes.c_int)
+
+_u32 = ctypes.c_uint32
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+class KVCacheConfigC(ctypes.Structure):
+    """cfa_kv_cache_config."""
+
+    _fields_ = [
+        ("num_layers", ctypes.c_uint32),
+        ("num_kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("block_size", ctypes.c_uint32),
+        ("element_size_bytes", ctypes.c_uint64),
+        ("total_gpu_blocks", ctypes.c_uint64),
+        ("enable_prefix_caching", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+        ("max_supported_batch_size", ctypes.c_uint64),
+        ("max_blocks_per_sequence", ctypes.c_uint64),
+    ]
+
+
+class KVCacheStatsC(ctypes.Structure):
+    """cfa_kv_cache_stats."""
+
+    _fields_ = [
+        ("total_blocks", ctypes.c_uint64),
+        ("free_blocks", ctypes.c_uint64),
+        ("allocated_blocks", ctypes.c_uint64),
+        ("cached_prefix_blocks", ctypes.c_uint64),
+        ("total_memory_bytes", ctypes.c_uint64),
+        ("used_memory_bytes", ctypes.c_uint64),
+        ("pool_utilization_ratio", ctypes.c_double),
+        ("active_sequences_count", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+        ("prefix_cache_hits", ctypes.c_uint64),
+        ("prefix_cache_misses", ctypes.c_uint64),
+        ("lru_evictions_count", ctypes.c_uint64),
+    ]
+
+
+class KVPageCopyC(ctypes.Structure):
+    """cfa_kv_page_copy."""
+
+    _fields_ = [("src_block", ctypes.c_int32), ("dst_block", ctypes.c_int32),
+                ("n_slots", ctypes.c_int32)]
+
 
 # name -> (restype, argtypes); every symbol the header declares.
 SIGNATURES: dict[str, tuple] = {
@@ -64,6 +118,20 @@ SIGNATURES: dict[str, tuple] = {
         _i,
         [_p, _p, _p, _i, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p],
     ),
+    "cfa_kv_cache_create": (_i, [ctypes.POINTER(KVCacheConfigC), ctypes.POINTER(_p)]),
+    "cfa_kv_cache_destroy": (None, [_p]),
+    "cfa_kv_cache_register_sequence": (_i, [_p, _u64, _i32p, _i64, _u32p]),
+    "cfa_kv_cache_append_tokens": (_i, [_p, _u64, _u32]),
+    "cfa_kv_cache_unregister_sequence": (_i, [_p, _u64]),
+    "cfa_kv_cache_fork_sequence": (_i, [_p, _u64, _u64]),
+    "cfa_kv_cache_truncate_sequence": (_i, [_p, _u64, _u32]),
+    "cfa_kv_cache_context_length": (_i, [_p, _u64, _u32p]),
+    "cfa_kv_cache_get_block_table": (_i, [_p, _u64, _i32p, _i64, _i64p]),
+    "cfa_kv_cache_prepare_batch": (
+        _i, [_p, ctypes.POINTER(_u64), _i, _p, _p, _i64, _p, _p, _i64, _i32p, _p]),
+    "cfa_kv_cache_get_stats": (_i, [_p, ctypes.POINTER(KVCacheStatsC)]),
+    "cfa_kv_cache_pop_page_copies": (_i, [_p, ctypes.POINTER(KVPageCopyC), _i64, _i64p]),
+    "cfa_kv_cache_block_info": (_i, [_p, _i32, _u32p, _u32p, _i32p]),
     "cfa_rng_create": (_p, [_u64]),
     "cfa_rng_destroy": (None, [_p]),
     "cfa_rng_peek": (_i, [_p, _i, _f32p]),
@@ -109,7 +177,16 @@ def check(rc: int, what: str) -> None:
     msg = f"{what}: {last_error()}"
     if rc == CFA_ERR_ARG:
         raise ValueError(msg)
+    if rc == CFA_ERR_RANGE:
+        raise IndexError(msg)
+    if rc == CFA_ERR_OUT_OF_PAGES:
+        raise OutOfPagesException(msg)
     raise RuntimeError(msg)
+
+
+class OutOfPagesException(RuntimeError):
+    """No free or evictable KV page (paged_kv_cache.h:31-34, raised at
+    paged_kv_cache.cpp:126-135)."""
 
 
 def profile_enable(on: bool) -> None:

@@ -21,6 +21,11 @@ int fail_arg(const char *msg) {
   return CFA_ERR_ARG;
 }
 
+int fail_code(int code, const char *msg) {
+  g_last_error = msg;
+  return code;
+}
+
 int fail_hip(hipError_t e, const char *where) {
   g_last_error = std::string(where) + ": " + hipGetErrorString(e);
   return CFA_ERR_HIP;

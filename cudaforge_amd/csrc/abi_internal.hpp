@@ -13,6 +13,7 @@ namespace abi {
 void clear_error();
 int fail_arg(const char *msg);
 int fail_hip(hipError_t e, const char *where);
+int fail_code(int code, const char *msg);
 int device_cu_count();
 
 }  // namespace abi

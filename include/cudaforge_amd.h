@@ -20,6 +20,8 @@
  *   csrc/bindings/pybind_module.cpp:196-239    SpeculativeEngine (C++)
  *   csrc/include/cudaforge/memory/paged_kv_cache.h:81-94
  *                                              KVCacheBatchDescriptor layout
+ *   csrc/include/cudaforge/memory/paged_kv_cache.h:36-179, bound at
+ *   csrc/bindings/pybind_module.cpp:20-99      PagedKVCache (host page tables)
  */
 #ifndef CUDAFORGE_AMD_H
 #define CUDAFORGE_AMD_H
@@ -34,6 +36,9 @@ extern "C" {
 #define CFA_OK 0
 #define CFA_ERR_ARG (-1)
 #define CFA_ERR_HIP (-2)
+#define CFA_ERR_STATE (-3)        /* std::runtime_error in the reference */
+#define CFA_ERR_RANGE (-4)        /* std::out_of_range in the reference */
+#define CFA_ERR_OUT_OF_PAGES (-5) /* OutOfPagesException (paged_kv_cache.h:31-34) */
 
 /* input_kind */
 #define CFA_INPUT_PROBS 0  /* rows are probabilities (the C++ engine's input) */
@@ -186,6 +191,126 @@ int cfa_kv_commit(void *k_pool, void *v_pool, const int32_t *block_tables,
                   int path_stride, const int32_t *path_lens, int B, int num_blocks,
                   int num_layers, int n_kv_heads, int block_size, int head_dim, int elem_bytes,
                   int32_t *new_ctx_lens, int32_t *status, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged KV cache page tables (host metadata).
+ *
+ * Replaces the metadata half of PagedKVCache (paged_kv_cache.h:36-179,
+ * paged_kv_cache.cpp:10-445; pybind names at pybind_module.cpp:20-99): page
+ * reference counts and fill counts, the LIFO free list (the first page handed
+ * out is page 0), prefix sharing of full prompt pages through chained block
+ * hashes (paged_kv_cache.cpp:80-88), LRU retention and eviction of released
+ * prefix pages, fork, and the per-batch staging of block tables and context
+ * lengths for the kernels.  The K/V pools, the pinned host staging buffers and
+ * the device block tables are the caller's: this library allocates no device
+ * or pinned memory.  All calls on one cache are serialised by its lock.
+ * Errors: CFA_ERR_STATE for an unknown sequence id (std::runtime_error in the
+ * reference), CFA_ERR_RANGE for batch/table limits (std::out_of_range),
+ * CFA_ERR_OUT_OF_PAGES when no page is free or evictable.
+ */
+typedef struct cfa_kv_cache cfa_kv_cache;
+
+/* KVCacheConfig (paged_kv_cache.h:36-46), same fields and meaning. */
+typedef struct cfa_kv_cache_config {
+  uint32_t num_layers;
+  uint32_t num_kv_heads;
+  uint32_t head_dim;
+  uint32_t block_size;
+  uint64_t element_size_bytes;
+  uint64_t total_gpu_blocks;
+  uint32_t enable_prefix_caching; /* bool */
+  uint32_t reserved;
+  uint64_t max_supported_batch_size;
+  uint64_t max_blocks_per_sequence;
+} cfa_kv_cache_config;
+
+/* KVCacheStats (paged_kv_cache.h:63-75), same fields and formulas
+ * (paged_kv_cache.cpp:423-445). */
+typedef struct cfa_kv_cache_stats {
+  uint64_t total_blocks;
+  uint64_t free_blocks;
+  uint64_t allocated_blocks;
+  uint64_t cached_prefix_blocks;
+  uint64_t total_memory_bytes;
+  uint64_t used_memory_bytes;
+  double pool_utilization_ratio;
+  uint32_t active_sequences_count;
+  uint32_t reserved;
+  uint64_t prefix_cache_hits;
+  uint64_t prefix_cache_misses;
+  uint64_t lru_evictions_count;
+} cfa_kv_cache_stats;
+
+/* PagedKVCache::PagedKVCache / ~PagedKVCache (paged_kv_cache.cpp:9-78),
+ * metadata only. */
+int cfa_kv_cache_create(const cfa_kv_cache_config *config, cfa_kv_cache **out);
+void cfa_kv_cache_destroy(cfa_kv_cache *cache);
+
+/* register_sequence_with_prefix (paged_kv_cache.cpp:167-253): reuses the
+ * cached pages of the longest matching run of full prompt pages, allocates the
+ * rest; *matched_tokens = tokens served from the prefix cache.  A sequence id
+ * already registered is left as it is (matched 0). */
+int cfa_kv_cache_register_sequence(cfa_kv_cache *cache, uint64_t sequence_id,
+                                   const int32_t *prompt_tokens, int64_t n_tokens,
+                                   uint32_t *matched_tokens);
+/* append_tokens (paged_kv_cache.cpp:255-286). */
+int cfa_kv_cache_append_tokens(cfa_kv_cache *cache, uint64_t sequence_id, uint32_t num_tokens);
+/* unregister_sequence (paged_kv_cache.cpp:288-299); unknown ids are ignored. */
+int cfa_kv_cache_unregister_sequence(cfa_kv_cache *cache, uint64_t sequence_id);
+/* fork_sequence (paged_kv_cache.cpp:301-316).  An already registered child
+ * releases its own pages first; parent == child is CFA_ERR_ARG.  Parent and
+ * child share every page; the first append (or truncate) that would change a
+ * shared, partly filled page gives the changing sequence a private copy and
+ * queues the device copy of its slots (see cfa_kv_cache_pop_page_copies).
+ * The reference shares the page for writing (paged_kv_cache.cpp:265-271). */
+int cfa_kv_cache_fork_sequence(cfa_kv_cache *cache, uint64_t parent_sequence_id,
+                               uint64_t child_sequence_id);
+/* Rollback (no counterpart in the reference, which only grows sequences):
+ * keep the first new_length tokens, release the pages past them (at least one
+ * page stays).  Cutting inside a page that another sequence shares copies the
+ * kept part to a private page (queued as for append); cutting inside a
+ * private prefix page drops its prefix entry.  new_length above the current
+ * length is CFA_ERR_ARG. */
+int cfa_kv_cache_truncate_sequence(cfa_kv_cache *cache, uint64_t sequence_id, uint32_t new_length);
+/* (pages - 1) * block_size + fill of the last page (paged_kv_cache.cpp:359-364). */
+int cfa_kv_cache_context_length(cfa_kv_cache *cache, uint64_t sequence_id, uint32_t *length);
+/* get_block_table (paged_kv_cache.cpp:398-407): *n_blocks = table length;
+ * min(capacity, length) ids are copied to out (out may be NULL). */
+int cfa_kv_cache_get_block_table(cfa_kv_cache *cache, uint64_t sequence_id, int32_t *out,
+                                 int64_t capacity, int64_t *n_blocks);
+/* prepare_batch_metadata (paged_kv_cache.cpp:318-396): writes the
+ * [batch, max_blocks] block tables (-1 padded) and the context lengths into
+ * the caller's host buffers (pinned for an asynchronous copy), then, when the
+ * device buffers are given, enqueues both host-to-device copies on `stream`.
+ * The host buffers must stay untouched until that copy has run.
+ * *max_blocks_out = the batch's longest table (the descriptor's
+ * max_blocks_per_seq).  Capacities are in int32 elements. */
+int cfa_kv_cache_prepare_batch(cfa_kv_cache *cache, const uint64_t *sequence_ids, int batch_size,
+                               int32_t *host_block_tables, int32_t *host_context_lens,
+                               int64_t host_capacity, int32_t *dev_block_tables,
+                               int32_t *dev_context_lens, int64_t dev_capacity,
+                               int32_t *max_blocks_out, void *stream);
+/* get_stats (paged_kv_cache.cpp:423-445). */
+int cfa_kv_cache_get_stats(cfa_kv_cache *cache, cfa_kv_cache_stats *out);
+/* Copy on write: a queued copy of slots [0, n_slots) of page src_block to
+ * page dst_block, for every layer and KV head of both pools.  The caller runs
+ * these copies (in order, before any write to dst_block) after each append or
+ * truncate; no counterpart in the reference. */
+typedef struct cfa_kv_page_copy {
+  int32_t src_block;
+  int32_t dst_block;
+  int32_t n_slots;
+} cfa_kv_page_copy;
+
+/* Moves up to `capacity` queued copies, oldest first, into out and sets
+ * *count to how many; with out == NULL or capacity <= 0 only reports the
+ * number pending. */
+int cfa_kv_cache_pop_page_copies(cfa_kv_cache *cache, cfa_kv_page_copy *out, int64_t capacity,
+                                 int64_t *count);
+/* Reference count, fill and LRU membership of one page (the reference's
+ * PhysicalBlock fields, paged_kv_cache.h:48-55); for tests and monitoring. */
+int cfa_kv_cache_block_info(cfa_kv_cache *cache, int32_t block_id, uint32_t *ref_count,
+                            uint32_t *tokens_filled, int32_t *is_cached);
 
 /* ---------------------------------------------------------------------------
  * Host uniform stream of the compatibility engine.
