@@ -33,6 +33,10 @@ CFA_MODE_CPP = 0
 CFA_MODE_PYTHON = 1
 CFA_MODE_GREEDY = 2
 
+CFA_SAMPLE_MULTINOMIAL = 0
+CFA_SAMPLE_FILTERED = 1
+CFA_SAMPLE_GREEDY = 2
+
 _i = ctypes.c_int
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -103,6 +107,9 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _i64, _p, _i64, _i64, _i, _p, _p, _i, _i, _i, _f, _f, _i, _i32,
          _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p],
     ),
+    "cfa_sample_workspace_size": (_sz, [_i, _i, _i, _i]),
+    "cfa_sample": (
+        _i, [_p, _i64, _i, _i, _i, _i, _f, _i, _f, _i, _p, _p, _p, _p, _sz, _p]),
     "cfa_tree_attention_workspace_size": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "cfa_tree_attention": (
         _i,

@@ -78,11 +78,14 @@ struct Args {
   const int32_t *tokens;  // [B,K]
   const float *U;         // [B,K+1]
   int B, K, V, rpb;       // rows per sequence: K+1 (greedy) or 2K+1
+  int draws;              // jobs per input row (sequence b reads row b / draws)
+  int R;                  // distinct rows: (B / draws) * rpb
   float c;                // log2(e) / temperature
   int logits;             // 1: inputs are logits
   int mode;               // CFA_MODE_*
   int eos;
   float top_p;
+  int top_k;              // > 0: keep only probabilities >= the top_k-th largest
   // partition of the stats / argmax passes
   long long Vw;  // row length in vector units
   long long C;   // units per work-group
@@ -104,9 +107,14 @@ struct Args {
   int32_t *out_accept_len, *out_tokens, *out_num_emitted, *out_final, *out_eos;
 };
 
+// Row j of input row group ub (a sequence's K+1 target rows, then its K draft rows).
+__device__ __forceinline__ const float *row_ptr_u(const Args &a, int ub, int j) {
+  return j <= a.K ? a.tgt + (long long)ub * a.t_sb + (long long)j * a.t_sk
+                  : a.drf + (long long)ub * a.d_sb + (long long)(j - a.K - 1) * a.d_sk;
+}
+// Row j of job b.
 __device__ __forceinline__ const float *row_ptr(const Args &a, int b, int j) {
-  return j <= a.K ? a.tgt + (long long)b * a.t_sb + (long long)j * a.t_sk
-                  : a.drf + (long long)b * a.d_sb + (long long)(j - a.K - 1) * a.d_sk;
+  return row_ptr_u(a, b / a.draws, j);
 }
 
 // (max, 1/S) of row r from the stats partials, combined in a fixed order.
@@ -127,20 +135,21 @@ __device__ float2 row_stat(const Args &a, int r) {
   return make_float2(M, 1.0f / S);
 }
 
-__device__ Dist make_dist(const Args &a, int b, int j) {
+__device__ Dist make_dist_u(const Args &a, int ub, int j) {
   Dist d;
-  d.p = row_ptr(a, b, j);
+  d.p = row_ptr_u(a, ub, j);
   d.c = a.c;
   d.logits = a.logits;
   d.M = 0.0f;
   d.invS = 1.0f;
   if (a.logits) {
-    const float2 st = row_stat(a, b * a.rpb + j);
+    const float2 st = row_stat(a, ub * a.rpb + j);
     d.M = st.x;
     d.invS = st.y;
   }
   return d;
 }
+__device__ Dist make_dist(const Args &a, int b, int j) { return make_dist_u(a, b / a.draws, j); }
 
 // ---------------------------------------------------------------------------
 // stats: online (max, sum exp2) over a balanced slice of the row space.
@@ -184,7 +193,7 @@ __device__ __forceinline__ float4 ld_stream4(const float4 *p) {
 
 template <int NT, int W>
 __global__ __launch_bounds__(NT) void stats_kernel(Args a) {
-  const long long total = (long long)a.B * a.rpb * a.Vw;
+  const long long total = (long long)a.R * a.Vw;
   const long long lo = (long long)blockIdx.x * a.C;
   const long long hi = min(lo + a.C, total);
   if (lo >= hi) return;
@@ -193,7 +202,7 @@ __global__ __launch_bounds__(NT) void stats_kernel(Args a) {
   for (long long r = lo / a.Vw; r * a.Vw < hi; ++r, ++slot) {
     const long long s0 = max(lo, r * a.Vw) - r * a.Vw;
     const long long s1 = min(hi, (r + 1) * a.Vw) - r * a.Vw;
-    const float *row = row_ptr(a, (int)(r / a.rpb), (int)(r % a.rpb));
+    const float *row = row_ptr_u(a, (int)(r / a.rpb), (int)(r % a.rpb));
     float m = -INFINITY, s = 0.0f;
     if (W == 4) {
       const float4 *p4 = reinterpret_cast<const float4 *>(row);
@@ -255,7 +264,7 @@ __device__ __forceinline__ void am_merge(float &v, int &i, float v2, int i2) {
 
 template <int NT>
 __global__ __launch_bounds__(NT) void argmax_kernel(Args a) {
-  const long long total = (long long)a.B * a.rpb * a.Vw;
+  const long long total = (long long)a.R * a.Vw;
   const long long lo = (long long)blockIdx.x * a.C;
   const long long hi = min(lo + a.C, total);
   if (lo >= hi) return;
@@ -265,7 +274,7 @@ __global__ __launch_bounds__(NT) void argmax_kernel(Args a) {
   for (long long r = lo / a.Vw; r * a.Vw < hi; ++r, ++slot) {
     const long long e0 = (max(lo, r * a.Vw) - r * a.Vw) * W;
     const long long e1 = (min(hi, (r + 1) * a.Vw) - r * a.Vw) * W;
-    const Dist d = make_dist(a, (int)(r / a.rpb), (int)(r % a.rpb));
+    const Dist d = make_dist_u(a, (int)(r / a.rpb), (int)(r % a.rpb));
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     for (long long i = e0 + threadIdx.x; i < e1; i += NT) am_merge(bv, bi, d(i), (int)i);
@@ -325,7 +334,7 @@ __global__ __launch_bounds__(64) void decide_kernel(Args a) {
     }
   }
   if (a.mode == CFA_MODE_GREEDY)
-    for (int i = lane; i <= K; i += 64) am[i] = row_argmax(a, b * a.rpb + i);
+    for (int i = lane; i <= K; i += 64) am[i] = row_argmax(a, (b / a.draws) * a.rpb + i);
   __syncthreads();
   if (lane != 0) return;
   const float *U = a.U + (long long)b * (K + 1);
@@ -466,6 +475,24 @@ __device__ float topp_threshold(const Dist &t, int V, float top_p, double *red) 
   return u2f(hi);
 }
 
+// The top_k-th largest probability (ties kept): the least v with
+// #{p_i > v} < top_k, found by bisection on the fp32 bits.
+template <int NT>
+__device__ float topk_threshold(const Dist &t, int V, int top_k, double *red) {
+  uint32_t lo = 0, hi = 0x7f800000u;
+  while (hi - lo > 1) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    const float tau = u2f(mid);
+    double cnt = 0.0;
+    for (int i = threadIdx.x; i < V; i += NT) cnt += (t(i) > tau) ? 1.0 : 0.0;
+    if (block_sum_f64<NT>(cnt, red) < (double)top_k)
+      hi = mid;
+    else
+      lo = mid;
+  }
+  return u2f(hi);
+}
+
 // ---------------------------------------------------------------------------
 // plan: the draw each sequence still needs (python mode applies the batch
 // lock-step rule n = min_b n_b of speculative.py:166 here).
@@ -501,11 +528,11 @@ __global__ __launch_bounds__(256) void plan_kernel(Args a) {
     j.tM = j.dM = 0.0f;
     j.tInvS = j.dInvS = 1.0f;
     if (a.logits && (j.kind == kResid || j.kind == kPlain)) {
-      const float2 ts = row_stat(a, b * a.rpb + j.row);
+      const float2 ts = row_stat(a, (b / a.draws) * a.rpb + j.row);
       j.tM = ts.x;
       j.tInvS = ts.y;
       if (j.kind == kResid) {
-        const float2 ds = row_stat(a, b * a.rpb + K + 1 + j.row);
+        const float2 ds = row_stat(a, (b / a.draws) * a.rpb + K + 1 + j.row);
         j.dM = ds.x;
         j.dInvS = ds.y;
       }
@@ -973,7 +1000,8 @@ __global__ __launch_bounds__(kSampleNT) void pybonus_kernel(Args a) {
   if (j.kind != kPyBonus) return;
   const Dist t = make_dist(a, b, j.row);
   long long idx = -1;
-  const float vstar = (a.top_p < 1.0f) ? topp_threshold<kSampleNT>(t, V, a.top_p, red) : 0.0f;
+  float vstar = (a.top_p < 1.0f) ? topp_threshold<kSampleNT>(t, V, a.top_p, red) : 0.0f;
+  if (a.top_k > 0 && a.top_k < V) vstar = fmaxf(vstar, topk_threshold<kSampleNT>(t, V, a.top_k, red));
   const float S = seq::run<kSampleNT>(XKeep{t, vstar}, V, false, 0.0f, sh, nullptr);
   if (S > 0.0f)
     seq::run<kSampleNT>(XKeepNorm{t, vstar, S}, V, true, j.u, sh, &idx);
@@ -1014,9 +1042,109 @@ __global__ __launch_bounds__(256) void probs_out_kernel(Args a, float *out_t, fl
   float *dst = (j <= a.K) ? out_t + ((long long)b * (a.K + 1) + j) * a.V
                           : out_d + ((long long)b * a.K + (j - a.K - 1)) * a.V;
   if ((j <= a.K && !out_t) || (j > a.K && !out_d)) return;
-  const Dist d = make_dist(a, b, j);
+  const Dist d = make_dist_u(a, b, j);
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < a.V; i += (long long)gridDim.x * 256)
     dst[i] = d(i);
+}
+
+// ---------------------------------------------------------------------------
+// Greedy top-k of raw rows (k <= kTopKMax): the k largest values, largest
+// first, equal values by lower index (sampling.h:107-135 for k = 1).
+// Pass 1: grid (splits, rows), each work-group the top-k of its slice;
+// pass 2: one thread per row merges the splits' lists.
+// ---------------------------------------------------------------------------
+
+constexpr int kTopKMax = 8;
+
+__device__ __forceinline__ bool tk_better(float v, int i, float w, int j) {
+  return v > w || (v == w && i < j);
+}
+
+template <int K>
+__device__ __forceinline__ void tk_insert(float (&v)[K], int (&ix)[K], float x, int i) {
+  if (!tk_better(x, i, v[K - 1], ix[K - 1])) return;
+#pragma unroll
+  for (int s = K - 1; s >= 0; --s) {
+    const bool shift = (s > 0) && tk_better(x, i, v[s - 1], ix[s - 1]);
+    if (shift) {
+      v[s] = v[s - 1];
+      ix[s] = ix[s - 1];
+    } else {
+      v[s] = x;
+      ix[s] = i;
+      break;
+    }
+  }
+}
+
+struct TopKArgs {
+  const float *x;
+  long long stride;
+  int R, V, k, splits;
+  long long per_split;
+  float2 *part;  // [R, splits, k] (value, index as bits)
+  int32_t *out;  // [R, k]
+};
+
+template <int NT>
+__global__ __launch_bounds__(NT) void topk_partial_kernel(TopKArgs a) {
+  __shared__ float sv[NT * kTopKMax];
+  __shared__ int si[NT * kTopKMax];
+  const int r = blockIdx.y, sp = blockIdx.x;
+  const float *row = a.x + (long long)r * a.stride;
+  const long long e0 = (long long)sp * a.per_split;
+  const long long e1 = min((long long)a.V, e0 + a.per_split);
+  float v[kTopKMax];
+  int ix[kTopKMax];
+#pragma unroll
+  for (int q = 0; q < kTopKMax; ++q) {
+    v[q] = -INFINITY;
+    ix[q] = 0x7fffffff;
+  }
+  for (long long i = e0 + threadIdx.x; i < e1; i += NT) {
+    const float x = __builtin_nontemporal_load(row + i);
+    if (x == x) tk_insert<kTopKMax>(v, ix, x, (int)i);  // NaN never ranks
+  }
+  // tree merge of the threads' lists through LDS
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int q = 0; q < kTopKMax; ++q) {
+    sv[t * kTopKMax + q] = v[q];
+    si[t * kTopKMax + q] = ix[q];
+  }
+  for (int half = NT / 2; half >= 1; half >>= 1) {
+    __syncthreads();
+    if (t < half) {
+      const int o = (t + half) * kTopKMax;
+      for (int q = 0; q < a.k; ++q) tk_insert<kTopKMax>(v, ix, sv[o + q], si[o + q]);
+#pragma unroll
+      for (int q = 0; q < kTopKMax; ++q) {
+        sv[t * kTopKMax + q] = v[q];
+        si[t * kTopKMax + q] = ix[q];
+      }
+    }
+  }
+  __syncthreads();
+  if (t < a.k) {
+    float2 *dst = a.part + ((long long)r * a.splits + sp) * a.k;
+    dst[t] = make_float2(sv[t], __int_as_float(si[t]));
+  }
+}
+
+__global__ __launch_bounds__(64) void topk_merge_kernel(TopKArgs a) {
+  const int r = blockIdx.x * 64 + threadIdx.x;
+  if (r >= a.R) return;
+  float v[kTopKMax];
+  int ix[kTopKMax];
+#pragma unroll
+  for (int q = 0; q < kTopKMax; ++q) {
+    v[q] = -INFINITY;
+    ix[q] = 0x7fffffff;
+  }
+  const float2 *src = a.part + (long long)r * a.splits * a.k;
+  for (int e = 0; e < a.splits * a.k; ++e) tk_insert<kTopKMax>(v, ix, src[e].x, __float_as_int(src[e].y));
+  for (int q = 0; q < a.k; ++q)
+    a.out[(long long)r * a.k + q] = (ix[q] == 0x7fffffff) ? (q == 0 ? 0 : -1) : ix[q];
 }
 
 }  // namespace chain
@@ -1071,6 +1199,9 @@ extern "C" size_t cfa_chain_verify_workspace_size(int B, int K, int V, int input
   return ws_layout(B, K, V, mode).total;
 }
 
+static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, float *out_target_probs,
+                        float *out_draft_probs);
+
 extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t t_stride_k,
                                 const float *draft, int64_t d_stride_b, int64_t d_stride_k,
                                 int input_kind, const int32_t *draft_tokens, const float *uniforms,
@@ -1113,12 +1244,14 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
   a.B = B;
   a.K = K;
   a.V = V;
+  a.draws = 1;
   a.rpb = (mode == CFA_MODE_GREEDY) ? K + 1 : 2 * K + 1;
   a.logits = input_kind == CFA_INPUT_LOGITS;
   a.c = a.logits ? (float)(1.4426950408889634 / (double)temperature) : 1.0f;
   a.mode = mode;
   a.eos = eos_token_id;
   a.top_p = top_p;
+  a.top_k = 0;
   a.out_accept_len = out_accept_len;
   a.out_tokens = out_tokens;
   a.out_num_emitted = out_num_emitted;
@@ -1130,9 +1263,19 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
                    (((uintptr_t)target & 15) == 0) &&
                    (mode == CFA_MODE_GREEDY || K == 0 ||
                     ((d_stride_k % 4 == 0) && (d_stride_b % 4 == 0) && (((uintptr_t)draft & 15) == 0)));
+  return run_pipeline(a, vec, workspace, (hipStream_t)stream, out_target_probs, out_draft_probs);
+}
+
+// Partition, workspace carve-up and launches shared by chain verification
+// and the sampler.  a.B jobs read a.B / a.draws row groups of a.rpb rows.
+static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, float *out_target_probs,
+                        float *out_draft_probs) {
+  using namespace cfa::abi;
+  const int B = a.B, K = a.K, V = a.V, mode = a.mode;
   const int W = vec ? 4 : 1;
   a.Vw = V / W;
-  const int R = B * a.rpb;
+  const int R = (B / a.draws) * a.rpb;
+  a.R = R;
   const long long total = (long long)R * a.Vw;
   const int cus = device_cu_count();
   long long G = std::min<long long>((long long)cus * 8, (total + 1023) / 1024);
@@ -1158,7 +1301,6 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
   a.badcnt = (int *)(ws + L.badcnt);
   a.bad = (MwBad *)(ws + L.bad);
 
-  hipStream_t st = (hipStream_t)stream;
   if (a.logits) {
     if (vec)
       CFA_LAUNCH("chain_stats", (stats_kernel<256, 4>), dim3(a.G), dim3(256), 0, st, a);
@@ -1181,10 +1323,104 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
     CFA_LAUNCH("chain_finish", finish_kernel, dim3((B + 63) / 64), dim3(64), 0, st, a);
   }
   if (out_target_probs || out_draft_probs) {
-    const int rows = B * a.rpb;
     const int gx = std::min(64, (V + 255) / 256);
-    CFA_LAUNCH("chain_probs_out", probs_out_kernel, dim3(gx, rows), dim3(256), 0, st, a,
+    CFA_LAUNCH("chain_probs_out", probs_out_kernel, dim3(gx, R), dim3(256), 0, st, a,
                out_target_probs, out_draft_probs);
   }
   return CFA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Sampler: plain decode and draft-tree expansion.
+// ---------------------------------------------------------------------------
+
+static int topk_splits(int R, int V) {
+  const int want = std::max(1, (1024 + R - 1) / R);
+  return std::max(1, std::min(want, V / 2048));
+}
+
+static int sample_chain_mode(int mode) {
+  return mode == CFA_SAMPLE_FILTERED ? CFA_MODE_PYTHON : CFA_MODE_CPP;
+}
+
+extern "C" size_t cfa_sample_workspace_size(int R, int V, int draws, int mode) {
+  if (R <= 0 || V <= 0 || draws <= 0) return 0;
+  if (mode == CFA_SAMPLE_GREEDY)
+    return align_up((size_t)R * topk_splits(R, V) * draws * sizeof(float2));
+  const size_t B = (size_t)R * draws;
+  return ws_layout((int)B, 0, V, sample_chain_mode(mode)).total + 3 * align_up(B * sizeof(int32_t));
+}
+
+extern "C" int cfa_sample(const float *rows, int64_t row_stride, int input_kind, int R, int V,
+                          int draws, float temperature, int top_k, float top_p, int mode,
+                          const float *uniforms, int32_t *out_tokens, float *out_probs,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace cfa::abi;
+  clear_error();
+  if (R <= 0 || V <= 0 || draws <= 0) return fail_arg("R, V and draws must be positive");
+  if ((long long)V > (long long)kMwMaxNC * kMwChunk) return fail_arg("V must be at most 4194304");
+  if ((long long)R * draws > 65535) return fail_arg("R * draws must be at most 65535");
+  if (mode != CFA_SAMPLE_MULTINOMIAL && mode != CFA_SAMPLE_FILTERED && mode != CFA_SAMPLE_GREEDY)
+    return fail_arg("mode must be CFA_SAMPLE_MULTINOMIAL, CFA_SAMPLE_FILTERED or CFA_SAMPLE_GREEDY");
+  if (input_kind != CFA_INPUT_PROBS && input_kind != CFA_INPUT_LOGITS)
+    return fail_arg("input_kind must be CFA_INPUT_PROBS or CFA_INPUT_LOGITS");
+  if (!rows || !out_tokens) return fail_arg("null pointer");
+  if (row_stride < V) return fail_arg("row_stride must be at least V");
+  const size_t need = cfa_sample_workspace_size(R, V, draws, mode);
+  if (!workspace || workspace_bytes < need) return fail_arg("workspace too small (see cfa_sample_workspace_size)");
+  hipStream_t st = (hipStream_t)stream;
+
+  if (mode == CFA_SAMPLE_GREEDY) {
+    if (draws > kTopKMax) return fail_arg("greedy sampling returns at most 8 tokens per row");
+    if (draws > V) return fail_arg("draws must not exceed V");
+    if (out_probs) return fail_arg("out_probs is not produced in greedy mode");
+    TopKArgs t{};
+    t.x = rows;
+    t.stride = row_stride;
+    t.R = R;
+    t.V = V;
+    t.k = draws;
+    t.splits = topk_splits(R, V);
+    t.per_split = (V + t.splits - 1) / t.splits;
+    t.part = (float2 *)workspace;
+    t.out = out_tokens;
+    CFA_LAUNCH("sample_topk", (topk_partial_kernel<256>), dim3(t.splits, R), dim3(256), 0, st, t);
+    CFA_LAUNCH("sample_topk_merge", topk_merge_kernel, dim3((R + 63) / 64), dim3(64), 0, st, t);
+    return CFA_OK;
+  }
+  if (!uniforms) return fail_arg("null uniforms");
+  if (input_kind == CFA_INPUT_LOGITS && !(temperature > 0.0f)) return fail_arg("temperature must be > 0");
+  if (mode == CFA_SAMPLE_FILTERED && !(top_p > 0.0f && top_p <= 1.0f))
+    return fail_arg("top_p must be in (0, 1]");
+
+  const int B = R * draws;
+  const int chain_mode = sample_chain_mode(mode);
+  Args a{};
+  a.tgt = rows;
+  a.t_sb = row_stride;
+  a.t_sk = V;
+  a.drf = nullptr;
+  a.tokens = nullptr;
+  a.U = uniforms;
+  a.B = B;
+  a.K = 0;
+  a.V = V;
+  a.draws = draws;
+  a.rpb = 1;
+  a.logits = input_kind == CFA_INPUT_LOGITS;
+  a.c = a.logits ? (float)(1.4426950408889634 / (double)temperature) : 1.0f;
+  a.mode = chain_mode;
+  a.eos = -1;
+  a.top_p = (mode == CFA_SAMPLE_FILTERED) ? top_p : 1.0f;
+  a.top_k = (mode == CFA_SAMPLE_FILTERED) ? top_k : 0;
+  const WsLayout L = ws_layout(B, 0, V, chain_mode);
+  int32_t *scratch = (int32_t *)((char *)workspace + L.total);
+  const size_t ib = align_up((size_t)B * sizeof(int32_t));
+  a.out_tokens = out_tokens;
+  a.out_final = (int32_t *)((char *)scratch);
+  a.out_accept_len = (int32_t *)((char *)scratch + ib);
+  a.out_num_emitted = (int32_t *)((char *)scratch + 2 * ib);
+  a.out_eos = a.out_accept_len;  // written after out_accept_len, never read
+  const bool vec = (V % 4 == 0) && (row_stride % 4 == 0) && (((uintptr_t)rows & 15) == 0);
+  return run_pipeline(a, vec, workspace, st, out_probs, nullptr);
 }

@@ -102,6 +102,41 @@ int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t t_stride_k
                      size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
+ * Token sampler: plain decode and draft-tree expansion.
+ *
+ * Replaces launch_fused_sampling / fused_sampling_kernel
+ * (csrc/include/cudaforge/engine/sampling.h:18-28, 61-216) and
+ * fused_sampling_triton (csrc/kernels/triton/sampling_triton.py:6-66), and
+ * draws the children of draft-tree nodes.  R rows of V values at
+ * rows + r * row_stride (logits, or probabilities for CFA_INPUT_PROBS);
+ * `draws` tokens per row, out_tokens [R, draws]:
+ *   CFA_SAMPLE_MULTINOMIAL  p = softmax(row / temperature); token = first i
+ *     with u <= p_0 + ... + p_i summed sequentially in fp32, V - 1 if none
+ *     (sampling.h:164-185, speculative.cpp:11-24), one uniform per draw
+ *     (uniforms [R, draws]).  top_k / top_p are ignored, as the reference
+ *     kernel ignores them.
+ *   CFA_SAMPLE_FILTERED  keep p_i >= the top-p threshold of
+ *     cudaforge/speculative.py:67-81 and >= the top_k-th largest p (top_k <= 0:
+ *     no top-k), renormalise by the kept mass, then the same draw.
+ *   CFA_SAMPLE_GREEDY  the `draws` (<= 8) largest raw values, largest first,
+ *     equal values by lower index (sampling.h:107-135 for draws = 1); no
+ *     uniforms, no temperature.
+ * out_probs [R, V] (optional, not in greedy mode) receives the probabilities
+ * the draws used.  Independent draws of one row (draws > 1) sample with
+ * replacement: the children of a tree node drawn i.i.d. from its draft
+ * distribution, as multi-candidate rejection sampling requires.
+ */
+#define CFA_SAMPLE_MULTINOMIAL 0
+#define CFA_SAMPLE_FILTERED 1
+#define CFA_SAMPLE_GREEDY 2
+
+size_t cfa_sample_workspace_size(int R, int V, int draws, int mode);
+int cfa_sample(const float *rows, int64_t row_stride, int input_kind, int R, int V, int draws,
+               float temperature, int top_k, float top_p, int mode, const float *uniforms,
+               int32_t *out_tokens, float *out_probs, void *workspace, size_t workspace_bytes,
+               void *stream);
+
+/* ---------------------------------------------------------------------------
  * Tree-masked verification attention over a paged KV cache (bf16, MFMA).
  *
  * No reference kernel exists (the reference's target forward recomputes the

@@ -16,7 +16,9 @@ Contents
     masked SDPA; conventions of ``csrc/kernels/triton/flash_attn_triton.py:
     112-172``) and for the KV commit (``index_copy`` of accepted slots; page
     addressing of ``csrc/src/memory/paged_kv_cache.cpp:13-21,409-421``);
-  * the context-length rule of ``paged_kv_cache.cpp:359-364``.
+  * the context-length rule of ``paged_kv_cache.cpp:359-364``;
+  * the sampler's keep rules and greedy top-k (``topk_keep``,
+    ``sample_filtered``, ``topk_greedy``; ``sampling.h:61-186``).
 """
 from __future__ import annotations
 
@@ -202,6 +204,36 @@ def topp_keep(p, top_p: float) -> np.ndarray:
     keep = np.zeros(a.size, np.uint8)
     lib().orc_topp_keep(_p(a, c_f32p), a.size, np.float32(top_p), _p(keep, c_u8p))
     return keep.astype(bool)
+
+
+def topk_keep(p, top_k: int) -> np.ndarray:
+    """Keep every p_i >= the top_k-th largest value (ties kept); top_k <= 0
+    or >= V keeps everything.  No reference counterpart (the reference
+    sampler takes top_k but never applies it, sampling.h:61-186)."""
+    a = _f32(p).ravel()
+    if top_k <= 0 or top_k >= a.size:
+        return np.ones(a.size, bool)
+    kth = np.sort(a)[::-1][top_k - 1]
+    return a >= kth
+
+
+def sample_filtered(p, r: float, top_p: float, top_k: int) -> int:
+    """Keep rule (top-p of speculative.py:67-81 and top-k), renormalise by
+    the sequential fp32 kept mass, sequential fp32 inverse CDF."""
+    a = _f32(p).ravel()
+    keep = topp_keep(a, top_p) & topk_keep(a, top_k)
+    return sample_weights(np.where(keep, a, np.float32(0)).astype(np.float32), r)
+
+
+def topk_greedy(rows, k: int) -> np.ndarray:
+    """The k largest values of each row, largest first, equal values by lower
+    index (sampling.h:107-135 for k = 1: the first argmax)."""
+    x = np.asarray(rows, np.float32)
+    out = np.empty((x.shape[0], k), np.int32)
+    for r in range(x.shape[0]):
+        order = np.lexsort((np.arange(x.shape[1]), -x[r].astype(np.float64)))
+        out[r] = order[:k]
+    return out
 
 
 def sample_weights(w, r: float) -> int:
