@@ -197,6 +197,46 @@ def tree_accept_commit_leg(dev, reps=10):
             "commit_gbs": round(alg_commit / t_com / 1e9, 1) if moved else None}
 
 
+def verify_step_8b_leg(dev, steps=6, warmup=2):
+    """one speculative verify step at Llama-3-8B shape --
+    random-init W4A16 (group 128) target (32L, d4096, GQA 32/8, FFN 14336,
+    V128256), random-init 1B-shape bf16 draft proposing a 63-node binary tree
+    (children drawn from the draft softmax), B=8, context 2048 (synthetic
+    N(0,1) K/V), T=1.0; tree attention, sampling, verification and commit
+    on this library's kernels.  Random-init models agree on nothing, so the
+    accepted path is the root alone and verified tok/s = B / step time."""
+    import torch
+    from cudaforge_amd.spec_step import (DRAFT_1B, TARGET_8B, DraftModel, TargetModel,
+                                         TreeSpeculator)
+
+    Bs, ctx = 8, 2048
+    tm = TargetModel(TARGET_8B, dev, seed=0)
+    dm = DraftModel(DRAFT_1B, dev, Bs, max_slots=ctx + 64 + 8 * (steps + warmup + 2))
+    sp = TreeSpeculator(tm, dm, Bs, ctx, depth=5, temperature=1.0, mode="cpp",
+                        max_steps=steps + warmup + 2)
+    for _ in range(warmup):
+        sp.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    emitted = 0
+    for _ in range(steps):
+        emitted += sum(sp.step().path_len)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    phases = {}
+    for _ in range(2):
+        sp.step(phases)
+    out = {"config": "Llama-3-8B-shape W4A16 g128 target, 1B-shape bf16 draft, 63-node binary "
+                     "tree, B=8, ctx 2048, T=1.0 (BASELINE configs[4]); random init",
+           "ms_per_step": round(dt / steps * 1e3, 2),
+           "verified_tok_s": round(emitted / dt, 1),
+           "mean_path_len": round(emitted / (steps * Bs), 3),
+           "phases_ms": {k: round(v / 2, 3) for k, v in phases.items()}}
+    del sp, tm, dm
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -310,6 +350,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         line["tree_accept_commit"] = tree_accept_commit_leg(dev)
         torch.cuda.empty_cache()
+        line["verify_step_8b"] = verify_step_8b_leg(dev)
     if not args.no_cpu_baseline:
         tl, dl, tok, U = make_inputs(dev, 1000)
         line["cpu_baseline"] = cpu_baseline(tl, dl, tok, U)

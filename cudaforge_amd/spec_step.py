@@ -1,0 +1,354 @@
+"""One speculative verify step at model scale: a draft proposes a token tree,
+the target scores it, and the tree is verified and committed.
+
+This is the end-to-end shape of the reference's speculative loop
+(``cudaforge/speculative.py:99-217``: draft proposal, one target forward over
+the candidates, acceptance, bonus token) with a draft-token tree in place of
+the chain, as a random-initialised Llama-3-8B-shape target with W4A16 weights
+and a 1B-shape bf16 draft.  The verification path runs on this library's
+kernels:
+
+* tree expansion    ``cfa_sample`` (children drawn i.i.d. from the draft
+                    softmax, or greedy top-2);
+* tree attention    ``cfa_tree_attention`` over the target's paged KV pools;
+* verification      ``cfa_tree_verify`` (multi-candidate rejection sampling,
+                    longest accepted path, bonus token);
+* KV commit         ``cfa_kv_commit`` plus the page-table rollback of
+                    ``PagedKVCache.truncate_sequence``;
+* W4A16 weights     ``cfa_w4a16_dequant`` (the reference's packed INT4
+                    format, ``int4_gemm_dequant.cu:20-31``) feeding
+                    PyTorch-ROCm GEMMs; the norms, rotary embeddings,
+                    activations and the draft's own attention run in PyTorch.
+
+The draft keeps a contiguous KV cache (``[layers, B, Hkv, head_dim, slots]``
+for K, so the score product reads a contiguous operand) because its head size
+(64) is not the tree-attention kernel's.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional
+
+import numpy as np
+import torch
+
+from . import tree as T
+from .kv_cache import KVCacheConfig, PagedKVCache
+from .sampling import expand_tree_level
+from .verify import tree_attention, tree_attention_workspace_bytes, tree_verify
+from .w4a16 import W4A16Linear
+
+__all__ = ["LlamaShape", "TARGET_8B", "DRAFT_1B", "TargetModel", "DraftModel", "TreeSpeculator",
+           "StepResult"]
+
+
+@dataclass(frozen=True)
+class LlamaShape:
+    n_layers: int
+    d_model: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn: int
+    vocab: int
+    rope_theta: float = 500000.0
+    eps: float = 1e-5
+
+
+TARGET_8B = LlamaShape(32, 4096, 32, 8, 128, 14336, 128256)
+DRAFT_1B = LlamaShape(16, 2048, 32, 8, 64, 8192, 128256)
+
+
+# ---------------------------------------------------------------------------
+# shared pieces
+# ---------------------------------------------------------------------------
+
+def _rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(x.dtype)
+
+
+def _rope(x: torch.Tensor, pos: torch.Tensor, theta: float) -> torch.Tensor:
+    """Rotate-half rotary embedding; x [..., T, H, D], pos [..., T]."""
+    D = x.shape[-1]
+    inv = theta ** (-torch.arange(0, D, 2, device=x.device, dtype=torch.float32) / D)
+    ang = pos.float()[..., None] * inv                       # [..., T, D/2]
+    cos = torch.cat([ang.cos(), ang.cos()], -1)[..., None, :]
+    sin = torch.cat([ang.sin(), ang.sin()], -1)[..., None, :]
+    xf = x.float()
+    rot = torch.cat([-xf[..., D // 2:], xf[..., : D // 2]], -1)
+    return (xf * cos + rot * sin).to(x.dtype)
+
+
+def _randn(shape, gen, device, scale=1.0, dtype=torch.bfloat16):
+    return (scale * torch.randn(shape, device=device, generator=gen)).to(dtype)
+
+
+# ---------------------------------------------------------------------------
+# target: W4A16 Llama shape over the paged cache, tree attention kernel
+# ---------------------------------------------------------------------------
+
+class TargetModel:
+    def __init__(self, shape: LlamaShape, device, seed: int = 0, group: int = 128):
+        if shape.head_dim != 128:
+            raise ValueError("the tree-attention kernel takes head_dim 128")
+        s = self.shape = shape
+        g = torch.Generator(device=device).manual_seed(seed)
+        d, hd = s.d_model, s.head_dim
+        qkv_n = (s.n_heads + 2 * s.n_kv_heads) * hd
+        self.embed = _randn((s.vocab, d), g, device)
+        self.layers = []
+        for _ in range(s.n_layers):
+            self.layers.append(dict(
+                attn_norm=torch.ones(d, dtype=torch.bfloat16, device=device),
+                wqkv=W4A16Linear(d, qkv_n, device, g, group),
+                wo=W4A16Linear(s.n_heads * hd, d, device, g, group),
+                ffn_norm=torch.ones(d, dtype=torch.bfloat16, device=device),
+                wgu=W4A16Linear(d, 2 * s.ffn, device, g, group),
+                wdown=W4A16Linear(s.ffn, d, device, g, group)))
+        self.norm = torch.ones(d, dtype=torch.bfloat16, device=device)
+        self.lm_head = _randn((d, s.vocab), g, device, 1.0 / math.sqrt(d))
+        biggest = max(d * qkv_n, s.n_heads * hd * d, d * 2 * s.ffn, s.ffn * d)
+        self.scratch = torch.empty(biggest, dtype=torch.bfloat16, device=device)
+        self.attn_ws = None
+
+    def forward_tree(self, tokens: torch.Tensor, positions: torch.Tensor, kv: PagedKVCache,
+                     block_tables: torch.Tensor, base_lens: torch.Tensor, masks: torch.Tensor,
+                     max_keys: int) -> torch.Tensor:
+        """tokens / positions [B, N]; the nodes' K/V go to slots base + node
+        of every layer; returns fp32 logits [B, N, V]."""
+        s = self.shape
+        B, N = tokens.shape
+        hd, Hq, Hkv = s.head_dim, s.n_heads, s.n_kv_heads
+        bs = kv.get_config().block_size
+        slot = base_lens.long()[:, None] + torch.arange(N, device=tokens.device)[None, :]
+        blk = torch.gather(block_tables.long(), 1, slot // bs).reshape(-1)
+        off = (slot % bs).reshape(-1)
+        need = tree_attention_workspace_bytes(B, N, Hq, Hkv, hd, max_keys)
+        if self.attn_ws is None or self.attn_ws.numel() < need:
+            self.attn_ws = torch.empty(max(need, 1), dtype=torch.uint8, device=tokens.device)
+        h = self.embed[tokens.reshape(-1).long()]               # [B*N, d]
+        for li, L in enumerate(self.layers):
+            x = _rmsnorm(h, L["attn_norm"], s.eps)
+            qkv = L["wqkv"](x, self.scratch).view(B, N, Hq + 2 * Hkv, hd)
+            q = _rope(qkv[:, :, :Hq], positions, s.rope_theta)
+            k = _rope(qkv[:, :, Hq:Hq + Hkv], positions, s.rope_theta)
+            v = qkv[:, :, Hq + Hkv:]
+            kv.key_pool[blk, li, :, off, :] = k.reshape(B * N, Hkv, hd)
+            kv.value_pool[blk, li, :, off, :] = v.reshape(B * N, Hkv, hd)
+            o = tree_attention(q.contiguous(), kv.key_pool, kv.value_pool, block_tables, base_lens,
+                               masks, layer=li, max_keys=max_keys, workspace=self.attn_ws)
+            h = h + L["wo"](o.reshape(B * N, Hq * hd), self.scratch)
+            x = _rmsnorm(h, L["ffn_norm"], s.eps)
+            gu = L["wgu"](x, self.scratch)
+            a = torch.nn.functional.silu(gu[:, : s.ffn]) * gu[:, s.ffn:]
+            h = h + L["wdown"](a, self.scratch)
+        h = _rmsnorm(h, self.norm, s.eps)
+        return (h @ self.lm_head).float().view(B, N, s.vocab)
+
+
+# ---------------------------------------------------------------------------
+# draft: bf16 Llama shape, contiguous KV cache, attention in PyTorch
+# ---------------------------------------------------------------------------
+
+class DraftModel:
+    def __init__(self, shape: LlamaShape, device, B: int, max_slots: int, seed: int = 1):
+        s = self.shape = shape
+        g = torch.Generator(device=device).manual_seed(seed)
+        d, hd = s.d_model, s.head_dim
+        qkv_n = (s.n_heads + 2 * s.n_kv_heads) * hd
+        self.embed = _randn((s.vocab, d), g, device)
+        self.layers = []
+        for _ in range(s.n_layers):
+            self.layers.append(dict(
+                attn_norm=torch.ones(d, dtype=torch.bfloat16, device=device),
+                wqkv=_randn((d, qkv_n), g, device, 1.0 / math.sqrt(d)),
+                wo=_randn((s.n_heads * hd, d), g, device, 1.0 / math.sqrt(s.n_heads * hd)),
+                ffn_norm=torch.ones(d, dtype=torch.bfloat16, device=device),
+                wgu=_randn((d, 2 * s.ffn), g, device, 1.0 / math.sqrt(d)),
+                wdown=_randn((s.ffn, d), g, device, 1.0 / math.sqrt(s.ffn))))
+        self.norm = torch.ones(d, dtype=torch.bfloat16, device=device)
+        self.lm_head = self.embed.t().contiguous()              # tied embeddings
+        self.kT = torch.zeros(s.n_layers, B, s.n_kv_heads, hd, max_slots, dtype=torch.bfloat16,
+                              device=device)
+        self.v = torch.zeros(s.n_layers, B, s.n_kv_heads, max_slots, hd, dtype=torch.bfloat16,
+                             device=device)
+        self.max_slots = max_slots
+
+    def forward_nodes(self, tokens: torch.Tensor, positions: torch.Tensor, slots: torch.Tensor,
+                      visible: torch.Tensor) -> torch.Tensor:
+        """tokens / positions / slots [B, n]; visible [B, n, max_slots] bool
+        (every cache slot, so both products read whole contiguous caches);
+        returns fp32 logits [B, n, V]."""
+        s = self.shape
+        B, n = tokens.shape
+        hd, Hq, Hkv = s.head_dim, s.n_heads, s.n_kv_heads
+        G = Hq // Hkv
+        bidx = torch.arange(B, device=tokens.device)[:, None].expand(B, n)
+        bias = torch.zeros(visible.shape, dtype=torch.float32, device=tokens.device)
+        bias.masked_fill_(~visible, float("-inf"))
+        h = self.embed[tokens.reshape(-1).long()]
+        for li, L in enumerate(self.layers):
+            x = _rmsnorm(h, L["attn_norm"], s.eps)
+            qkv = (x @ L["wqkv"]).view(B, n, Hq + 2 * Hkv, hd)
+            q = _rope(qkv[:, :, :Hq], positions, s.rope_theta)
+            k = _rope(qkv[:, :, Hq:Hq + Hkv], positions, s.rope_theta)
+            v = qkv[:, :, Hq + Hkv:]
+            self.kT[li][bidx, :, :, slots] = k                   # [B, n, Hkv, hd]
+            self.v[li][bidx, :, slots, :] = v
+            # scores [B, Hkv, G*n, keys]: q grouped by KV head, K^T contiguous
+            qg = q.view(B, n, Hkv, G, hd).permute(0, 2, 3, 1, 4).reshape(B, Hkv, G * n, hd)
+            S = self.max_slots
+            sc = torch.matmul(qg.contiguous(), self.kT[li]).float()
+            sc = sc.view(B, Hkv, G, n, S) * (1.0 / math.sqrt(hd)) + bias[:, None, None]
+            p = torch.softmax(sc, dim=-1).to(torch.bfloat16).view(B, Hkv, G * n, S)
+            o = torch.matmul(p, self.v[li])                       # [B, Hkv, G*n, hd]
+            o = o.view(B, Hkv, G, n, hd).permute(0, 3, 1, 2, 4).reshape(B * n, Hq * hd)
+            h = h + o @ L["wo"]
+            x = _rmsnorm(h, L["ffn_norm"], s.eps)
+            gu = x @ L["wgu"]
+            h = h + (torch.nn.functional.silu(gu[:, : s.ffn]) * gu[:, s.ffn:]) @ L["wdown"]
+        h = _rmsnorm(h, self.norm, s.eps)
+        return (h @ self.lm_head).float().view(B, n, s.vocab)
+
+    def commit(self, base: torch.Tensor, paths: torch.Tensor, path_lens: List[int]) -> None:
+        """Move the accepted nodes (slot base + node) to base + j, as
+        cfa_kv_commit does for the paged target cache."""
+        for b, L in enumerate(path_lens):
+            if L <= 1:
+                continue
+            src = base[b] + paths[b, :L].long()
+            dst = base[b] + torch.arange(L, device=base.device)
+            self.kT[:, b, :, :, dst] = self.kT[:, b, :, :, src].clone()
+            self.v[:, b, :, dst, :] = self.v[:, b, :, src, :].clone()
+
+
+# ---------------------------------------------------------------------------
+# the step
+# ---------------------------------------------------------------------------
+
+@dataclass
+class StepResult:
+    path_len: List[int]          # 1 + accepted drafts, per sequence
+    emitted: List[List[int]]     # accepted draft tokens then the final token
+    final: List[int]
+
+
+class TreeSpeculator:
+    """Batched tree speculation: a binary draft tree of `depth` levels below
+    the root (2^(depth+1) - 1 nodes), the last emitted token as its root."""
+
+    def __init__(self, target: TargetModel, draft: DraftModel, B: int, context: int, *,
+                 depth: int = 5, temperature: float = 1.0, mode: str = "cpp",
+                 max_steps: int = 64, block_size: int = 16, seed: int = 0):
+        dev = target.embed.device
+        self.t, self.d = target, draft
+        self.B, self.depth, self.T, self.mode = B, depth, temperature, mode
+        self.N = 2 ** (depth + 1) - 1
+        if self.N > 64:
+            raise ValueError("a tree has at most 64 nodes")
+        self.parents_np = T.binary_tree_parents(self.N)
+        self.parents = torch.from_numpy(self.parents_np).to(dev)
+        self.depths = torch.from_numpy(T.depths(self.parents_np)).to(dev)
+        anc = T.ancestor_masks(self.parents_np)
+        self.masks = T.mask_tensor(anc, dev)
+        anc_bits = np.array([[(int(anc[i]) >> j) & 1 for j in range(self.N)]
+                             for i in range(self.N)], bool)
+        self.anc = torch.from_numpy(anc_bits).to(dev)           # [N, N]
+        s = target.shape
+        slots = context + self.N + 8 * max_steps
+        nblk = B * (slots // block_size + 2) + 8
+        cfg = KVCacheConfig(num_layers=s.n_layers, num_kv_heads=s.n_kv_heads,
+                            head_dim=s.head_dim, block_size=block_size, total_gpu_blocks=nblk,
+                            enable_prefix_caching=False, max_supported_batch_size=B,
+                            max_blocks_per_sequence=slots // block_size + 2)
+        self.kv = PagedKVCache(cfg, device=dev)
+        self.gen = torch.Generator(device=dev).manual_seed(seed)
+        # synthetic context: page tables for `context` tokens, N(0,1) K/V
+        rng = np.random.default_rng(seed)
+        for b in range(B):
+            self.kv.register_sequence_with_prefix(b, rng.integers(0, s.vocab, context).tolist())
+        self.kv.key_pool.normal_(generator=self.gen)
+        self.kv.value_pool.normal_(generator=self.gen)
+        draft.kT.normal_(generator=self.gen)
+        draft.v.normal_(generator=self.gen)
+        self.ctx = [context] * B
+        self.root = torch.randint(0, s.vocab, (B,), device=dev, generator=self.gen,
+                                  dtype=torch.int32)
+        self.draft_rows = torch.zeros(B, self.N, s.vocab, dtype=torch.float32, device=dev)
+        self.max_slots = draft.max_slots
+
+    def propose(self, base: torch.Tensor) -> torch.Tensor:
+        """Draft tree tokens [B, N] (node 0 = root); fills self.draft_rows
+        with the draft logits of every expanded node."""
+        B, dev = self.B, self.root.device
+        tokens = torch.empty(B, self.N, dtype=torch.int32, device=dev)
+        tokens[:, 0] = self.root
+        n_keys = self.max_slots
+        key_ix = torch.arange(n_keys, device=dev)
+        prefix = key_ix[None, :] < base[:, None]                 # [B, keys]
+        for lvl in range(self.depth):
+            lo, hi = 2 ** lvl - 1, 2 ** (lvl + 1) - 1
+            nodes = torch.arange(lo, hi, device=dev)
+            slots = base[:, None] + nodes[None, :]
+            pos = base[:, None] + self.depths[nodes][None, :]
+            # node i sees the prefix and its ancestors' slots
+            rel = key_ix[None, None, :] - base[:, None, None]     # [B, 1, keys]
+            in_tree = (rel >= 0) & (rel < self.N)
+            anc = self.anc[nodes][None, :, :].expand(B, -1, -1)   # [B, n, N]
+            tree_vis = torch.gather(anc, 2, rel.clamp(0, self.N - 1).expand(B, hi - lo, n_keys))
+            visible = prefix[:, None, :] | (in_tree & tree_vis)
+            logits = self.d.forward_nodes(tokens[:, lo:hi], pos, slots, visible)
+            self.draft_rows[:, lo:hi] = logits
+            kids = expand_tree_level(logits.view(B * (hi - lo), -1), children=2,
+                                     mode="sample" if self.mode == "cpp" else "greedy",
+                                     temperature=self.T, generator=self.gen)
+            tokens[:, 2 * lo + 1: 2 * hi + 1] = kids.view(B, 2 * (hi - lo))
+        return tokens
+
+    def step(self, phase_ms: Optional[dict] = None) -> StepResult:
+        """One verify step.  With `phase_ms`, the device time of each phase
+        (propose, target, verify, commit) is added to it, in ms."""
+        B, dev, N = self.B, self.root.device, self.N
+        if max(self.ctx) + N > self.max_slots:
+            raise RuntimeError("draft cache full: raise max_steps")
+        ev = []
+
+        def mark():
+            if phase_ms is not None:
+                e = torch.cuda.Event(enable_timing=True)
+                e.record()
+                ev.append(e)
+
+        mark()
+        base = torch.tensor(self.ctx, dtype=torch.int32, device=dev)
+        tokens = self.propose(base)
+        mark()
+        for b in range(B):
+            self.kv.append_tokens(b, N)
+        desc = self.kv.prepare_batch_metadata(list(range(B)))
+        pos = base[:, None] + self.depths[None, :]
+        max_keys = max(self.ctx) + N
+        logits = self.t.forward_tree(tokens, pos, self.kv, desc.block_tables, base, self.masks,
+                                     max_keys)
+        mark()
+        n_u = 2 * 2 * self.depth + 2
+        u = 1.0 - torch.rand(B, n_u, device=dev, generator=self.gen)
+        res = tree_verify(logits, self.draft_rows, self.parents, tokens, u, input_kind="logits",
+                          temperature=self.T, mode=self.mode)
+        mark()
+        new_lens = self.kv.commit_tree_paths(list(range(B)), desc, base, res.path, res.path_len)
+        plen = [n - c for n, c in zip(new_lens, self.ctx)]
+        self.d.commit(base, res.path, plen)
+        toks = res.tokens.cpu().tolist()
+        ne = res.num_emitted.cpu().tolist()
+        final = res.final.cpu().tolist()
+        self.ctx = new_lens
+        self.root = res.final.to(torch.int32)
+        mark()
+        if phase_ms is not None:
+            torch.cuda.synchronize()
+            for name, a, b in zip(("propose", "target", "verify", "commit"), ev[:-1], ev[1:]):
+                phase_ms[name] = phase_ms.get(name, 0.0) + a.elapsed_time(b)
+        return StepResult(path_len=plen, emitted=[t[:e] for t, e in zip(toks, ne)], final=final)

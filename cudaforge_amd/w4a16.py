@@ -1,0 +1,96 @@
+"""W4A16 weights in the reference's packed INT4 format.
+
+``B_quant`` [K / 8, N] int32 holds nibble k % 8 of column n at bits
+4 * (k % 8) of word (k // 8, n), unsigned 0..15, with fp16 group scales
+[K / group, N] and optional fp16 zero points
+(``csrc/include/cudaforge/kernels/dequantize.cuh:12-25``,
+``tests/unit/test_int4_dequant.py:6-15``).  ``int4_gemm_dequant`` mirrors
+``int4_gemm_dequant_triton`` (``csrc/kernels/triton/int4_dequant_triton.py:
+86-131``): the weights are dequantised on the device by ``cfa_w4a16_dequant``
+and multiplied by a PyTorch-ROCm GEMM in the activations' dtype.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .verify import _stream_ptr
+
+__all__ = ["pack_int4_weights", "w4a16_dequant", "int4_gemm_dequant", "W4A16Linear"]
+
+
+def pack_int4_weights(w_int4: torch.Tensor) -> torch.Tensor:
+    """[K, N] values 0..15 -> [K // 8, N] int32, nibble k % 8 of word k // 8
+    at bits 4 * (k % 8) (tests/unit/test_int4_dequant.py:6-15)."""
+    K, N = w_int4.shape
+    if K % 8:
+        raise ValueError("K must be a multiple of 8")
+    w = w_int4.to(torch.int32) & 0x0F
+    packed = torch.zeros((K // 8, N), dtype=torch.int32, device=w.device)
+    for i in range(8):
+        packed |= w[i::8, :] << (i * 4)
+    return packed
+
+
+def w4a16_dequant(b_quant: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor] = None,
+                  *, group_size: int = 128, dtype: torch.dtype = torch.bfloat16,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Dequantise packed INT4 weights to [K, N] fp16 or bf16 on the device."""
+    if b_quant.dtype != torch.int32 or b_quant.device.type != "cuda" or b_quant.dim() != 2:
+        raise ValueError("b_quant must be an int32 [K/8, N] HIP tensor")
+    Kq, N = b_quant.shape
+    K = Kq * 8
+    if scales.dtype != torch.float16 or tuple(scales.shape) != (K // group_size, N):
+        raise ValueError("scales must be fp16 [K/group_size, N]")
+    if zeros is not None and (zeros.dtype != torch.float16 or zeros.shape != scales.shape):
+        raise ValueError("zeros must be fp16 [K/group_size, N]")
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("dtype must be float16 or bfloat16")
+    if out is None:
+        out = torch.empty(K, N, dtype=dtype, device=b_quant.device)
+    elif out.dtype != dtype or tuple(out.shape) != (K, N) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [K, N] tensor of `dtype`")
+    bq, sc = b_quant.contiguous(), scales.contiguous()
+    zz = zeros.contiguous() if zeros is not None else None
+    with torch.cuda.device(b_quant.device):
+        rc = _lib.load().cfa_w4a16_dequant(
+            bq.data_ptr(), sc.data_ptr(), zz.data_ptr() if zz is not None else None, K, N,
+            group_size, 1 if dtype == torch.bfloat16 else 0, out.data_ptr(),
+            _stream_ptr(b_quant.device))
+    _lib.check(rc, "cfa_w4a16_dequant")
+    return out
+
+
+class W4A16Linear:
+    """y = x @ W with W [K, N] held as packed INT4 + fp16 group scales.
+    Random initialisation: uniform nibbles, scales chosen so that the output
+    of a unit-RMS input has RMS about 1 (nibbles are unsigned, as in the
+    reference format, so W has a positive mean)."""
+
+    def __init__(self, K: int, N: int, device, gen: torch.Generator, group: int = 128):
+        self.K, self.N, self.group = K, N, group
+        self.qweight = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), dtype=torch.int32,
+                                     device=device, generator=gen)
+        base = 1.0 / (9.0 * math.sqrt(K))
+        self.scales = (base * (0.5 + torch.rand(K // group, N, device=device, generator=gen))
+                       ).to(torch.float16)
+
+    def __call__(self, x: torch.Tensor, scratch: torch.Tensor) -> torch.Tensor:
+        w = scratch[: self.K * self.N].view(self.K, self.N)
+        w4a16_dequant(self.qweight, self.scales, group_size=self.group, dtype=x.dtype, out=w)
+        return x @ w
+
+
+def int4_gemm_dequant(a: torch.Tensor, b_quant: torch.Tensor, scales: torch.Tensor,
+                      zeros: Optional[torch.Tensor] = None, group_size: int = 128) -> torch.Tensor:
+    """a [M, K] fp16 (or bf16) @ dequant(b_quant) -> [M, N] in a's dtype
+    (fp32 accumulation), as int4_dequant_triton.py:86-131."""
+    if a.dim() != 2 or a.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("a must be [M, K] fp16 or bf16")
+    if b_quant.shape[0] * 8 != a.shape[1]:
+        raise ValueError("K of a and b_quant differ")
+    w = w4a16_dequant(b_quant, scales, zeros, group_size=group_size, dtype=a.dtype)
+    return a @ w

@@ -228,6 +228,21 @@ int cfa_kv_commit(void *k_pool, void *v_pool, const int32_t *block_tables,
                   int32_t *new_ctx_lens, int32_t *status, void *stream);
 
 /* ---------------------------------------------------------------------------
+ * W4A16 weight dequantisation.
+ *
+ * The reference's packed INT4 weights (dequantize.cuh:12-25): b_quant
+ * [K/8, N] 32-bit words, nibble k % 8 of word (k/8, n) at bits 4*(k % 8),
+ * unsigned; scales [K/group_size, N] fp16; zeros (optional) the same shape,
+ * fp16.  out [K, N]: fp16 (out_bf16 = 0) w = (fp16(nibble) - z) * s in fp16
+ * arithmetic, as int4_gemm_dequant.cu:20-31 (without zeros: fp16(nibble * s),
+ * as int4_dequant_triton.py:74-78); bf16 (out_bf16 = 1) w = bf16((nibble - z)
+ * * s) formed in fp32.  Feeds the GEMMs of int4_gemm_dequant_triton
+ * (int4_dequant_triton.py:86-131) / launch_int4_gemm_dequant.
+ */
+int cfa_w4a16_dequant(const uint32_t *b_quant, const void *scales, const void *zeros, int K,
+                      int N, int group_size, int out_bf16, void *out, void *stream);
+
+/* ---------------------------------------------------------------------------
  * Paged KV cache page tables (host metadata).
  *
  * Replaces the metadata half of PagedKVCache (paged_kv_cache.h:36-179,

@@ -1,0 +1,121 @@
+"""GPU tier: the model-scale verify step (cudaforge_amd/spec_step.py) at
+small shapes.  The target's tree forward (W4A16 GEMMs, paged KV writes, tree
+attention kernel) against an fp32 PyTorch forward over gathered pages with an
+explicit tree mask; a few full steps checked for bookkeeping (context growth,
+page tables, emitted tokens on the accepted path, draft-cache commit)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from cudaforge_amd import tree as T
+from cudaforge_amd.spec_step import DraftModel, LlamaShape, TargetModel, TreeSpeculator
+from cudaforge_amd.w4a16 import w4a16_dequant
+
+pytestmark = pytest.mark.gpu
+
+SMALL_T = LlamaShape(2, 256, 4, 2, 128, 384, 1000)
+SMALL_D = LlamaShape(2, 128, 4, 2, 64, 256, 1000)
+
+
+def _ref_forward(tm: TargetModel, tokens, positions, kv, tables, base, N):
+    """fp32 reference of TargetModel.forward_tree given the pool contents
+    before the call (the tree's own K/V come from this forward)."""
+    s = tm.shape
+    B = tokens.shape[0]
+    hd, Hq, Hkv = s.head_dim, s.n_heads, s.n_kv_heads
+    G = Hq // Hkv
+    par = T.binary_tree_parents(N)
+    anc = T.ancestor_masks(par)
+    allow = torch.tensor([[bool((int(anc[i]) >> j) & 1) for j in range(N)] for i in range(N)],
+                         device=tokens.device)
+    bs = kv.get_config().block_size
+
+    def W(lin):
+        return w4a16_dequant(lin.qweight, lin.scales, group_size=lin.group,
+                             dtype=torch.bfloat16).float()
+
+    def rms(x, w):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + s.eps) * w.float()
+
+    def rope(x, pos):
+        D = x.shape[-1]
+        inv = s.rope_theta ** (-torch.arange(0, D, 2, device=x.device, dtype=torch.float32) / D)
+        ang = pos.float()[..., None] * inv
+        cos = torch.cat([ang.cos(), ang.cos()], -1)[..., None, :]
+        sin = torch.cat([ang.sin(), ang.sin()], -1)[..., None, :]
+        rot = torch.cat([-x[..., D // 2:], x[..., : D // 2]], -1)
+        return x * cos + rot * sin
+
+    h = tm.embed[tokens.reshape(-1).long()].float()
+    for li, L in enumerate(tm.layers):
+        x = rms(h, L["attn_norm"])
+        qkv = (x @ W(L["wqkv"])).view(B, N, Hq + 2 * Hkv, hd)
+        q = rope(qkv[:, :, :Hq], positions)
+        k = rope(qkv[:, :, Hq:Hq + Hkv], positions)
+        v = qkv[:, :, Hq + Hkv:]
+        o = torch.empty(B, N, Hq, hd, device=tokens.device)
+        for b in range(B):
+            ctx = int(base[b])
+            pos = torch.arange(ctx, device=tokens.device)
+            blk = tables[b].long()[pos // bs]
+            kc = kv.key_pool[blk, li][torch.arange(ctx), :, pos % bs].float()
+            vc = kv.value_pool[blk, li][torch.arange(ctx), :, pos % bs].float()
+            kk = torch.cat([kc, k[b]], 0)
+            vv = torch.cat([vc, v[b]], 0)
+            mask = torch.ones(N, ctx + N, dtype=torch.bool, device=tokens.device)
+            mask[:, ctx:] = allow
+            for hh in range(Hq):
+                sc = (q[b, :, hh] @ kk[:, hh // G].T) / math.sqrt(hd)
+                sc = sc.masked_fill(~mask, float("-inf"))
+                o[b, :, hh] = torch.softmax(sc, -1) @ vv[:, hh // G]
+        h = h + o.reshape(B * N, Hq * hd) @ W(L["wo"])
+        x = rms(h, L["ffn_norm"])
+        gu = x @ W(L["wgu"])
+        h = h + (torch.nn.functional.silu(gu[:, : s.ffn]) * gu[:, s.ffn:]) @ W(L["wdown"])
+    h = rms(h, tm.norm)
+    return (h @ tm.lm_head.float()).view(B, N, s.vocab)
+
+
+def test_target_tree_forward_vs_fp32(device):
+    B, ctx0, N = 3, 50, 15
+    tm = TargetModel(SMALL_T, device, seed=3)
+    dm = DraftModel(SMALL_D, device, B, max_slots=ctx0 + 64 + 64)
+    sp = TreeSpeculator(tm, dm, B, ctx0, depth=3, temperature=1.0, max_steps=8, seed=4)
+    sp.ctx = [50, 37, 45]
+    for b in range(B):
+        sp.kv.truncate_sequence(b, sp.ctx[b])
+    base = torch.tensor(sp.ctx, dtype=torch.int32, device=device)
+    tokens = torch.randint(0, SMALL_T.vocab, (B, N), device=device, dtype=torch.int32)
+    for b in range(B):
+        sp.kv.append_tokens(b, N)
+    desc = sp.kv.prepare_batch_metadata(list(range(B)))
+    pos = base[:, None] + sp.depths[None, :]
+    want = _ref_forward(tm, tokens, pos, sp.kv, desc.block_tables, base, N)
+    got = tm.forward_tree(tokens, pos, sp.kv, desc.block_tables, base, sp.masks, max(sp.ctx) + N)
+    torch.cuda.synchronize()
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    assert err <= 3e-2 * max(1.0, scale), (err, scale)
+
+
+@pytest.mark.parametrize("mode", ["cpp", "greedy"])
+def test_steps_bookkeeping(device, mode):
+    B, ctx0 = 4, 40
+    tm = TargetModel(SMALL_T, device, seed=5)
+    dm = DraftModel(SMALL_D, device, B, max_slots=ctx0 + 64 + 8 * 8)
+    sp = TreeSpeculator(tm, dm, B, ctx0, depth=3, temperature=0.8, mode=mode, max_steps=8, seed=6)
+    for _ in range(3):
+        ctx_before = list(sp.ctx)
+        base = torch.tensor(ctx_before, dtype=torch.int32, device=device)
+        r = sp.step()
+        torch.cuda.synchronize()
+        for b in range(B):
+            L = r.path_len[b]
+            assert 1 <= L <= sp.depth + 1
+            assert sp.ctx[b] == ctx_before[b] + L
+            assert sp.kv.context_length(b) == sp.ctx[b]
+            assert len(sp.kv.get_block_table(b)) == -(-sp.ctx[b] // 16)
+            assert len(r.emitted[b]) == L and r.emitted[b][-1] == r.final[b]
+        assert sp.root.tolist() == r.final

@@ -1,0 +1,77 @@
+"""GPU tier: W4A16 dequantisation (cfa_w4a16_dequant) bit-exact against a
+numpy restatement of the reference formula (int4_gemm_dequant.cu:20-31,
+int4_dequant_triton.py:74-78), and the reference's own GEMM parity test
+(tests/unit/test_int4_dequant.py:18-53: atol = rtol = 1e-2 against an fp16
+dequantised matmul)."""
+import numpy as np
+import pytest
+import torch
+
+from cudaforge_amd.w4a16 import int4_gemm_dequant, pack_int4_weights, w4a16_dequant
+
+pytestmark = pytest.mark.gpu
+
+
+def _np_dequant(w_int4, scales, zeros, group, dtype):
+    """fp16: (fp16(n) - z) * s with each operation rounded to fp16 (the fp32
+    result of a difference or product of these fp16 operands is exact, so one
+    rounding to fp16 is the correctly rounded fp16 operation); bf16: the fp32
+    value (n - z) * s rounded to nearest even."""
+    K, N = w_int4.shape
+    g = np.arange(K) // group
+    s = scales[g].astype(np.float32)
+    n = w_int4.astype(np.float32)
+    if dtype == "fp16":
+        z = zeros[g].astype(np.float32) if zeros is not None else np.zeros_like(s)
+        d = (n - z).astype(np.float16).astype(np.float32)
+        return (d * s).astype(np.float16)
+    z = zeros[g].astype(np.float32) if zeros is not None else 0.0
+    f = ((n - z) * s).astype(np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return r
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("with_zeros", [False, True])
+@pytest.mark.parametrize("K,N,group", [(128, 256, 128), (512, 96, 64), (1024, 48, 128)])
+def test_dequant_bit_exact(device, dtype, with_zeros, K, N, group):
+    g = torch.Generator().manual_seed(K + N)
+    w = torch.randint(0, 16, (K, N), generator=g, dtype=torch.int32)
+    scales = (torch.rand(K // group, N, generator=g) * 0.1 + 1e-3).half()
+    zeros = torch.randint(0, 16, (K // group, N), generator=g).half() if with_zeros else None
+    q = pack_int4_weights(w)
+    out = w4a16_dequant(q.to(device), scales.to(device),
+                        zeros.to(device) if zeros is not None else None, group_size=group,
+                        dtype=torch.float16 if dtype == "fp16" else torch.bfloat16)
+    want = _np_dequant(w.numpy(), scales.numpy(), zeros.numpy() if zeros is not None else None,
+                       group, dtype)
+    got = out.cpu().view(torch.int16).numpy().view(np.uint16)
+    exp = want.view(np.uint16)
+    assert np.array_equal(got, exp)
+
+
+def test_pack_layout_known_answer():
+    w = torch.arange(16, dtype=torch.int32).reshape(16, 1) % 16
+    q = pack_int4_weights(w)
+    assert q.shape == (2, 1)
+    assert q[0, 0].item() == 0x76543210
+    assert q[1, 0].item() == np.int32(np.uint32(0xFEDCBA98)).item()
+
+
+@pytest.mark.parametrize("M", [16, 64])
+@pytest.mark.parametrize("N", [128, 256])
+@pytest.mark.parametrize("K", [128, 512])
+def test_reference_gemm_parity(device, M, N, K):
+    group = 128
+    torch.manual_seed(42)
+    a = torch.randn((M, K), dtype=torch.float16, device=device)
+    w_int4 = torch.randint(0, 16, (K, N), device=device, dtype=torch.int32)
+    scales = torch.randn((K // group, N), dtype=torch.float16, device=device).abs() * 0.1
+    b_quant = pack_int4_weights(w_int4)
+    w_dequant = torch.zeros((K, N), dtype=torch.float16, device=device)
+    for k in range(K):
+        w_dequant[k, :] = w_int4[k, :].to(torch.float16) * scales[k // group, :]
+    c_ref = torch.matmul(a, w_dequant)
+    c = int4_gemm_dequant(a, b_quant, scales, group_size=group)
+    torch.testing.assert_close(c, c_ref, atol=1e-2, rtol=1e-2)
