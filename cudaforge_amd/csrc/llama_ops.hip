@@ -1,0 +1,293 @@
+// llama_ops.hip -- fused element-wise layers around the verify step's
+// attention: residual add + RMSNorm, rotary embedding fused with the KV-cache
+// write, and SiLU-gated product.  All bf16 in HBM with fp32 arithmetic; each
+// replaces a chain of PyTorch kernels with one pass over the activations.
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+
+#include "abi_internal.hpp"
+
+namespace cfa {
+namespace ops {
+
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// ---------------------------------------------------------------------------
+// h <- bf16(h + delta) (when delta is given); out <- bf16(h * rsqrt(mean(h^2)
+// + eps) * w).  One work-group per row, 8 elements (16 bytes) per access.
+// ---------------------------------------------------------------------------
+constexpr int kNormNT = 256;
+
+__global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(uint16_t *h, const uint16_t *delta,
+                                                          const uint16_t *w, uint16_t *out, int d,
+                                                          float eps) {
+  const long long row = blockIdx.x;
+  uint16_t *hr = h + row * d;
+  const uint16_t *dr = delta ? delta + row * d : nullptr;
+  uint16_t *orow = out + row * d;
+  const int nvec = d / 8;
+  float ss = 0.0f;
+  for (int v = threadIdx.x; v < nvec; v += kNormNT) {
+    uint4 x = reinterpret_cast<const uint4 *>(hr)[v];
+    if (dr) {
+      const uint4 y = reinterpret_cast<const uint4 *>(dr)[v];
+      uint32_t *xs = reinterpret_cast<uint32_t *>(&x);
+      const uint32_t *ys = reinterpret_cast<const uint32_t *>(&y);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a0 = bf2f(xs[q] & 0xffff) + bf2f(ys[q] & 0xffff);
+        const float a1 = bf2f(xs[q] >> 16) + bf2f(ys[q] >> 16);
+        xs[q] = (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16);
+      }
+      reinterpret_cast<uint4 *>(hr)[v] = x;
+    }
+    const uint32_t *xs = reinterpret_cast<const uint32_t *>(&x);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float a0 = bf2f(xs[q] & 0xffff), a1 = bf2f(xs[q] >> 16);
+      ss += a0 * a0 + a1 * a1;
+    }
+  }
+  __shared__ float red[kNormNT / 64];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormNT / 64; ++i) tot += red[i];
+  const float inv = rsqrtf(tot / (float)d + eps);
+  for (int v = threadIdx.x; v < nvec; v += kNormNT) {
+    const uint4 x = reinterpret_cast<const uint4 *>(hr)[v];  // own writes, same thread
+    const uint4 g = reinterpret_cast<const uint4 *>(w)[v];
+    const uint32_t *xs = reinterpret_cast<const uint32_t *>(&x);
+    const uint32_t *gs = reinterpret_cast<const uint32_t *>(&g);
+    uint4 o;
+    uint32_t *os = reinterpret_cast<uint32_t *>(&o);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float a0 = bf2f(xs[q] & 0xffff) * inv * bf2f(gs[q] & 0xffff);
+      const float a1 = bf2f(xs[q] >> 16) * inv * bf2f(gs[q] >> 16);
+      os[q] = (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16);
+    }
+    reinterpret_cast<uint4 *>(orow)[v] = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Rotary embedding (rotate-half pairs (i, i + D/2), angle pos * theta^(-2i/D))
+// of the q and k heads of a fused [M, Hq + 2 Hkv, D] projection, fused with
+// the write of k and v into the KV cache:
+//   q_out [M, Hq, D] (contiguous);
+//   paged cache (kind 0): token m = b * n + j goes to slot base[b] + j of
+//     pool[block][layer][kv_head][slot_in_block][D], block =
+//     block_tables[b][slot / bs] (an unmapped page, -1 or past max_blocks,
+//     is skipped);
+//   strided cache (kind 1): k to kc + b*k_sb + h*k_sh + slot*k_ss + e*k_se,
+//     v to vc + b*v_sb + h*v_sh + slot*v_ss + e (slot = slots[m]).
+// One thread per (token, head, rotation pair).
+// ---------------------------------------------------------------------------
+struct RopeArgs {
+  const uint16_t *qkv;
+  const int32_t *pos;   // [M]
+  uint16_t *q_out;
+  uint16_t *kc, *vc;
+  int M, n, Hq, Hkv, D;
+  float log2_theta;
+  int kind;
+  // paged
+  const int32_t *block_tables;
+  int max_blocks, bs, layer;
+  const int32_t *base;
+  long long blk_stride, layer_stride, head_stride;  // elements
+  // strided
+  const int32_t *slots;  // [M]
+  long long k_sb, k_sh, k_ss, k_se, v_sb, v_sh, v_ss;
+};
+
+__global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
+  const int half = a.D / 2;
+  const int H = a.Hq + 2 * a.Hkv;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long total = (long long)a.M * (a.Hq + a.Hkv) * half;
+  const long long tv = (long long)a.M * a.Hkv * a.D;
+  if (t >= total + tv) return;
+  if (t >= total) {  // v copy: one element per thread
+    const long long r = t - total;
+    const int e = (int)(r % a.D);
+    const int h = (int)((r / a.D) % a.Hkv);
+    const int m = (int)(r / ((long long)a.D * a.Hkv));
+    const uint16_t val = a.qkv[((long long)m * H + a.Hq + a.Hkv + h) * a.D + e];
+    const int b = m / a.n, j = m % a.n;
+    if (a.kind == 0) {
+      const int slot = a.base[b] + j;
+      if (slot / a.bs >= a.max_blocks) return;
+      const long long blk = a.block_tables[(long long)b * a.max_blocks + slot / a.bs];
+      if (blk < 0) return;  // unmapped page: never written
+      a.vc[blk * a.blk_stride + a.layer * a.layer_stride + h * a.head_stride +
+           (long long)(slot % a.bs) * a.D + e] = val;
+    } else {
+      const long long slot = a.slots[m];
+      a.vc[b * a.v_sb + h * a.v_sh + slot * a.v_ss + e] = val;
+    }
+    return;
+  }
+  const int i = (int)(t % half);
+  const int hh = (int)((t / half) % (a.Hq + a.Hkv));
+  const int m = (int)(t / ((long long)half * (a.Hq + a.Hkv)));
+  const uint16_t *src = a.qkv + ((long long)m * H + hh) * a.D;
+  const float x0 = bf2f(src[i]), x1 = bf2f(src[i + half]);
+  const float inv_freq = exp2f(-(float)(2 * i) / (float)a.D * a.log2_theta);
+  const float ang = (float)a.pos[m] * inv_freq;
+  float sn, cs;
+  sincosf(ang, &sn, &cs);
+  const uint16_t y0 = f2bf(x0 * cs - x1 * sn);
+  const uint16_t y1 = f2bf(x1 * cs + x0 * sn);
+  if (hh < a.Hq) {
+    uint16_t *dst = a.q_out + ((long long)m * a.Hq + hh) * a.D;
+    dst[i] = y0;
+    dst[i + half] = y1;
+    return;
+  }
+  const int h = hh - a.Hq;
+  const int b = m / a.n, j = m % a.n;
+  if (a.kind == 0) {
+    const int slot = a.base[b] + j;
+    if (slot / a.bs >= a.max_blocks) return;
+    const long long blk = a.block_tables[(long long)b * a.max_blocks + slot / a.bs];
+    if (blk < 0) return;
+    uint16_t *dst = a.kc + blk * a.blk_stride + a.layer * a.layer_stride + h * a.head_stride +
+                    (long long)(slot % a.bs) * a.D;
+    dst[i] = y0;
+    dst[i + half] = y1;
+  } else {
+    const long long slot = a.slots[m];
+    uint16_t *dst = a.kc + b * a.k_sb + h * a.k_sh + slot * a.k_ss;
+    dst[(long long)i * a.k_se] = y0;
+    dst[(long long)(i + half) * a.k_se] = y1;
+  }
+}
+
+// out[m, f] = bf16(bf16(silu(g)) * u) for gu [M, 2F] = [g | u] (the rounding
+// of silu(g) * u in two bf16 PyTorch ops).
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *gu, uint16_t *out, int M,
+                                                       int F) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)M * F) return;
+  const long long m = t / F, f = t % F;
+  const float g = bf2f(gu[m * 2 * F + f]);
+  const float u = bf2f(gu[m * 2 * F + F + f]);
+  const float s = bf2f(f2bf(g / (1.0f + expf(-g))));
+  out[t] = f2bf(s * u);
+}
+
+}  // namespace ops
+}  // namespace cfa
+
+using namespace cfa::ops;
+
+extern "C" int cfa_rmsnorm(void *h, const void *delta, const void *weight, void *out, int M, int d,
+                           float eps, void *stream) {
+  using namespace cfa::abi;
+  clear_error();
+  if (M <= 0 || d <= 0 || d % 8 != 0) return fail_arg("M > 0 and d a positive multiple of 8");
+  if (!h || !weight || !out) return fail_arg("null pointer");
+  if ((((uintptr_t)h | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)delta) & 15) != 0)
+    return fail_arg("rows must be 16-byte aligned");
+  CFA_LAUNCH("rmsnorm", rmsnorm_kernel, dim3(M), dim3(kNormNT), 0, (hipStream_t)stream,
+             (uint16_t *)h, (const uint16_t *)delta, (const uint16_t *)weight, (uint16_t *)out, d,
+             eps);
+  return CFA_OK;
+}
+
+extern "C" int cfa_rope_kv_paged(const void *qkv, const int32_t *positions, int B, int n, int Hq,
+                                 int Hkv, int D, float theta, void *q_out, void *k_pool,
+                                 void *v_pool, int layer, int num_layers, int block_size,
+                                 const int32_t *block_tables, int max_blocks,
+                                 const int32_t *base_lens, void *stream) {
+  using namespace cfa::abi;
+  clear_error();
+  if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || D % 2) return fail_arg("bad shape");
+  if (layer < 0 || layer >= num_layers || block_size <= 0) return fail_arg("bad layer or block size");
+  if (!qkv || !positions || !q_out || !k_pool || !v_pool || !block_tables || !base_lens)
+    return fail_arg("null pointer");
+  RopeArgs a{};
+  a.qkv = (const uint16_t *)qkv;
+  a.pos = positions;
+  a.q_out = (uint16_t *)q_out;
+  a.kc = (uint16_t *)k_pool;
+  a.vc = (uint16_t *)v_pool;
+  a.M = B * n;
+  a.n = n;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.D = D;
+  a.log2_theta = log2f(theta);
+  a.kind = 0;
+  a.block_tables = block_tables;
+  a.max_blocks = max_blocks;
+  a.bs = block_size;
+  a.layer = layer;
+  a.base = base_lens;
+  a.head_stride = (long long)block_size * D;
+  a.layer_stride = (long long)Hkv * a.head_stride;
+  a.blk_stride = (long long)num_layers * a.layer_stride;
+  const long long total = (long long)a.M * (Hq + Hkv) * (D / 2) + (long long)a.M * Hkv * D;
+  CFA_LAUNCH("rope_kv", rope_kv_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+             (hipStream_t)stream, a);
+  return CFA_OK;
+}
+
+extern "C" int cfa_rope_kv_strided(const void *qkv, const int32_t *positions, int B, int n, int Hq,
+                                   int Hkv, int D, float theta, void *q_out, void *k_cache,
+                                   const int64_t *k_strides, void *v_cache,
+                                   const int64_t *v_strides, const int32_t *slots, void *stream) {
+  using namespace cfa::abi;
+  clear_error();
+  if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || D % 2) return fail_arg("bad shape");
+  if (!qkv || !positions || !q_out || !k_cache || !v_cache || !slots || !k_strides || !v_strides)
+    return fail_arg("null pointer");
+  if (v_strides[3] != 1) return fail_arg("v rows must be contiguous");
+  RopeArgs a{};
+  a.qkv = (const uint16_t *)qkv;
+  a.pos = positions;
+  a.q_out = (uint16_t *)q_out;
+  a.kc = (uint16_t *)k_cache;
+  a.vc = (uint16_t *)v_cache;
+  a.M = B * n;
+  a.n = n;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.D = D;
+  a.log2_theta = log2f(theta);
+  a.kind = 1;
+  a.slots = slots;
+  a.k_sb = k_strides[0];
+  a.k_sh = k_strides[1];
+  a.k_ss = k_strides[2];
+  a.k_se = k_strides[3];
+  a.v_sb = v_strides[0];
+  a.v_sh = v_strides[1];
+  a.v_ss = v_strides[2];
+  const long long total = (long long)a.M * (Hq + Hkv) * (D / 2) + (long long)a.M * Hkv * D;
+  CFA_LAUNCH("rope_kv", rope_kv_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+             (hipStream_t)stream, a);
+  return CFA_OK;
+}
+
+extern "C" int cfa_silu_mul(const void *gu, void *out, int M, int F, void *stream) {
+  using namespace cfa::abi;
+  clear_error();
+  if (M <= 0 || F <= 0) return fail_arg("bad shape");
+  if (!gu || !out) return fail_arg("null pointer");
+  const long long total = (long long)M * F;
+  CFA_LAUNCH("silu_mul", silu_mul_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+             (hipStream_t)stream, (const uint16_t *)gu, (uint16_t *)out, M, F);
+  return CFA_OK;
+}

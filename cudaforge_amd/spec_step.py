@@ -26,6 +26,7 @@ for K, so the score product reads a contiguous operand) because its head size
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import List, Optional
@@ -33,10 +34,11 @@ from typing import List, Optional
 import numpy as np
 import torch
 
+from . import _lib
 from . import tree as T
 from .kv_cache import KVCacheConfig, PagedKVCache
 from .sampling import expand_tree_level
-from .verify import tree_attention, tree_attention_workspace_bytes, tree_verify
+from .verify import _stream_ptr, tree_attention, tree_attention_workspace_bytes, tree_verify
 from .w4a16 import W4A16Linear
 
 __all__ = ["LlamaShape", "TARGET_8B", "DRAFT_1B", "TargetModel", "DraftModel", "TreeSpeculator",
@@ -64,21 +66,53 @@ DRAFT_1B = LlamaShape(16, 2048, 32, 8, 64, 8192, 128256)
 # shared pieces
 # ---------------------------------------------------------------------------
 
-def _rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(x.dtype)
+def rmsnorm_(h: torch.Tensor, delta: Optional[torch.Tensor], w: torch.Tensor, eps: float,
+             out: torch.Tensor) -> torch.Tensor:
+    """h += delta (bf16, in place) when delta is given; out = RMSNorm(h) * w
+    (cfa_rmsnorm)."""
+    M, d = h.shape
+    rc = _lib.load().cfa_rmsnorm(h.data_ptr(), delta.data_ptr() if delta is not None else None,
+                                 w.data_ptr(), out.data_ptr(), M, d, float(eps),
+                                 _stream_ptr(h.device))
+    _lib.check(rc, "cfa_rmsnorm")
+    return out
 
 
-def _rope(x: torch.Tensor, pos: torch.Tensor, theta: float) -> torch.Tensor:
-    """Rotate-half rotary embedding; x [..., T, H, D], pos [..., T]."""
-    D = x.shape[-1]
-    inv = theta ** (-torch.arange(0, D, 2, device=x.device, dtype=torch.float32) / D)
-    ang = pos.float()[..., None] * inv                       # [..., T, D/2]
-    cos = torch.cat([ang.cos(), ang.cos()], -1)[..., None, :]
-    sin = torch.cat([ang.sin(), ang.sin()], -1)[..., None, :]
-    xf = x.float()
-    rot = torch.cat([-xf[..., D // 2:], xf[..., : D // 2]], -1)
-    return (xf * cos + rot * sin).to(x.dtype)
+def silu_mul(gu: torch.Tensor) -> torch.Tensor:
+    """[M, 2F] = [g | u] -> silu(g) * u in bf16 (cfa_silu_mul)."""
+    M, F2 = gu.shape
+    out = torch.empty(M, F2 // 2, dtype=gu.dtype, device=gu.device)
+    rc = _lib.load().cfa_silu_mul(gu.data_ptr(), out.data_ptr(), M, F2 // 2, _stream_ptr(gu.device))
+    _lib.check(rc, "cfa_silu_mul")
+    return out
+
+
+def rope_kv_paged(qkv: torch.Tensor, pos: torch.Tensor, B: int, n: int, s: "LlamaShape",
+                  q_out: torch.Tensor, kv: PagedKVCache, layer: int, block_tables: torch.Tensor,
+                  base: torch.Tensor) -> None:
+    """Rotary embedding of q and k from qkv [B*n, (Hq+2Hkv)*D]; q -> q_out,
+    k and v -> slots base + j of `layer` in the paged pools."""
+    cfg = kv.get_config()
+    rc = _lib.load().cfa_rope_kv_paged(
+        qkv.data_ptr(), pos.data_ptr(), B, n, s.n_heads, s.n_kv_heads, s.head_dim,
+        float(s.rope_theta), q_out.data_ptr(), kv.key_pool.data_ptr(), kv.value_pool.data_ptr(),
+        layer, cfg.num_layers, cfg.block_size, block_tables.data_ptr(), block_tables.shape[1],
+        base.data_ptr(), _stream_ptr(qkv.device))
+    _lib.check(rc, "cfa_rope_kv_paged")
+
+
+def rope_kv_strided(qkv: torch.Tensor, pos: torch.Tensor, B: int, n: int, s: "LlamaShape",
+                    q_out: torch.Tensor, kT: torch.Tensor, v: torch.Tensor,
+                    slots: torch.Tensor) -> None:
+    """As rope_kv_paged into a contiguous cache: kT [B, Hkv, D, S] (K stored
+    transposed), v [B, Hkv, S, D], slot of token (b, j) = slots[b, j]."""
+    ks = (ctypes.c_int64 * 4)(kT.stride(0), kT.stride(1), kT.stride(3), kT.stride(2))
+    vs = (ctypes.c_int64 * 4)(v.stride(0), v.stride(1), v.stride(2), v.stride(3))
+    rc = _lib.load().cfa_rope_kv_strided(
+        qkv.data_ptr(), pos.data_ptr(), B, n, s.n_heads, s.n_kv_heads, s.head_dim,
+        float(s.rope_theta), q_out.data_ptr(), kT.data_ptr(), ks, v.data_ptr(), vs,
+        slots.data_ptr(), _stream_ptr(qkv.device))
+    _lib.check(rc, "cfa_rope_kv_strided")
 
 
 def _randn(shape, gen, device, scale=1.0, dtype=torch.bfloat16):
@@ -128,24 +162,25 @@ class TargetModel:
         need = tree_attention_workspace_bytes(B, N, Hq, Hkv, hd, max_keys)
         if self.attn_ws is None or self.attn_ws.numel() < need:
             self.attn_ws = torch.empty(max(need, 1), dtype=torch.uint8, device=tokens.device)
-        h = self.embed[tokens.reshape(-1).long()]               # [B*N, d]
+        M = B * N
+        pos = positions.reshape(-1).to(torch.int32).contiguous()
+        base_i = base_lens.to(torch.int32).contiguous()
+        h = self.embed[tokens.reshape(-1).long()]               # [B*N, d], a copy
+        x = torch.empty_like(h)
+        q = torch.empty(B, N, Hq, hd, dtype=torch.bfloat16, device=tokens.device)
+        delta = None
         for li, L in enumerate(self.layers):
-            x = _rmsnorm(h, L["attn_norm"], s.eps)
-            qkv = L["wqkv"](x, self.scratch).view(B, N, Hq + 2 * Hkv, hd)
-            q = _rope(qkv[:, :, :Hq], positions, s.rope_theta)
-            k = _rope(qkv[:, :, Hq:Hq + Hkv], positions, s.rope_theta)
-            v = qkv[:, :, Hq + Hkv:]
-            kv.key_pool[blk, li, :, off, :] = k.reshape(B * N, Hkv, hd)
-            kv.value_pool[blk, li, :, off, :] = v.reshape(B * N, Hkv, hd)
-            o = tree_attention(q.contiguous(), kv.key_pool, kv.value_pool, block_tables, base_lens,
-                               masks, layer=li, max_keys=max_keys, workspace=self.attn_ws)
-            h = h + L["wo"](o.reshape(B * N, Hq * hd), self.scratch)
-            x = _rmsnorm(h, L["ffn_norm"], s.eps)
-            gu = L["wgu"](x, self.scratch)
-            a = torch.nn.functional.silu(gu[:, : s.ffn]) * gu[:, s.ffn:]
-            h = h + L["wdown"](a, self.scratch)
-        h = _rmsnorm(h, self.norm, s.eps)
-        return (h @ self.lm_head).float().view(B, N, s.vocab)
+            rmsnorm_(h, delta, L["attn_norm"], s.eps, x)         # h += delta; x = norm(h)
+            qkv = L["wqkv"](x, self.scratch)
+            rope_kv_paged(qkv, pos, B, N, s, q, kv, li, block_tables, base_i)
+            o = tree_attention(q, kv.key_pool, kv.value_pool, block_tables, base_lens, masks,
+                               layer=li, max_keys=max_keys, workspace=self.attn_ws)
+            delta = L["wo"](o.reshape(M, Hq * hd), self.scratch)
+            rmsnorm_(h, delta, L["ffn_norm"], s.eps, x)
+            a = silu_mul(L["wgu"](x, self.scratch))
+            delta = L["wdown"](a, self.scratch)
+        rmsnorm_(h, delta, self.norm, s.eps, x)
+        return (x @ self.lm_head).float().view(B, N, s.vocab)
 
 
 # ---------------------------------------------------------------------------
@@ -185,32 +220,31 @@ class DraftModel:
         B, n = tokens.shape
         hd, Hq, Hkv = s.head_dim, s.n_heads, s.n_kv_heads
         G = Hq // Hkv
-        bidx = torch.arange(B, device=tokens.device)[:, None].expand(B, n)
         bias = torch.zeros(visible.shape, dtype=torch.float32, device=tokens.device)
         bias.masked_fill_(~visible, float("-inf"))
+        pos = positions.reshape(-1).to(torch.int32).contiguous()
+        sl = slots.reshape(-1).to(torch.int32).contiguous()
+        S = self.max_slots
         h = self.embed[tokens.reshape(-1).long()]
+        x = torch.empty_like(h)
+        q = torch.empty(B * n, Hq, hd, dtype=torch.bfloat16, device=tokens.device)
+        delta = None
         for li, L in enumerate(self.layers):
-            x = _rmsnorm(h, L["attn_norm"], s.eps)
-            qkv = (x @ L["wqkv"]).view(B, n, Hq + 2 * Hkv, hd)
-            q = _rope(qkv[:, :, :Hq], positions, s.rope_theta)
-            k = _rope(qkv[:, :, Hq:Hq + Hkv], positions, s.rope_theta)
-            v = qkv[:, :, Hq + Hkv:]
-            self.kT[li][bidx, :, :, slots] = k                   # [B, n, Hkv, hd]
-            self.v[li][bidx, :, slots, :] = v
-            # scores [B, Hkv, G*n, keys]: q grouped by KV head, K^T contiguous
+            rmsnorm_(h, delta, L["attn_norm"], s.eps, x)
+            qkv = x @ L["wqkv"]
+            rope_kv_strided(qkv, pos, B, n, s, q, self.kT[li], self.v[li], sl)
+            # scores [B, Hkv, G*n, S]: q grouped by KV head, K^T contiguous
             qg = q.view(B, n, Hkv, G, hd).permute(0, 2, 3, 1, 4).reshape(B, Hkv, G * n, hd)
-            S = self.max_slots
-            sc = torch.matmul(qg.contiguous(), self.kT[li]).float()
+            sc = torch.matmul(qg, self.kT[li]).float()
             sc = sc.view(B, Hkv, G, n, S) * (1.0 / math.sqrt(hd)) + bias[:, None, None]
             p = torch.softmax(sc, dim=-1).to(torch.bfloat16).view(B, Hkv, G * n, S)
             o = torch.matmul(p, self.v[li])                       # [B, Hkv, G*n, hd]
             o = o.view(B, Hkv, G, n, hd).permute(0, 3, 1, 2, 4).reshape(B * n, Hq * hd)
-            h = h + o @ L["wo"]
-            x = _rmsnorm(h, L["ffn_norm"], s.eps)
-            gu = x @ L["wgu"]
-            h = h + (torch.nn.functional.silu(gu[:, : s.ffn]) * gu[:, s.ffn:]) @ L["wdown"]
-        h = _rmsnorm(h, self.norm, s.eps)
-        return (h @ self.lm_head).float().view(B, n, s.vocab)
+            delta = o @ L["wo"]
+            rmsnorm_(h, delta, L["ffn_norm"], s.eps, x)
+            delta = silu_mul(x @ L["wgu"]) @ L["wdown"]
+        rmsnorm_(h, delta, self.norm, s.eps, x)
+        return (x @ self.lm_head).float().view(B, n, s.vocab)
 
     def commit(self, base: torch.Tensor, paths: torch.Tensor, path_lens: List[int]) -> None:
         """Move the accepted nodes (slot base + node) to base + j, as

@@ -243,6 +243,36 @@ int cfa_w4a16_dequant(const uint32_t *b_quant, const void *scales, const void *z
                       int N, int group_size, int out_bf16, void *out, void *stream);
 
 /* ---------------------------------------------------------------------------
+ * Fused layers of the model-scale verify step (bf16 activations, fp32 math;
+ * no counterpart in the reference, whose model runner is out of this
+ * library's scope).
+ *
+ * cfa_rmsnorm: h <- bf16(h + delta) when delta != NULL, then out <- bf16(h *
+ *   rsqrt(mean(h^2) + eps) * weight); h, delta, out [M, d], weight [d];
+ *   d % 8 == 0, 16-byte aligned rows.
+ * cfa_rope_kv_paged / _strided: rotate-half rotary embedding (angle pos *
+ *   theta^(-2i/D)) of the q and k heads of qkv [B*n, Hq + 2*Hkv, D]; writes
+ *   q_out [B*n, Hq, D] and stores k (rotated) and v in the KV cache: paged
+ *   pools [blocks][num_layers][Hkv][block_size][D] at slot base_lens[b] + j of
+ *   `layer` (pages from block_tables [B, max_blocks]; an unmapped page is
+ *   skipped); or strided caches at k_cache + b*ks[0] + h*ks[1] + slot*ks[2] +
+ *   e*ks[3] (v likewise, with vs[3] == 1), slot = slots[b*n + j].
+ *   positions [B*n].
+ * cfa_silu_mul: out [M, F] = bf16(bf16(silu(g)) * u) for gu [M, 2F] = [g | u].
+ */
+int cfa_rmsnorm(void *h, const void *delta, const void *weight, void *out, int M, int d,
+                float eps, void *stream);
+int cfa_rope_kv_paged(const void *qkv, const int32_t *positions, int B, int n, int Hq, int Hkv,
+                      int D, float theta, void *q_out, void *k_pool, void *v_pool, int layer,
+                      int num_layers, int block_size, const int32_t *block_tables, int max_blocks,
+                      const int32_t *base_lens, void *stream);
+int cfa_rope_kv_strided(const void *qkv, const int32_t *positions, int B, int n, int Hq, int Hkv,
+                        int D, float theta, void *q_out, void *k_cache, const int64_t *k_strides,
+                        void *v_cache, const int64_t *v_strides, const int32_t *slots,
+                        void *stream);
+int cfa_silu_mul(const void *gu, void *out, int M, int F, void *stream);
+
+/* ---------------------------------------------------------------------------
  * Paged KV cache page tables (host metadata).
  *
  * Replaces the metadata half of PagedKVCache (paged_kv_cache.h:36-179,
