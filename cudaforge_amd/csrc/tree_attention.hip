@@ -43,7 +43,8 @@
 // Softmax rescaling is lazy: a column's exponent base b only moves when its
 // running maximum exceeds it by more than kRescaleSlack (log2 units), so P^T
 // entries stay below 2^kRescaleSlack and the O^T rescale is rare.  Splits of
-// the key range are merged by a log-sum-exp pass.
+// the key range write normalised bf16 partials with their (base, sum), merged
+// by a log-sum-exp pass.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -87,7 +88,7 @@ struct Args {
   const uint64_t *mask;    // [N] or [B, N]
   long long mask_sb;
   uint16_t *out;           // [B, N, Hq, D]
-  float *part_o;           // [S, B, Hkv, rows, D] unnormalised partial outputs
+  uint16_t *part_o;        // [S, B, Hkv, rows, D] partial outputs O / l, bf16
   float2 *part_ml;         // [S, B, Hkv, rows] (exponent base in log2 units, sum)
   int B, N, Hq, Hkv, G, rows;
   int max_blocks, num_blocks, num_layers, layer, bs;
@@ -539,21 +540,31 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
         *reinterpret_cast<uint2 *>(op + dt * 16 + 4 * g) = w;
       }
     } else {
+      // normalised partial in bf16 (the merge weighs it by its sum l)
       const long long prow = (((long long)split * a.B + b) * a.Hkv + h) * a.rows + r;
-      float *pp = a.part_o + prow * kD;
+      uint16_t *pp = a.part_o + prow * kD;
+      const float inv = (ls > 0.0f) ? 1.0f / ls : 0.0f;
 #pragma unroll
-      for (int dt = 0; dt < kD / 16; ++dt)
-        *reinterpret_cast<f32x4 *>(pp + dt * 16 + 4 * g) = o[qt][dt];
+      for (int dt = 0; dt < kD / 16; ++dt) {
+        uint2 w;
+        w.x = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(o[qt][dt][0] * inv)) |
+              ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(o[qt][dt][1] * inv)) << 16);
+        w.y = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(o[qt][dt][2] * inv)) |
+              ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(o[qt][dt][3] * inv)) << 16);
+        *reinterpret_cast<uint2 *>(pp + dt * 16 + 4 * g) = w;
+      }
       if (g == 0) a.part_ml[prow] = make_float2(sm.valid[qt] ? sm.b[qt] : -INFINITY, ls);
     }
   }
 }
 
-// Log-sum-exp merge of the splits: 32 threads per query row, four d-values
-// (one 16-byte load per split) per thread, eight rows per work-group.
+// Log-sum-exp merge of the splits: out = sum_s w_s l_s o_s / sum_s w_s l_s
+// with w_s = 2^(m_s - max m) and o_s the normalised bf16 partial; 16 threads
+// per query row, eight d-values (one 16-byte load per split) per thread,
+// sixteen rows per work-group.
 __global__ __launch_bounds__(256) void tree_merge_kernel(Args a) {
-  const long long row_g = (long long)blockIdx.x * 8 + (threadIdx.x >> 5);
-  const int q4 = threadIdx.x & 31;
+  const long long row_g = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int q8 = threadIdx.x & 15;
   const long long total = (long long)a.B * a.Hkv * a.rows;
   if (row_g >= total) return;
   const int r = (int)(row_g % a.rows);
@@ -565,25 +576,31 @@ __global__ __launch_bounds__(256) void tree_merge_kernel(Args a) {
   for (int s = 0; s < a.splits; ++s) M = fmaxf(M, a.part_ml[prow0 + s * split_stride].x);
   const float base = (M == -INFINITY) ? 0.0f : M;
   float L = 0.0f;
-  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
   for (int s = 0; s < a.splits; ++s) {
     const long long prow = prow0 + s * split_stride;
     const float2 ml = a.part_ml[prow];
-    const f32x4 v = *reinterpret_cast<const f32x4 *>(a.part_o + prow * kD + 4 * q4);
-    const float w = __builtin_amdgcn_exp2f(ml.x - base);
-    L += ml.y * w;
-    acc += v * w;
+    const uint4 v = *reinterpret_cast<const uint4 *>(a.part_o + prow * kD + 8 * q8);
+    const float w = __builtin_amdgcn_exp2f(ml.x - base) * ml.y;
+    L += w;
+    const uint32_t *vs = reinterpret_cast<const uint32_t *>(&v);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] += w * __uint_as_float(vs[j] << 16);
+      acc[2 * j + 1] += w * __uint_as_float(vs[j] & 0xffff0000u);
+    }
   }
   const float inv = (L > 0.0f) ? 1.0f / L : 0.0f;
   const int node = r / a.G, hg = r % a.G;
   uint16_t *op = a.out + (((long long)b * a.N + node) * a.Hq + (long long)h * a.G + hg) * kD;
-  uint2 w;
-  w.x = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc[0] * inv)) |
-        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc[1] * inv)) << 16);
-  w.y = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc[2] * inv)) |
-        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc[3] * inv)) << 16);
-  *reinterpret_cast<uint2 *>(op + 4 * q4) = w;
+  uint4 w;
+  uint32_t *ws = reinterpret_cast<uint32_t *>(&w);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    ws[j] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc[2 * j] * inv)) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(acc[2 * j + 1] * inv)) << 16);
+  *reinterpret_cast<uint4 *>(op + 8 * q8) = w;
 }
 
 }  // namespace tree
@@ -618,7 +635,7 @@ extern "C" size_t cfa_tree_attention_workspace_size(int B, int N, int n_q_heads,
   const int G = n_q_heads / n_kv_heads;
   const size_t rows = (size_t)G * N;
   const size_t prows = (size_t)splits * B * n_kv_heads * rows;
-  return align256(prows * kD * sizeof(float)) + align256(prows * sizeof(float2));
+  return align256(prows * kD * sizeof(uint16_t)) + align256(prows * sizeof(float2));
 }
 
 extern "C" int cfa_tree_attention(const void *q, const void *k_pool, const void *v_pool,
@@ -674,15 +691,15 @@ extern "C" int cfa_tree_attention(const void *q, const void *k_pool, const void 
     if (!workspace || workspace_bytes < need)
       return fail_arg("workspace too small (see cfa_tree_attention_workspace_size)");
     const size_t prows = (size_t)a.splits * B * n_kv_heads * a.rows;
-    a.part_o = (float *)workspace;
-    a.part_ml = (float2 *)((char *)workspace + align256(prows * kD * sizeof(float)));
+    a.part_o = (uint16_t *)workspace;
+    a.part_ml = (float2 *)((char *)workspace + align256(prows * kD * sizeof(uint16_t)));
   }
   hipStream_t st = (hipStream_t)stream;
   CFA_LAUNCH("tree_attn", tree_attn_kernel, dim3(a.splits, n_kv_heads, B), dim3(kNT), 0, st, a);
   if (a.splits > 1) {
     const long long rows = (long long)B * n_kv_heads * a.rows;
-    CFA_LAUNCH("tree_attn_merge", tree_merge_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0,
-               st, a);
+    CFA_LAUNCH("tree_attn_merge", tree_merge_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256),
+               0, st, a);
   }
   return CFA_OK;
 }
