@@ -203,8 +203,9 @@ def verify_step_8b_leg(dev, steps=6, warmup=2):
     V128256), random-init 1B-shape bf16 draft proposing a 63-node binary tree
     (children drawn from the draft softmax), B=8, context 2048 (synthetic
     N(0,1) K/V), T=1.0; tree attention, sampling, verification and commit
-    on this library's kernels.  Random-init models agree on nothing, so the
-    accepted path is the root alone and verified tok/s = B / step time."""
+    on this library's kernels; the draft levels replay from HIP graphs.
+    Random-init models agree on nothing, so the accepted path is the root
+    alone and verified tok/s = B / step time."""
     import torch
     from cudaforge_amd.spec_step import (DRAFT_1B, TARGET_8B, DraftModel, TargetModel,
                                          TreeSpeculator)
@@ -213,7 +214,7 @@ def verify_step_8b_leg(dev, steps=6, warmup=2):
     tm = TargetModel(TARGET_8B, dev, seed=0)
     dm = DraftModel(DRAFT_1B, dev, Bs, max_slots=ctx + 64 + 8 * (steps + warmup + 2))
     sp = TreeSpeculator(tm, dm, Bs, ctx, depth=5, temperature=1.0, mode="cpp",
-                        max_steps=steps + warmup + 2)
+                        max_steps=steps + warmup + 2, use_graphs=True)
     for _ in range(warmup):
         sp.step()
     torch.cuda.synchronize()

@@ -9,8 +9,9 @@
 //          and without zero points w = fp16(nibble * s), the value
 //          int4_dequant_triton.py:74-78 produces;
 //   bf16:  w = bf16((nibble - z) * s) with the product formed in fp32.
-// One thread per packed word: it reads 4 bytes of weights and one scale and
-// writes 8 outputs down the K column, so the kernel streams at HBM rate.
+// Each thread takes four adjacent packed words (one 16-byte read) and writes
+// 8 rows of four outputs (8-byte stores); a one-word-per-thread kernel covers
+// unaligned or N % 4 != 0 shapes.
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
@@ -35,30 +36,77 @@ __device__ __forceinline__ uint16_t to_bf16_bits(float f) {
   return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);  // round to nearest even
 }
 
-__global__ __launch_bounds__(256) void dequant_kernel(Args a) {
-  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-  const long long words = (long long)(a.K / 8) * a.N;
-  if (idx >= words) return;
-  const int kb = (int)(idx / a.N), n = (int)(idx % a.N);
-  const uint32_t w = a.q[idx];
-  const int g = (kb * 8) / a.group;
-  const __half sh = a.s[(long long)g * a.N + n];
-  const __half zh = a.z ? a.z[(long long)g * a.N + n] : __float2half(0.0f);
+__device__ __forceinline__ void dequant_word(const Args &a, uint32_t w, __half sh, __half zh,
+                                             long long row0, int n) {
   if (a.bf16) {
     uint16_t *o = reinterpret_cast<uint16_t *>(a.out);
     const float sf = __half2float(sh), zf = __half2float(zh);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float nib = (float)((w >> (4 * i)) & 15u);
-      o[(long long)(kb * 8 + i) * a.N + n] = to_bf16_bits((nib - zf) * sf);
+      o[(row0 + i) * a.N + n] = to_bf16_bits((nib - zf) * sf);
     }
   } else {
     __half *o = reinterpret_cast<__half *>(a.out);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const __half nib = __float2half((float)((w >> (4 * i)) & 15u));
-      o[(long long)(kb * 8 + i) * a.N + n] = __hmul(__hsub(nib, zh), sh);
+      o[(row0 + i) * a.N + n] = __hmul(__hsub(nib, zh), sh);
     }
+  }
+}
+
+// One thread per packed word.
+__global__ __launch_bounds__(256) void dequant_kernel(Args a) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long words = (long long)(a.K / 8) * a.N;
+  if (idx >= words) return;
+  const int kb = (int)(idx / a.N), n = (int)(idx % a.N);
+  const int g = (kb * 8) / a.group;
+  const __half sh = a.s[(long long)g * a.N + n];
+  const __half zh = a.z ? a.z[(long long)g * a.N + n] : __float2half(0.0f);
+  dequant_word(a, a.q[idx], sh, zh, (long long)kb * 8, n);
+}
+
+// Four adjacent columns per thread (N % 4 == 0, 16-byte aligned words):
+// one 16-byte read of words, 8-byte writes of each output row.
+__global__ __launch_bounds__(256) void dequant4_kernel(Args a) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  const int N4 = a.N / 4;
+  const long long quads = (long long)(a.K / 8) * N4;
+  if (idx >= quads) return;
+  const int kb = (int)(idx / N4), n = (int)(idx % N4) * 4;
+  const int g = (kb * 8) / a.group;
+  const uint4 w = *reinterpret_cast<const uint4 *>(a.q + (long long)kb * a.N + n);
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  __half sh[4], zh[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    sh[c] = a.s[(long long)g * a.N + n + c];
+    zh[c] = a.z ? a.z[(long long)g * a.N + n + c] : __float2half(0.0f);
+  }
+  uint16_t r[8][4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    if (a.bf16) {
+      const float sf = __half2float(sh[c]), zf = __half2float(zh[c]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i][c] = to_bf16_bits(((float)((ws[c] >> (4 * i)) & 15u) - zf) * sf);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const __half nib = __float2half((float)((ws[c] >> (4 * i)) & 15u));
+        r[i][c] = __half_as_ushort(__hmul(__hsub(nib, zh[c]), sh[c]));
+      }
+    }
+  }
+  uint16_t *o = reinterpret_cast<uint16_t *>(a.out);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint2 v;
+    v.x = (uint32_t)r[i][0] | ((uint32_t)r[i][1] << 16);
+    v.y = (uint32_t)r[i][2] | ((uint32_t)r[i][3] << 16);
+    *reinterpret_cast<uint2 *>(o + ((long long)kb * 8 + i) * a.N + n) = v;
   }
 }
 
@@ -84,10 +132,15 @@ extern "C" int cfa_w4a16_dequant(const uint32_t *b_quant, const void *scales, co
   a.N = N;
   a.group = group_size;
   a.bf16 = out_bf16 ? 1 : 0;
-  const long long words = (long long)(K / 8) * N;
-  const long long blocks = (words + 255) / 256;
+  const bool vec = (N % 4 == 0) && (((uintptr_t)b_quant & 15) == 0) && (((uintptr_t)out & 7) == 0);
+  const long long items = (long long)(K / 8) * (vec ? N / 4 : N);
+  const long long blocks = (items + 255) / 256;
   if (blocks > 0x7fffffffLL) return fail_arg("matrix too large");
-  CFA_LAUNCH("w4a16_dequant", cfa::w4::dequant_kernel, dim3((unsigned)blocks), dim3(256), 0,
-             (hipStream_t)stream, a);
+  if (vec)
+    CFA_LAUNCH("w4a16_dequant", cfa::w4::dequant4_kernel, dim3((unsigned)blocks), dim3(256), 0,
+               (hipStream_t)stream, a);
+  else
+    CFA_LAUNCH("w4a16_dequant", cfa::w4::dequant_kernel, dim3((unsigned)blocks), dim3(256), 0,
+               (hipStream_t)stream, a);
   return CFA_OK;
 }

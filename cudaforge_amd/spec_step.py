@@ -275,8 +275,11 @@ class TreeSpeculator:
 
     def __init__(self, target: TargetModel, draft: DraftModel, B: int, context: int, *,
                  depth: int = 5, temperature: float = 1.0, mode: str = "cpp",
-                 max_steps: int = 64, block_size: int = 16, seed: int = 0):
+                 max_steps: int = 64, block_size: int = 16, seed: int = 0,
+                 use_graphs: bool = False):
         dev = target.embed.device
+        self.use_graphs = use_graphs
+        self._graphs: dict = {}
         self.t, self.d = target, draft
         self.B, self.depth, self.T, self.mode = B, depth, temperature, mode
         self.N = 2 ** (depth + 1) - 1
@@ -313,27 +316,55 @@ class TreeSpeculator:
         self.draft_rows = torch.zeros(B, self.N, s.vocab, dtype=torch.float32, device=dev)
         self.max_slots = draft.max_slots
 
+    def _level_forward(self, lvl: int, base: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
+        """Draft logits [B, n, V] of the nodes of level `lvl` (tokens toks
+        [B, n]), each seeing the context and its ancestors' tree slots."""
+        B, dev = self.B, toks.device
+        lo, hi = 2 ** lvl - 1, 2 ** (lvl + 1) - 1
+        n_keys = self.max_slots
+        key_ix = torch.arange(n_keys, device=dev)
+        nodes = torch.arange(lo, hi, device=dev)
+        slots = base[:, None] + nodes[None, :]
+        pos = base[:, None] + self.depths[nodes][None, :]
+        rel = key_ix[None, None, :] - base[:, None, None]         # [B, 1, keys]
+        in_tree = (rel >= 0) & (rel < self.N)
+        anc = self.anc[nodes][None, :, :].expand(B, -1, -1)       # [B, n, N]
+        tree_vis = torch.gather(anc, 2, rel.clamp(0, self.N - 1).expand(B, hi - lo, n_keys))
+        visible = (rel < 0) | (in_tree & tree_vis)
+        return self.d.forward_nodes(toks, pos, slots, visible)
+
+    def _level_graph(self, lvl: int, base: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
+        """_level_forward replayed from a HIP graph captured on first use
+        (static base / token buffers; every other tensor it touches is
+        persistent: weights, the draft KV cache, the graph's own pool)."""
+        if lvl not in self._graphs:
+            sb = base.clone()
+            st = toks.clone()
+            side = torch.cuda.Stream(base.device)
+            side.wait_stream(torch.cuda.current_stream(base.device))
+            with torch.cuda.stream(side):
+                self._level_forward(lvl, sb, st)                # warm-up outside capture
+            torch.cuda.current_stream(base.device).wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                out = self._level_forward(lvl, sb, st)
+            self._graphs[lvl] = (g, sb, st, out)
+        g, sb, st, out = self._graphs[lvl]
+        sb.copy_(base)
+        st.copy_(toks)
+        g.replay()
+        return out
+
     def propose(self, base: torch.Tensor) -> torch.Tensor:
         """Draft tree tokens [B, N] (node 0 = root); fills self.draft_rows
         with the draft logits of every expanded node."""
         B, dev = self.B, self.root.device
         tokens = torch.empty(B, self.N, dtype=torch.int32, device=dev)
         tokens[:, 0] = self.root
-        n_keys = self.max_slots
-        key_ix = torch.arange(n_keys, device=dev)
-        prefix = key_ix[None, :] < base[:, None]                 # [B, keys]
         for lvl in range(self.depth):
             lo, hi = 2 ** lvl - 1, 2 ** (lvl + 1) - 1
-            nodes = torch.arange(lo, hi, device=dev)
-            slots = base[:, None] + nodes[None, :]
-            pos = base[:, None] + self.depths[nodes][None, :]
-            # node i sees the prefix and its ancestors' slots
-            rel = key_ix[None, None, :] - base[:, None, None]     # [B, 1, keys]
-            in_tree = (rel >= 0) & (rel < self.N)
-            anc = self.anc[nodes][None, :, :].expand(B, -1, -1)   # [B, n, N]
-            tree_vis = torch.gather(anc, 2, rel.clamp(0, self.N - 1).expand(B, hi - lo, n_keys))
-            visible = prefix[:, None, :] | (in_tree & tree_vis)
-            logits = self.d.forward_nodes(tokens[:, lo:hi], pos, slots, visible)
+            run = self._level_graph if self.use_graphs else self._level_forward
+            logits = run(lvl, base, tokens[:, lo:hi].contiguous())
             self.draft_rows[:, lo:hi] = logits
             kids = expand_tree_level(logits.view(B * (hi - lo), -1), children=2,
                                      mode="sample" if self.mode == "cpp" else "greedy",

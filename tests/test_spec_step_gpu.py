@@ -119,3 +119,26 @@ def test_steps_bookkeeping(device, mode):
             assert len(sp.kv.get_block_table(b)) == -(-sp.ctx[b] // 16)
             assert len(r.emitted[b]) == L and r.emitted[b][-1] == r.final[b]
         assert sp.root.tolist() == r.final
+
+
+def test_draft_level_graphs_match_eager(device):
+    """The draft levels replayed from HIP graphs give the eager logits, on
+    every replay (several steps, eager work in between)."""
+    B, ctx0 = 3, 30
+    tm = TargetModel(SMALL_T, device, seed=7)
+    dm = DraftModel(SMALL_D, device, B, max_slots=ctx0 + 64 + 8 * 8)
+    sp = TreeSpeculator(tm, dm, B, ctx0, depth=3, max_steps=8, seed=8, use_graphs=True)
+    for rep in range(4):
+        base = torch.tensor([ctx0 + 2 * rep, ctx0 + rep, ctx0], dtype=torch.int32, device=device)
+        for lvl in range(3):
+            n = 2 ** lvl
+            toks = torch.randint(0, SMALL_D.vocab, (B, n), device=device, dtype=torch.int32)
+            kT0, v0 = dm.kT.clone(), dm.v.clone()
+            eager = sp._level_forward(lvl, base, toks).clone()
+            kT1, v1 = dm.kT.clone(), dm.v.clone()
+            dm.kT.copy_(kT0)
+            dm.v.copy_(v0)
+            graph = sp._level_graph(lvl, base, toks).clone()
+            torch.cuda.synchronize()
+            assert torch.equal(graph, eager), (rep, lvl, (graph - eager).abs().max().item())
+            assert torch.equal(dm.kT, kT1) and torch.equal(dm.v, v1)

@@ -34,7 +34,8 @@ def _np_dequant(w_int4, scales, zeros, group, dtype):
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("with_zeros", [False, True])
-@pytest.mark.parametrize("K,N,group", [(128, 256, 128), (512, 96, 64), (1024, 48, 128)])
+@pytest.mark.parametrize("K,N,group", [(128, 256, 128), (512, 96, 64), (1024, 48, 128),
+                                       (256, 50, 128)])
 def test_dequant_bit_exact(device, dtype, with_zeros, K, N, group):
     g = torch.Generator().manual_seed(K + N)
     w = torch.randint(0, 16, (K, N), generator=g, dtype=torch.int32)
