@@ -244,7 +244,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-tree", action="store_true", help="skip the tree attention / accept legs")
+    ap.add_argument("--no-tree", action="store_true",
+                    help="skip the extra legs (tree attention, tree accept/commit, 8B verify step)")
+    ap.add_argument("--legs", default="tree_attention,tree_accept_commit,verify_step_8b",
+                    help="comma-separated extra legs to run")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (reference for HBM byte counters)")
     args = ap.parse_args()
@@ -344,14 +347,18 @@ def main() -> int:
         "step_hbm_gbs": round(ALG_BYTES / (ms_per_step * 1e-3) / 1e9, 1),
         "wall_s": round(wall, 4),
     }
-    if not args.no_tree:
+    legs = [] if args.no_tree else [x for x in args.legs.split(",") if x]
+    known = {"tree_attention": tree_attention_leg, "tree_accept_commit": tree_accept_commit_leg,
+             "verify_step_8b": verify_step_8b_leg}
+    if legs:
         del sets
         torch.cuda.empty_cache()
-        line["tree_attention"] = tree_attention_leg(dev)
+    for name in legs:
+        if name not in known:
+            print(f"bench.py: unknown leg {name!r} (known: {sorted(known)})", file=sys.stderr)
+            return 2
+        line[name] = known[name](dev)
         torch.cuda.empty_cache()
-        line["tree_accept_commit"] = tree_accept_commit_leg(dev)
-        torch.cuda.empty_cache()
-        line["verify_step_8b"] = verify_step_8b_leg(dev)
     if not args.no_cpu_baseline:
         tl, dl, tok, U = make_inputs(dev, 1000)
         line["cpu_baseline"] = cpu_baseline(tl, dl, tok, U)
