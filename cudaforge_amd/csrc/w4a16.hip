@@ -17,6 +17,7 @@
 #include <hip/hip_fp16.h>
 
 #include "abi_internal.hpp"
+#include "lds_dma.hpp"
 
 namespace cfa {
 namespace w4 {
@@ -142,5 +143,225 @@ extern "C" int cfa_w4a16_dequant(const uint32_t *b_quant, const void *scales, co
   else
     CFA_LAUNCH("w4a16_dequant", cfa::w4::dequant_kernel, dim3((unsigned)blocks), dim3(256), 0,
                (hipStream_t)stream, a);
+  return CFA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Fused W4A16 GEMM: C [M, N] = A [M, K] x dequant(B_quant) for bf16 or fp16
+// activations, fp32 accumulation on v_mfma_f32_16x16x32_{bf16,f16}.
+//
+// Work-group tile BM x 256 (BM = 64 or 32), four waves of BM x 64, K in steps
+// of 64.  Each step's A tile (16-byte chunks XOR-swizzled by row, for
+// conflict-free MFMA operand reads), packed weights and scale row move by
+// direct HBM -> LDS transfers into a 4-stage ring, three steps ahead, with
+// one barrier per step.  Lane l of a wave reads, per 32-k half step, the four
+// adjacent words of columns n0 + 4 (l % 16) + j (j = 0..3) at packed row
+// k0/8 + l/16 -- one 16-byte LDS read -- and word j, dequantised in
+// registers, is exactly the lane's 8-element B fragment of the wave's n-tile
+// j, whose column c is global column n0 + 4c + j.  Dequantisation is the bf16 / fp16
+// formula of dequant_kernel, so the result equals dequantise-then-GEMM up to
+// the order of the fp32 accumulation.
+// ---------------------------------------------------------------------------
+namespace cfa {
+namespace w4 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct GArgs {
+  const uint16_t *A;   // [M, K]
+  const uint32_t *q;   // [K/8, N]
+  const __half *s;     // [K/g, N]
+  uint16_t *C;         // [M, N]
+  int M, N, K, group;
+  int mtiles, ntiles;
+};
+
+constexpr int kGBN = 256, kGBK = 64;
+
+template <bool F16>
+__device__ __forceinline__ void dequant_frag(uint32_t w, float s, uint32_t (&out)[4]) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float f0 = (float)((w >> (8 * p)) & 15u) * s;
+    const float f1 = (float)((w >> (8 * p + 4)) & 15u) * s;
+    uint32_t lo, hi;
+    if (F16) {
+      lo = __half_as_ushort(__float2half(f0));
+      hi = __half_as_ushort(__float2half(f1));
+    } else {
+      lo = __builtin_bit_cast(uint16_t, (__bf16)f0);
+      hi = __builtin_bit_cast(uint16_t, (__bf16)f1);
+    }
+    out[p] = lo | (hi << 16);
+  }
+}
+
+template <int BM, bool F16>
+__global__ __launch_bounds__(256, 2) void w4gemm_kernel(GArgs a) {
+  constexpr int MT = BM / 16;                   // 16-row MFMA tiles per wave
+  constexpr int kS = 4, kP = 3;                 // ring stages, iterations in flight
+  constexpr int ABYTES = BM * kGBK * 2;         // A tile (128-byte rows)
+  constexpr int BBYTES = (kGBK / 8) * kGBN * 4; // 8 packed rows of 256 words
+  constexpr int SBYTES = kGBN * 2;              // one scale row
+  constexpr int STAGE = ABYTES + BBYTES + SBYTES;
+  constexpr int AX = ABYTES / 1024 / 4;         // A transfers per wave
+  constexpr int LPI = AX + 2 + 1;               // transfers per wave per iteration
+  __shared__ __align__(16) uint8_t ring[kS * STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Work-groups go to the 8 XCDs round-robin by linear index; the m-tiles of
+  // one n-tile take indices 8 apart, so they share an XCD and its L2, which
+  // then serves their common weight columns.
+  const int L = blockIdx.x;
+  const int ntile = (L % 8) + 8 * (L / (8 * a.mtiles));
+  const int mti = (L / 8) % a.mtiles;
+  if (ntile >= a.ntiles) return;  // padding of the last group of 8 n-tiles
+  const int m0 = mti * BM;
+  const int nbase = ntile * kGBN;
+  const int iters = a.K / kGBK;
+
+  // this lane's sources of the per-iteration transfers (k0 added per issue)
+  const uint16_t *asrc[AX];
+#pragma unroll
+  for (int j = 0; j < AX; ++j) {
+    const int x = wave * AX + j;                  // 1 KiB transfer: A rows 8x .. 8x + 7
+    const int row = 8 * x + (lane >> 3);
+    const int c = (lane & 7) ^ (row & 7);         // chunk landing at position lane % 8
+    asrc[j] = a.A + (long long)min(m0 + row, a.M - 1) * a.K + 8 * c;
+  }
+  const uint32_t *bsrc = a.q + (long long)(2 * wave) * a.N + nbase + 4 * lane;
+  const __half *ssrc = a.s + nbase + 64 * wave + 8 * (lane & 7);
+
+  auto issue = [&](int u) {
+    uint8_t *st = ring + (u % kS) * STAGE;
+    const int k0 = u * kGBK;
+#pragma unroll
+    for (int j = 0; j < AX; ++j)
+      dma16(asrc[j] + k0, (CFA_LDS void *)(st + 1024 * (wave * AX + j)));
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      dma16(bsrc + (long long)(k0 / 8 + j) * a.N,
+            (CFA_LDS void *)(st + ABYTES + 1024 * (2 * wave + j)));
+    if (lane < 8)
+      dma16(ssrc + (long long)(k0 / a.group) * a.N, (CFA_LDS void *)(st + ABYTES + BBYTES + 128 * wave));
+  };
+
+  f32x4 acc[MT][4];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int u = 0; u < min(kP, iters); ++u) issue(u);
+  for (int it = 0; it < iters; ++it) {
+    const int later = min(kP - 1, iters - 1 - it);  // iterations issued after this one
+    if (later >= 2) wait_vmcnt<2 * LPI>();
+    else if (later == 1) wait_vmcnt<LPI>();
+    else wait_vmcnt<0>();
+    block_barrier();  // every wave's part of stage `it` has landed
+    // the stage refilled here was last read in iteration it - 1
+    if (it + kP < iters) issue(it + kP);
+    const uint8_t *st = ring + (it % kS) * STAGE;
+    const uint2 sv = *reinterpret_cast<const uint2 *>(st + ABYTES + BBYTES + (64 * wave + 4 * (lane & 15)) * 2);
+    float sc[4];
+    sc[0] = __half2float(__ushort_as_half((uint16_t)(sv.x & 0xffff)));
+    sc[1] = __half2float(__ushort_as_half((uint16_t)(sv.x >> 16)));
+    sc[2] = __half2float(__ushort_as_half((uint16_t)(sv.y & 0xffff)));
+    sc[3] = __half2float(__ushort_as_half((uint16_t)(sv.y >> 16)));
+    const uint4 *Ab = reinterpret_cast<const uint4 *>(st);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint4 bw = *reinterpret_cast<const uint4 *>(
+          st + ABYTES + (4 * s + (lane >> 4)) * 1024 + (64 * wave + 4 * (lane & 15)) * 4);
+      const uint32_t wj[4] = {bw.x, bw.y, bw.z, bw.w};
+      uint32_t bf[4][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dequant_frag<F16>(wj[j], sc[j], bf[j]);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int row = 16 * i + (lane & 15);
+        const int kc = s * 4 + (lane >> 4);
+        const uint4 av = Ab[row * 8 + (kc ^ (row & 7))];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 bv = make_uint4(bf[j][0], bf[j][1], bf[j][2], bf[j][3]);
+          if (F16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, bv), acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv), acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // C[row][n0 + 4c + j] = acc[i][j][e], row = m0 + 16 i + 4 (lane / 16) + e
+  const int bcol = nbase + 64 * wave + 4 * (lane & 15);
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = m0 + 16 * i + 4 * (lane >> 4) + e;
+      if (row >= a.M) continue;
+      uint16_t v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (F16)
+          v[j] = __half_as_ushort(__float2half(acc[i][j][e]));
+        else
+          v[j] = __builtin_bit_cast(uint16_t, (__bf16)acc[i][j][e]);
+      }
+      uint2 w;
+      w.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+      w.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
+      *reinterpret_cast<uint2 *>(a.C + (long long)row * a.N + bcol) = w;
+    }
+}
+
+}  // namespace w4
+}  // namespace cfa
+
+extern "C" int cfa_w4a16_gemm(const void *a, const uint32_t *b_quant, const void *scales, int M,
+                              int N, int K, int group_size, int fp16, void *c, void *stream) {
+  using namespace cfa::abi;
+  clear_error();
+  if (M <= 0 || N <= 0 || K <= 0) return fail_arg("M, N and K must be positive");
+  if (N % cfa::w4::kGBN != 0) return fail_arg("N must be a multiple of 256");
+  if (group_size <= 0 || group_size % cfa::w4::kGBK != 0 || K % group_size != 0)
+    return fail_arg("group_size must be a multiple of 64 that divides K");
+  if (!a || !b_quant || !scales || !c) return fail_arg("null pointer");
+  if ((((uintptr_t)a | (uintptr_t)b_quant | (uintptr_t)c) & 15) != 0 || ((uintptr_t)scales & 7) != 0)
+    return fail_arg("operands must be 16-byte aligned (scales 8-byte)");
+  cfa::w4::GArgs g{};
+  g.A = (const uint16_t *)a;
+  g.q = b_quant;
+  g.s = (const __half *)scales;
+  g.C = (uint16_t *)c;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.group = group_size;
+  g.ntiles = N / cfa::w4::kGBN;
+  const int cus = device_cu_count();
+  const bool small = ((M + 63) / 64) * g.ntiles < cus;  // 32-row tiles fill the chip better
+  const int BM = small ? 32 : 64;
+  g.mtiles = (M + BM - 1) / BM;
+  const long long blocks = (long long)g.mtiles * ((g.ntiles + 7) / 8) * 8;
+  if (blocks > 0x7fffffffLL) return fail_arg("problem too large");
+  hipStream_t st = (hipStream_t)stream;
+  if (fp16) {
+    if (small)
+      CFA_LAUNCH("w4a16_gemm", (cfa::w4::w4gemm_kernel<32, true>), dim3((unsigned)blocks), dim3(256), 0, st, g);
+    else
+      CFA_LAUNCH("w4a16_gemm", (cfa::w4::w4gemm_kernel<64, true>), dim3((unsigned)blocks), dim3(256), 0, st, g);
+  } else {
+    if (small)
+      CFA_LAUNCH("w4a16_gemm", (cfa::w4::w4gemm_kernel<32, false>), dim3((unsigned)blocks), dim3(256), 0, st, g);
+    else
+      CFA_LAUNCH("w4a16_gemm", (cfa::w4::w4gemm_kernel<64, false>), dim3((unsigned)blocks), dim3(256), 0, st, g);
+  }
   return CFA_OK;
 }

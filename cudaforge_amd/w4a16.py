@@ -6,8 +6,9 @@
 (``csrc/include/cudaforge/kernels/dequantize.cuh:12-25``,
 ``tests/unit/test_int4_dequant.py:6-15``).  ``int4_gemm_dequant`` mirrors
 ``int4_gemm_dequant_triton`` (``csrc/kernels/triton/int4_dequant_triton.py:
-86-131``): the weights are dequantised on the device by ``cfa_w4a16_dequant``
-and multiplied by a PyTorch-ROCm GEMM in the activations' dtype.
+86-131``): ``cfa_w4a16_dequant`` followed by a PyTorch-ROCm GEMM in the
+activations' dtype.  ``w4a16_gemm`` is the fused MFMA kernel
+(``cfa_w4a16_gemm``: dequantisation in registers, no zero points).
 """
 from __future__ import annotations
 
@@ -19,7 +20,8 @@ import torch
 from . import _lib
 from .verify import _stream_ptr
 
-__all__ = ["pack_int4_weights", "w4a16_dequant", "int4_gemm_dequant", "W4A16Linear"]
+__all__ = ["pack_int4_weights", "w4a16_dequant", "w4a16_gemm", "int4_gemm_dequant",
+           "W4A16Linear"]
 
 
 def pack_int4_weights(w_int4: torch.Tensor) -> torch.Tensor:
@@ -64,6 +66,32 @@ def w4a16_dequant(b_quant: torch.Tensor, scales: torch.Tensor, zeros: Optional[t
     return out
 
 
+def fused_gemm_ok(a: torch.Tensor, b_quant: torch.Tensor, zeros, group_size: int) -> bool:
+    """Whether cfa_w4a16_gemm takes this problem (else dequantise + GEMM)."""
+    N = b_quant.shape[1]
+    return (zeros is None and N % 256 == 0 and group_size % 64 == 0 and a.is_contiguous()
+            and b_quant.is_contiguous() and a.data_ptr() % 16 == 0 and b_quant.data_ptr() % 16 == 0)
+
+
+def w4a16_gemm(a: torch.Tensor, b_quant: torch.Tensor, scales: torch.Tensor, *,
+               group_size: int = 128, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused a [M, K] (fp16 or bf16) x dequant(b_quant) -> [M, N] in a's dtype
+    (cfa_w4a16_gemm)."""
+    M, K = a.shape
+    N = b_quant.shape[1]
+    if b_quant.shape[0] * 8 != K:
+        raise ValueError("K of a and b_quant differ")
+    if out is None:
+        out = torch.empty(M, N, dtype=a.dtype, device=a.device)
+    sc = scales.contiguous()
+    with torch.cuda.device(a.device):
+        rc = _lib.load().cfa_w4a16_gemm(a.data_ptr(), b_quant.data_ptr(), sc.data_ptr(), M, N, K,
+                                        group_size, 1 if a.dtype == torch.float16 else 0,
+                                        out.data_ptr(), _stream_ptr(a.device))
+    _lib.check(rc, "cfa_w4a16_gemm")
+    return out
+
+
 class W4A16Linear:
     """y = x @ W with W [K, N] held as packed INT4 + fp16 group scales.
     Random initialisation: uniform nibbles, scales chosen so that the output
@@ -78,7 +106,14 @@ class W4A16Linear:
         self.scales = (base * (0.5 + torch.rand(K // group, N, device=device, generator=gen))
                        ).to(torch.float16)
 
+    # class-wide switch: the fused GEMM (cfa_w4a16_gemm) where the shape
+    # allows; off by default because dequantise + hipBLASLt is faster at the
+    # verify step's shapes on MI355X (M = 504: 70 vs 105 us for QKV)
+    fused = False
+
     def __call__(self, x: torch.Tensor, scratch: torch.Tensor) -> torch.Tensor:
+        if self.fused and fused_gemm_ok(x, self.qweight, None, self.group):
+            return w4a16_gemm(x, self.qweight, self.scales, group_size=self.group)
         w = scratch[: self.K * self.N].view(self.K, self.N)
         w4a16_dequant(self.qweight, self.scales, group_size=self.group, dtype=x.dtype, out=w)
         return x @ w

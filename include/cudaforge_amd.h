@@ -242,6 +242,15 @@ int cfa_kv_commit(void *k_pool, void *v_pool, const int32_t *block_tables,
 int cfa_w4a16_dequant(const uint32_t *b_quant, const void *scales, const void *zeros, int K,
                       int N, int group_size, int out_bf16, void *out, void *stream);
 
+/* Fused W4A16 GEMM: c [M, N] = a [M, K] x dequant(b_quant, scales) with the
+ * dequantisation of cfa_w4a16_dequant (no zero points) done in registers and
+ * fp32 accumulation on MFMA.  fp16 = 1: a and c fp16 (int4_gemm_dequant.cu /
+ * int4_dequant_triton.py semantics); fp16 = 0: bf16.  N % 256 == 0,
+ * group_size % 64 == 0, K % group_size == 0; a, b_quant, c 16-byte aligned,
+ * scales 8-byte aligned. */
+int cfa_w4a16_gemm(const void *a, const uint32_t *b_quant, const void *scales, int M, int N,
+                   int K, int group_size, int fp16, void *c, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Fused layers of the model-scale verify step (bf16 activations, fp32 math;
  * no counterpart in the reference, whose model runner is out of this

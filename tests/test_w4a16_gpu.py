@@ -76,3 +76,37 @@ def test_reference_gemm_parity(device, M, N, K):
     c_ref = torch.matmul(a, w_dequant)
     c = int4_gemm_dequant(a, b_quant, scales, group_size=group)
     torch.testing.assert_close(c, c_ref, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 128), (37, 1024, 512), (504, 512, 4096),
+                                   (64, 768, 256), (200, 256, 1024)])
+def test_fused_gemm_vs_dequantised_fp32(device, dtype, M, N, K):
+    """cfa_w4a16_gemm against an fp32 product of the bit-exact dequantised
+    weights: differences come from the fp32 accumulation order and the final
+    rounding to 16 bits (tolerance 1e-2 of the output scale + 2^-7 relative)."""
+    from cudaforge_amd.w4a16 import w4a16_gemm
+
+    g = torch.Generator().manual_seed(M + N + K)
+    group = 128
+    a = torch.randn(M, K, generator=g).to(dtype).to(device)
+    w_int4 = torch.randint(0, 16, (K, N), generator=g, dtype=torch.int32)
+    scales = (torch.rand(K // group, N, generator=g) * 0.05 + 1e-3).half().to(device)
+    q = pack_int4_weights(w_int4).to(device)
+    c = w4a16_gemm(a, q, scales, group_size=group)
+    w = w4a16_dequant(q, scales, group_size=group, dtype=dtype).float()
+    ref = a.float() @ w
+    torch.cuda.synchronize()
+    err = (c.float() - ref).abs()
+    tol = 1e-2 * ref.abs().max() + 2.0 ** -7 * ref.abs()
+    assert (err <= tol).all(), err.max().item()
+
+
+def test_fused_gemm_rejects_bad_shapes(device):
+    from cudaforge_amd.w4a16 import w4a16_gemm
+
+    a = torch.randn(4, 128, device=device).bfloat16()
+    q = torch.zeros(16, 100, dtype=torch.int32, device=device)
+    s = torch.ones(1, 100, dtype=torch.float16, device=device)
+    with pytest.raises(ValueError):
+        w4a16_gemm(a, q, s)
