@@ -11,11 +11,13 @@
 //   pool[block][layer][kv_head][slot][head_dim].
 //
 // Hazard: a destination slot j can be the source of an earlier path entry
-// (path[j'] = j for j' < j), so moving in parallel would race.  Each
-// work-group owns one (sequence, layer, head) and reads every moved row of K
-// and V into LDS before writing any.  Rows with path[j] == j (the root, and
-// any prefix of a chain) are already in place and are neither read nor
-// written.
+// (path[j'] = j for j' < j), but never of a later one (path[j'] >= j' > j).
+// So a thread that moves one 16-byte column (KV head, chunk, K or V) of the
+// rows in increasing j order reads every source before anything overwrites
+// it; a batch of rows is read before the batch is written.  One work-group
+// per (sequence, layer) checks the path once, one thread per entry.  Rows
+// with path[j] == j (the root, and any prefix of a chain) are already in
+// place and are neither read nor written.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -40,63 +42,61 @@ struct Args {
   int max_blocks, num_blocks, num_layers, Hkv, bs, row_bytes, path_stride, B;
 };
 
-// Byte offset of (sequence b, slot pos, layer, head) or -1 when the page is
-// outside the table or the pool.
-__device__ __forceinline__ long long slot_off(const Args &a, int b, int pos, int layer, int h) {
+// Byte offset of (sequence b, slot pos) in layer 0, head 0, or -1 when the
+// page is outside the table or the pool.
+__device__ __forceinline__ long long slot_base(const Args &a, int b, int pos) {
   const int page = pos / a.bs;
   if (pos < 0 || page >= a.max_blocks) return -1;
   const int blk = a.bt[(long long)b * a.max_blocks + page];
   if (blk < 0 || blk >= a.num_blocks) return -1;
-  return ((((long long)blk * a.num_layers + layer) * a.Hkv + h) * a.bs + pos % a.bs) *
-         (long long)a.row_bytes;
+  return ((long long)blk * a.num_layers * a.Hkv * a.bs + pos % a.bs) * (long long)a.row_bytes;
 }
 
-// Validity of sequence b's path: 1 <= L <= kMaxPath, path[0] == 0, strictly
-// increasing, and every source and destination slot mapped.  Evaluated
-// identically by every work-group of the sequence, so a rejected sequence is
-// left untouched everywhere.
-__device__ bool path_ok(const Args &a, int b, int ctx, int L) {
-  if (L < 1 || L > kMaxPath || L > a.path_stride || ctx < 0) return false;
-  const int32_t *p = a.paths + (long long)b * a.path_stride;
-  if (p[0] != 0) return false;
-  for (int j = 1; j < L; ++j)
-    if (p[j] <= p[j - 1]) return false;
-  for (int j = 0; j < L; ++j)
-    if (slot_off(a, b, ctx + p[j], 0, 0) < 0 || slot_off(a, b, ctx + j, 0, 0) < 0) return false;
-  return true;
-}
+constexpr int kBatch = 8;  // rows held in registers per thread at a time
 
 __global__ __launch_bounds__(kNT) void commit_kernel(Args a) {
-  __shared__ uint4 buf[2][kMaxPath * (kMaxRowBytes / 16)];
-  __shared__ int ok;
-  const int h = blockIdx.x, layer = blockIdx.y, b = blockIdx.z;
+  __shared__ long long src[kMaxPath], dst[kMaxPath];
+  const int layer = blockIdx.x, b = blockIdx.y;
   const int ctx = a.ctx[b];
   const int L = a.plen[b];
-  if (threadIdx.x == 0) ok = path_ok(a, b, ctx, L) ? 1 : 0;
-  __syncthreads();
-  if (h == 0 && layer == 0 && threadIdx.x == 0) {
+  const int32_t *p = a.paths + (long long)b * a.path_stride;
+  // path check, one thread per entry: 1 <= L <= kMaxPath, path[0] == 0,
+  // strictly increasing, every source and destination slot mapped
+  bool good = true;
+  const bool shape_ok = L >= 1 && L <= kMaxPath && L <= a.path_stride && ctx >= 0;
+  if (shape_ok && threadIdx.x < L) {
+    const int j = threadIdx.x;
+    const int pj = p[j];
+    good = (j == 0) ? (pj == 0) : (pj > p[j - 1]);
+    const long long so = slot_base(a, b, ctx + pj), d = slot_base(a, b, ctx + j);
+    good = good && so >= 0 && d >= 0;
+    src[j] = (pj == j) ? -1 : so;  // -1: already in place
+    dst[j] = d;
+  }
+  const bool ok = __syncthreads_and(good ? 1 : 0) && shape_ok;
+  if (layer == 0 && threadIdx.x == 0) {
     if (a.status) a.status[b] = ok ? 0 : 1;
     if (a.new_ctx) a.new_ctx[b] = ok ? ctx + L : ctx;
   }
   if (!ok) return;
-  const int32_t *p = a.paths + (long long)b * a.path_stride;
   const int cpr = a.row_bytes / 16;  // 16-byte chunks per row
-  const int n = L * cpr;
-  // read every moved row (K then V) before writing any
-  for (int i = threadIdx.x; i < n; i += kNT) {
-    const int j = i / cpr, c = i % cpr;
-    if (p[j] == j) continue;
-    const long long so = slot_off(a, b, ctx + p[j], layer, h) + 16LL * c;
-    buf[0][i] = *reinterpret_cast<const uint4 *>(a.kpool + so);
-    buf[1][i] = *reinterpret_cast<const uint4 *>(a.vpool + so);
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < n; i += kNT) {
-    const int j = i / cpr, c = i % cpr;
-    if (p[j] == j) continue;
-    const long long d = slot_off(a, b, ctx + j, layer, h) + 16LL * c;
-    *reinterpret_cast<uint4 *>(a.kpool + d) = buf[0][i];
-    *reinterpret_cast<uint4 *>(a.vpool + d) = buf[1][i];
+  const long long head_stride = (long long)a.bs * a.row_bytes;
+  const long long layer_off = (long long)layer * a.Hkv * head_stride;
+  for (int col = threadIdx.x; col < a.Hkv * cpr * 2; col += kNT) {
+    const int kv = col / (a.Hkv * cpr), h = (col / cpr) % a.Hkv, c = col % cpr;
+    uint8_t *pool = kv ? a.vpool : a.kpool;
+    const long long off = layer_off + h * head_stride + 16LL * c;
+    for (int j0 = 0; j0 < L; j0 += kBatch) {
+      uint4 v[kBatch];
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q)
+        if (j0 + q < L && src[j0 + q] >= 0)
+          v[q] = *reinterpret_cast<const uint4 *>(pool + src[j0 + q] + off);
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q)
+        if (j0 + q < L && src[j0 + q] >= 0)
+          *reinterpret_cast<uint4 *>(pool + dst[j0 + q] + off) = v[q];
+    }
   }
 }
 
@@ -123,7 +123,7 @@ extern "C" int cfa_kv_commit(void *k_pool, void *v_pool, const int32_t *block_ta
     return fail_arg("head_dim * elem_bytes must be a multiple of 16 and at most 512");
   if (path_stride < 1) return fail_arg("path_stride must be positive");
   if ((((uintptr_t)k_pool | (uintptr_t)v_pool) & 15) != 0) return fail_arg("pools must be 16-byte aligned");
-  if (B > 65535 || num_layers > 65535) return fail_arg("B and num_layers must be at most 65535");
+  if (B > 65535) return fail_arg("B must be at most 65535");
   commit::Args a{};
   a.kpool = (uint8_t *)k_pool;
   a.vpool = (uint8_t *)v_pool;
@@ -141,7 +141,7 @@ extern "C" int cfa_kv_commit(void *k_pool, void *v_pool, const int32_t *block_ta
   a.row_bytes = (int)row;
   a.path_stride = path_stride;
   a.B = B;
-  CFA_LAUNCH("kv_commit", commit::commit_kernel, dim3(n_kv_heads, num_layers, B), dim3(commit::kNT),
-             0, (hipStream_t)stream, a);
+  CFA_LAUNCH("kv_commit", commit::commit_kernel, dim3(num_layers, B), dim3(commit::kNT), 0,
+             (hipStream_t)stream, a);
   return CFA_OK;
 }
