@@ -17,8 +17,11 @@ kernels:
                     ``PagedKVCache.truncate_sequence``;
 * W4A16 weights     ``cfa_w4a16_dequant`` (the reference's packed INT4
                     format, ``int4_gemm_dequant.cu:20-31``) feeding
-                    PyTorch-ROCm GEMMs; the norms, rotary embeddings,
-                    activations and the draft's own attention run in PyTorch.
+                    PyTorch-ROCm GEMMs;
+* fused layers      ``cfa_rmsnorm`` (with the residual add),
+                    ``cfa_rope_kv_paged`` / ``_strided`` (rotary embedding
+                    plus the KV-cache write), ``cfa_silu_mul``; the draft's
+                    own attention runs in PyTorch.
 
 The draft keeps a contiguous KV cache (``[layers, B, Hkv, head_dim, slots]``
 for K, so the score product reads a contiguous operand) because its head size
@@ -155,10 +158,6 @@ class TargetModel:
         s = self.shape
         B, N = tokens.shape
         hd, Hq, Hkv = s.head_dim, s.n_heads, s.n_kv_heads
-        bs = kv.get_config().block_size
-        slot = base_lens.long()[:, None] + torch.arange(N, device=tokens.device)[None, :]
-        blk = torch.gather(block_tables.long(), 1, slot // bs).reshape(-1)
-        off = (slot % bs).reshape(-1)
         need = tree_attention_workspace_bytes(B, N, Hq, Hkv, hd, max_keys)
         if self.attn_ws is None or self.attn_ws.numel() < need:
             self.attn_ws = torch.empty(max(need, 1), dtype=torch.uint8, device=tokens.device)
