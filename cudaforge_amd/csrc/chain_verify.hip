@@ -1278,7 +1278,7 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   a.R = R;
   const long long total = (long long)R * a.Vw;
   const int cus = device_cu_count();
-  long long G = std::min<long long>((long long)cus * 8, (total + 1023) / 1024);
+  long long G = std::min<long long>((long long)cus * 4, (total + 1023) / 1024);
   G = std::max<long long>(G, R);
   G = std::min<long long>(G, max_groups(R));
   a.C = (total + G - 1) / G;

@@ -13,8 +13,8 @@
 // One work-group = (split, kv head, sequence); its 8 waves hold all G*N query
 // rows (two 16-row tiles each, Q^T in registers, pre-scaled by
 // scale*log2(e)).  64-key K and V tiles move HBM -> LDS with direct 16-byte
-// global_load_lds transfers (no register staging) into two rings (K: 3
-// stages, V: 4), three tiles ahead of the tile being computed; the split's
+// global_load_lds transfers (no register staging) into two rings (K: 4
+// stages, V: 5), three tiles ahead of the tile being computed; the split's
 // page lookups are resolved once into an LDS table.  Everything is computed
 // in the transposed form
 //   S^T = K Q^T - b        (MFMA A = K rows, B = Q^T columns, C = -b)
@@ -69,8 +69,8 @@ constexpr int kQT = 2;                        // 16-row query tiles per wave
 constexpr int kMaxRows = kWaves * kQT * 16;   // 256 query rows per work-group
 constexpr int kRowBytes = kD * 2;             // one K or V row, bf16
 constexpr int kTileBytes = kKT * kRowBytes;   // 16 KiB
-constexpr int kKStages = 3;                   // K-tile ring (tile u: stage u % 3)
-constexpr int kVStages = 4;                   // V-tile ring (read one iteration after K)
+constexpr int kKStages = 4;                   // K-tile ring (tile u: stage u % 4)
+constexpr int kVStages = 5;                   // V-tile ring (read one iteration after K)
 constexpr int kLoadsPerTile = 4;              // global_load_lds per wave per tile
 constexpr float kRescaleSlack = 8.0f;         // log2 units
 #ifndef CFA_TA_SGB
@@ -179,7 +179,16 @@ __device__ __forceinline__ uint64_t tile_visibility(int kbase, int ctx, uint64_t
   return ctx_bits | tree_bits;
 }
 
-__device__ __forceinline__ float xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m, 64)); }
+// Maximum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four lanes holding
+// one query column) without an LDS round trip: each permlane swap returns the
+// lane's own value and its partner's (in one order or the other), so the max
+// of the pair is the max of the two lanes.
+__device__ __forceinline__ float column_max(float v) {
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+}
 
 // Per-wave state of the pipelined loop: 16-row query tiles qt of this wave,
 // scores of one 64-key tile s[qt][blk][T] (keys blk*32 + 8g + 4T + i) and its
@@ -267,8 +276,7 @@ __device__ __forceinline__ void valu_phase(const Lane &ln, int kbase, int ctx, S
       for (int T = 0; T < 2; ++T)
 #pragma unroll
         for (int i = 0; i < 4; ++i) v = fmaxf(v, S.s[qt][blk][T][i]);
-    v = xor_max(v, 16);
-    mx[qt] = xor_max(v, 32);
+    mx[qt] = column_max(v);
     resc[qt] = mx[qt] > -INFINITY && (!sm.valid[qt] || mx[qt] > kRescaleSlack);
     any |= resc[qt];
   }
@@ -449,9 +457,12 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
     // other is in its MFMA phase.  Barrier k ties group 0's phase k to group
     // 1's phase k - 1; group 1 takes one extra barrier first, group 0 one at
     // the end.  Tile t+1 must be visible before barrier 2(t - t0) + 1 (the
-    // first MFMA phase reading it follows that barrier), and tile t + 3 is
-    // issued right after it: its stages last held tiles t (K) and t - 1 (V),
-    // whose last readers finished before that barrier.
+    // first MFMA phase reading it follows that barrier).  Tile t + 3 goes to
+    // the stages of tiles t - 1 (K) and t - 2 (V), whose last readers (the
+    // MFMA phases t - 2) finished before barrier 2(t - t0) - 1, so each group
+    // issues its share before a VALU phase: group 0 after barrier 2(t - t0),
+    // group 1 after barrier 2(t - t0) + 1.  No MFMA phase waits behind the
+    // transfers' issue.
     const bool lag = wave >= kWaves / 2;
     if (lag) block_barrier();
     Scores S;
@@ -461,6 +472,11 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
       const int kbase = t * kKT;
       if (!lag) {
         block_barrier();
+        if (t + 3 < t1) {
+          const int u = t + 3 - t0;
+          issue_tile(a, gtab, g0, (t + 3) * kKT, nkeys, kring + (u % kKStages) * kTileBytes,
+                     vring + (u % kVStages) * kTileBytes, wave, lane);
+        }
       } else {
         if (t + 2 < t1) wait_vmcnt<kLoadsPerTile>();
         else wait_vmcnt<0>();
@@ -473,14 +489,10 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
       }
       valu_phase(ln, kbase, ctx, S, sm, o, lacc, P);
       if (!lag) {
-        if (t + 2 < t1) wait_vmcnt<kLoadsPerTile>();
+        if (t + 3 < t1) wait_vmcnt<2 * kLoadsPerTile>();
+        else if (t + 2 < t1) wait_vmcnt<kLoadsPerTile>();
         else wait_vmcnt<0>();
         block_barrier();
-        if (t + 3 < t1) {
-          const int u = t + 3 - t0;
-          issue_tile(a, gtab, g0, (t + 3) * kKT, nkeys, kring + (u % kKStages) * kTileBytes,
-                     vring + (u % kVStages) * kTileBytes, wave, lane);
-        }
       } else {
         block_barrier();
       }
@@ -532,7 +544,9 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
 // Log-sum-exp merge of the splits: out = sum_s w_s l_s o_s / sum_s w_s l_s
 // with w_s = 2^(m_s - max m) and o_s the normalised bf16 partial; 16 threads
 // per query row, eight d-values (one 16-byte load per split) per thread,
-// sixteen rows per work-group.
+// sixteen rows per work-group.  Up to kMergeRegs splits are loaded in one
+// round before any arithmetic.
+constexpr int kMergeRegs = 4;  // splits merged from registers in one round of loads
 __global__ __launch_bounds__(256) void tree_merge_kernel(Args a) {
   const long long row_g = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int q8 = threadIdx.x & 15;
@@ -543,23 +557,53 @@ __global__ __launch_bounds__(256) void tree_merge_kernel(Args a) {
   const int b = (int)(row_g / ((long long)a.rows * a.Hkv));
   const long long split_stride = (long long)a.B * a.Hkv * a.rows;  // rows per split
   const long long prow0 = ((long long)b * a.Hkv + h) * a.rows + r;
-  float M = -INFINITY;
-  for (int s = 0; s < a.splits; ++s) M = fmaxf(M, a.part_ml[prow0 + s * split_stride].x);
-  const float base = (M == -INFINITY) ? 0.0f : M;
   float L = 0.0f;
   float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-  for (int s = 0; s < a.splits; ++s) {
-    const long long prow = prow0 + s * split_stride;
-    const float2 ml = a.part_ml[prow];
-    const uint4 v = *reinterpret_cast<const uint4 *>(a.part_o + prow * kD + 8 * q8);
-    const float w = __builtin_amdgcn_exp2f(ml.x - base) * ml.y;
-    L += w;
+  auto add = [&](float w, const uint4 &v) {
     const uint32_t *vs = reinterpret_cast<const uint32_t *>(&v);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       acc[2 * j] += w * __uint_as_float(vs[j] << 16);
       acc[2 * j + 1] += w * __uint_as_float(vs[j] & 0xffff0000u);
+    }
+  };
+  if (a.splits <= kMergeRegs) {
+    // every split's (base, sum) and partial in flight at once
+    float2 ml[kMergeRegs];
+    uint4 v[kMergeRegs];
+#pragma unroll
+    for (int s = 0; s < kMergeRegs; ++s) {
+      if (s < a.splits) {
+        const long long prow = prow0 + s * split_stride;
+        ml[s] = a.part_ml[prow];
+        v[s] = *reinterpret_cast<const uint4 *>(a.part_o + prow * kD + 8 * q8);
+      }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kMergeRegs; ++s)
+      if (s < a.splits) M = fmaxf(M, ml[s].x);
+    const float base = (M == -INFINITY) ? 0.0f : M;
+#pragma unroll
+    for (int s = 0; s < kMergeRegs; ++s) {
+      if (s < a.splits) {
+        const float w = __builtin_amdgcn_exp2f(ml[s].x - base) * ml[s].y;
+        L += w;
+        add(w, v[s]);
+      }
+    }
+  } else {
+    float M = -INFINITY;
+    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, a.part_ml[prow0 + s * split_stride].x);
+    const float base = (M == -INFINITY) ? 0.0f : M;
+#pragma unroll 4
+    for (int s = 0; s < a.splits; ++s) {
+      const long long prow = prow0 + s * split_stride;
+      const float2 ml = a.part_ml[prow];
+      const uint4 v = *reinterpret_cast<const uint4 *>(a.part_o + prow * kD + 8 * q8);
+      const float w = __builtin_amdgcn_exp2f(ml.x - base) * ml.y;
+      L += w;
+      add(w, v);
     }
   }
   const float inv = (L > 0.0f) ? 1.0f / L : 0.0f;
