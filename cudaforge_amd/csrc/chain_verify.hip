@@ -558,7 +558,9 @@ __global__ __launch_bounds__(256) void plan_kernel(Args a) {
 //                            serial replay are cached;
 //   walk    (grid B, 1 wave) per pass: chunk 0, where the running value is
 //                            small and crosses a binade every doubling, is
-//                            replayed serially; later chunks apply their
+//                            walked tile by tile from records the walk builds
+//                            itself (the straddling tiles replayed serially
+//                            from LDS); later chunks apply their
 //                            functions from the exact running value, and a
 //                            chunk with a break costs a check, the break
 //                            tile's serial replay and a second check.  Any
@@ -709,7 +711,7 @@ __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
   const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
   const MwJob j = a.jobs[b];
   if (!mw_active(j, pass)) return;
-  if (c == 0 || c >= a.NC) return;  // chunk 0 is replayed serially by the walk
+  if (c == 0 || c >= a.NC) return;  // the walk builds chunk 0's records itself
   const MwElem e = mw_elem(a, b, j, pass);
   const long long rowrec = ((long long)pass * a.B + b);
   MwChunk *crec = a.crec + rowrec * a.NC;
@@ -825,6 +827,31 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
 #pragma unroll
     for (int k = 0; k < kMwTile; k += 4)
       *reinterpret_cast<float4 *>(&xs[lane * kMwTile + k]) = make_float4(x[k], x[k + 1], x[k + 2], x[k + 3]);
+    // chunk 0's tile records (lane = tile), built here as mw_records builds
+    // those of the later chunks: region guesses from an approximate prefix
+    // that starts at the exact entry value 0
+    float A = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMwTile; ++k) A += x[k];
+    const float E = wave_incl_scan_f32(A) - A;
+    int r_lo = region_of(E * (1.0f - kDelta));
+    const int r_hi = region_of((E + A) * (1.0f + kDelta));
+    bool ok = (r_lo == r_hi);
+    Inc f{kBad, kBad};
+    if (A == 0.0f) {
+      ok = true;
+      r_lo = kAnyRegion;
+      f = inc_identity();
+    } else if (ok) {
+      uint32_t I;
+      if (quantize_tile_fast(x, kMwTile, r_lo, I))
+        f = Inc{I, I};
+      else
+        quantize_tile(x, kMwTile, r_lo, f.e, f.o);
+      ok = (f.e <= kUnitsTop) && (f.o <= kUnitsTop);
+      if (!ok) f = Inc{kBad, kBad};
+    }
+    tr[lane] = MwRec{f.e, f.o, ok ? r_lo : kAnyRegion, ok ? 0 : 1};
   }
   for (int c = 1 + lane; c < min(a.NC, 1 + kMwWin); c += 64) cr[c - 1] = crec[c];
   for (int q = lane; q < nbad; q += 64) bad[q] = a.bad[rowrec * kMwMaxBad + q];
@@ -872,31 +899,31 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
     return replay16(x, tile * kMwTile, s);
   };
 
+  // chunk 0: runs of tiles applied from their records, the tiles straddling
+  // a binade (every doubling of the small running value) replayed serially
+  // from LDS
   float s = 0.0f;
-  long long found = -1;
-  // chunk 0, serially (all lanes redundantly); the next tile's values are
-  // read from LDS while this tile's adds run
+  long long found;
   {
-    float4 cur[4], nxt[4];
-    const float4 *x4 = reinterpret_cast<const float4 *>(xs);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) cur[k] = x4[k];
-    for (int t = 0; t < kMwChunkTiles && found < 0; ++t) {
-      const int tn = (t + 1 < kMwChunkTiles) ? t + 1 : t;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) nxt[k] = x4[tn * 4 + k];
+    auto item0 = [&](int i, int &reg) -> Inc {
+      const MwRec q = tr[i];
+      reg = q.reg;
+      return q.pad ? Inc{kBad, kBad} : Inc{q.e, q.o};
+    };
+    auto desc0 = [&](int i, float &s2) -> long long {
+      const float4 *x4 = reinterpret_cast<const float4 *>(xs + i * kMwTile);
       float x[kMwTile];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        x[4 * k] = cur[k].x;
-        x[4 * k + 1] = cur[k].y;
-        x[4 * k + 2] = cur[k].z;
-        x[4 * k + 3] = cur[k].w;
+        const float4 q = x4[k];
+        x[4 * k] = q.x;
+        x[4 * k + 1] = q.y;
+        x[4 * k + 2] = q.z;
+        x[4 * k + 3] = q.w;
       }
-      found = replay16(x, (long long)t * kMwTile, s);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) cur[k] = nxt[k];
-    }
+      return replay16(x, (long long)i * kMwTile, s2);
+    };
+    found = walk(kMwChunkTiles, s, cdf, r, item0, desc0);
   }
 
   // tile-level walk of chunk c from its tile t0 (records from memory)

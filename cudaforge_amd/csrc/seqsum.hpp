@@ -292,14 +292,16 @@ __device__ long long walk(int count, float &s, bool cdf, float r, const Item &it
     const int rs = region_of(s);
     const uint32_t a = units_of(s, rs);
     const int ti = t + lane;
-    bool vin = false;
+    bool vin = false, none = false;
     Inc f = inc_identity();
     if (ti < count) {
       int reg;
       const Inc v = item(ti, reg);
-      vin = (v.e != kBad) && (reg == rs || reg == kAnyRegion);
+      none = (v.e == kBad);
+      vin = !none && (reg == rs || reg == kAnyRegion);
       if (vin) f = v;
     }
+    const unsigned long long nonem = __ballot(none);
     // Without a tie-dependent item the functions are plain integers: an add
     // scan (6 DPP adds) replaces the composition scan.
     uint32_t inc;
@@ -323,6 +325,13 @@ __device__ long long walk(int count, float &s, bool cdf, float r, const Item &it
       const uint32_t tot = lane_bcast(inc, nvalid - 1);
       s = value_of(a + tot, rs);
       t += nvalid;
+      // an item without a function ended the run: replay it now instead of
+      // after another scan
+      if (nvalid < 64 && ((nonem >> nvalid) & 1ull)) {
+        const long long f2 = descend(t, s);
+        if (f2 >= 0) return f2;
+        ++t;
+      }
       continue;
     }
     const long long f2 = descend(t, s);
