@@ -104,6 +104,7 @@ struct Args {
   MwRec *trec;            // [2, B, NC*64] tile functions, per pass
   int *badcnt;            // [2, B]
   MwBad *bad;             // [2, B, kMwMaxBad]
+  float *x0;              // [2, B, kMwChunk] chunk 0's element values per pass
   int32_t *out_accept_len, *out_tokens, *out_num_emitted, *out_final, *out_eos;
 };
 
@@ -558,9 +559,9 @@ __global__ __launch_bounds__(256) void plan_kernel(Args a) {
 //                            serial replay are cached;
 //   walk    (grid B, 1 wave) per pass: chunk 0, where the running value is
 //                            small and crosses a binade every doubling, is
-//                            walked tile by tile from records the walk builds
-//                            itself (the straddling tiles replayed serially
-//                            from LDS); later chunks apply their
+//                            walked tile by tile from its records (mw_records
+//                            also stores all its values, so the straddling
+//                            tiles replay from LDS); later chunks apply their
 //                            functions from the exact running value, and a
 //                            chunk with a break costs a check, the break
 //                            tile's serial replay and a second check.  Any
@@ -711,7 +712,7 @@ __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
   const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
   const MwJob j = a.jobs[b];
   if (!mw_active(j, pass)) return;
-  if (c == 0 || c >= a.NC) return;  // the walk builds chunk 0's records itself
+  if (c >= a.NC) return;
   const MwElem e = mw_elem(a, b, j, pass);
   const long long rowrec = ((long long)pass * a.B + b);
   MwChunk *crec = a.crec + rowrec * a.NC;
@@ -755,6 +756,12 @@ __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
     if (!ok) f = Inc{kBad, kBad};
   }
   trec[tile] = MwRec{f.e, f.o, ok ? r_lo : kAnyRegion, ok ? 0 : 1};
+  if (c == 0) {  // chunk 0 is walked tile by tile: all its values go to the walk
+    float4 *dst = reinterpret_cast<float4 *>(a.x0 + rowrec * kMwChunk + lane * kMwTile);
+#pragma unroll
+    for (int k = 0; k < kMwTile; k += 4) dst[k / 4] = make_float4(x[k], x[k + 1], x[k + 2], x[k + 3]);
+    return;
+  }
   if (!ok) {  // cache the values for the walk's serial replay
     const int slot = atomicAdd(&a.badcnt[rowrec], 1);
     if (slot < kMwMaxBad) {
@@ -810,52 +817,31 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
   __shared__ MwBad bad[kMwMaxBad];
   __shared__ __align__(16) float xs[kMwChunk];
   const int b = blockIdx.x, lane = threadIdx.x;
-  const MwJob j = a.jobs[b];
-  if (!mw_active(j, pass)) return;
-  const MwElem e = mw_elem(a, b, j, pass);
   const long long rowrec = ((long long)pass * a.B + b);
   const MwChunk *crec = a.crec + rowrec * a.NC;
   const MwRec *trec = a.trec + rowrec * a.NC * kMwChunkTiles;
-  const int nbad = min(a.badcnt[rowrec], kMwMaxBad);
-  const bool cdf = (pass == kPassCdf);
-  const float r = j.u;
 
-  // chunk 0's values, the first window of chunk records and the cached tiles
+  // One round of loads before the first wait: chunk 0's values and tile
+  // records, the first window of chunk records and every cache slot (all
+  // written by mw_records for active jobs; in-bounds, unused otherwise), the
+  // job and the cache count.
   {
-    float x[kMwTile];
-    mw_tile_values(a, e, lane, x);
+    const float4 *src = reinterpret_cast<const float4 *>(a.x0 + rowrec * kMwChunk + lane * kMwTile);
+    float4 *dst = reinterpret_cast<float4 *>(xs + lane * kMwTile);
 #pragma unroll
-    for (int k = 0; k < kMwTile; k += 4)
-      *reinterpret_cast<float4 *>(&xs[lane * kMwTile + k]) = make_float4(x[k], x[k + 1], x[k + 2], x[k + 3]);
-    // chunk 0's tile records (lane = tile), built here as mw_records builds
-    // those of the later chunks: region guesses from an approximate prefix
-    // that starts at the exact entry value 0
-    float A = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kMwTile; ++k) A += x[k];
-    const float E = wave_incl_scan_f32(A) - A;
-    int r_lo = region_of(E * (1.0f - kDelta));
-    const int r_hi = region_of((E + A) * (1.0f + kDelta));
-    bool ok = (r_lo == r_hi);
-    Inc f{kBad, kBad};
-    if (A == 0.0f) {
-      ok = true;
-      r_lo = kAnyRegion;
-      f = inc_identity();
-    } else if (ok) {
-      uint32_t I;
-      if (quantize_tile_fast(x, kMwTile, r_lo, I))
-        f = Inc{I, I};
-      else
-        quantize_tile(x, kMwTile, r_lo, f.e, f.o);
-      ok = (f.e <= kUnitsTop) && (f.o <= kUnitsTop);
-      if (!ok) f = Inc{kBad, kBad};
-    }
-    tr[lane] = MwRec{f.e, f.o, ok ? r_lo : kAnyRegion, ok ? 0 : 1};
+    for (int k = 0; k < kMwTile / 4; ++k) dst[k] = src[k];
+    tr[lane] = trec[lane];
   }
   for (int c = 1 + lane; c < min(a.NC, 1 + kMwWin); c += 64) cr[c - 1] = crec[c];
-  for (int q = lane; q < nbad; q += 64) bad[q] = a.bad[rowrec * kMwMaxBad + q];
+  static_assert(kMwMaxBad <= 64, "one cache slot per lane");
+  bad[lane] = a.bad[rowrec * kMwMaxBad + lane];
+  const MwJob j = a.jobs[b];
+  const int nbad = min(a.badcnt[rowrec], kMwMaxBad);
   __syncthreads();
+  if (!mw_active(j, pass)) return;
+  const MwElem e = mw_elem(a, b, j, pass);
+  const bool cdf = (pass == kPassCdf);
+  const float r = j.u;
 
   // Serial replay of a tile's 16 values from s (CDF: first hit index).  The
   // running value never decreases (x >= 0), so the first i with r <= s_i is
@@ -1189,7 +1175,7 @@ static int max_groups(int R) { return std::max(R, 8192); }
 
 // Workspace layout (each region 256-byte aligned).
 struct WsLayout {
-  size_t part, apart, dec, ufin, jobs, res, csum_x, csum_t, crec, trec, badcnt, bad, total;
+  size_t part, apart, dec, ufin, jobs, res, csum_x, csum_t, crec, trec, badcnt, bad, x0, total;
 };
 
 static WsLayout ws_layout(int B, int K, int V, int mode) {
@@ -1216,6 +1202,7 @@ static WsLayout ws_layout(int B, int K, int V, int mode) {
   L.trec = take(mw ? 2 * (size_t)B * NC * kMwChunkTiles * sizeof(MwRec) : 0);
   L.badcnt = take(2 * (size_t)B * sizeof(int));
   L.bad = take(mw ? 2 * (size_t)B * kMwMaxBad * sizeof(MwBad) : 0);
+  L.x0 = take(mw ? 2 * (size_t)B * kMwChunk * sizeof(float) : 0);
   L.total = o;
   return L;
 }
@@ -1327,6 +1314,7 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   a.trec = (MwRec *)(ws + L.trec);
   a.badcnt = (int *)(ws + L.badcnt);
   a.bad = (MwBad *)(ws + L.bad);
+  a.x0 = (float *)(ws + L.x0);
 
   if (a.logits) {
     if (vec)
