@@ -316,6 +316,8 @@ __device__ int row_argmax(const Args &a, int r) {
 
 constexpr int kMaxK = 64;
 
+__device__ void write_job(const Args &a, int b, int n, int kind, int row, int eos_acc, float u);
+
 __global__ __launch_bounds__(64) void decide_kernel(Args a) {
   const int b = blockIdx.x, lane = threadIdx.x;
   __shared__ float pt[kMaxK], qd[kMaxK];
@@ -397,8 +399,12 @@ __global__ __launch_bounds__(64) void decide_kernel(Args a) {
     a.out_num_emitted[b] = eos_acc ? n : n + 1;
     return;
   }
-  a.dec[b] = make_int4(n, kind, row, eos_acc);
-  a.ufin[b] = uf;
+  if (a.mode == CFA_MODE_CPP) {
+    write_job(a, b, n, kind, row, eos_acc, uf);
+  } else {
+    a.dec[b] = make_int4(n, kind, row, eos_acc);
+    a.ufin[b] = uf;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -495,54 +501,53 @@ __device__ float topk_threshold(const Dist &t, int V, int top_k, double *red) {
 }
 
 // ---------------------------------------------------------------------------
-// plan: the draw each sequence still needs (python mode applies the batch
-// lock-step rule n = min_b n_b of speculative.py:166 here).
+// plan: the draw each sequence still needs.  Python mode applies the batch
+// lock-step rule n = min_b n_b of speculative.py:166 here; cpp mode's draws
+// are per sequence, so decide writes them directly.
 // ---------------------------------------------------------------------------
 
+// The job of sequence b: its draw (n, kind, row, eos_acc, uniform u) and the
+// statistics of the draw's rows, once for every kernel that reads them; also
+// resets the walk state of b.
+__device__ void write_job(const Args &a, int b, int n, int kind, int row, int eos_acc, float u) {
+  const int K = a.K;
+  MwJob j;
+  j.n = n;
+  j.kind = kind;
+  j.row = row;
+  j.eos_acc = eos_acc;
+  j.u = u;
+  j.pad[0] = j.pad[1] = j.pad[2] = 0;
+  j.tM = j.dM = 0.0f;
+  j.tInvS = j.dInvS = 1.0f;
+  if (a.logits && (j.kind == kResid || j.kind == kPlain)) {
+    const float2 ts = row_stat(a, (b / a.draws) * a.rpb + j.row);
+    j.tM = ts.x;
+    j.tInvS = ts.y;
+    if (j.kind == kResid) {
+      const float2 ds = row_stat(a, (b / a.draws) * a.rpb + K + 1 + j.row);
+      j.dM = ds.x;
+      j.dInvS = ds.y;
+    }
+  }
+  a.jobs[b] = j;
+  a.res[b] = MwRes{0.0f, 0, -1, 0};
+  a.badcnt[b] = 0;
+  a.badcnt[a.B + b] = 0;
+}
+
+// Python mode only (cpp mode writes its jobs in decide).
 __global__ __launch_bounds__(256) void plan_kernel(Args a) {
   __shared__ int nmin;
   const int K = a.K;
   if (threadIdx.x == 0) nmin = K;
   __syncthreads();
-  if (a.mode == CFA_MODE_PYTHON) {
-    int local = K;
-    for (int q = threadIdx.x; q < a.B; q += blockDim.x) local = min(local, a.dec[q].x);
-    atomicMin(&nmin, local);
-  }
+  int local = K;
+  for (int q = threadIdx.x; q < a.B; q += blockDim.x) local = min(local, a.dec[q].x);
+  atomicMin(&nmin, local);
   __syncthreads();
-  for (int b = threadIdx.x; b < a.B; b += blockDim.x) {
-    const int4 dj = a.dec[b];
-    MwJob j;
-    j.n = dj.x;
-    j.kind = dj.y;
-    j.row = dj.z;
-    j.eos_acc = dj.w;
-    j.u = a.ufin[b];
-    j.pad[0] = j.pad[1] = j.pad[2] = 0;
-    if (a.mode == CFA_MODE_PYTHON) {
-      j.n = nmin;
-      j.kind = (nmin < K) ? kResid : kPyBonus;
-      j.row = (nmin < K) ? nmin : K;
-      j.eos_acc = 0;
-    }
-    // row statistics of the draw's rows, once for every kernel that reads them
-    j.tM = j.dM = 0.0f;
-    j.tInvS = j.dInvS = 1.0f;
-    if (a.logits && (j.kind == kResid || j.kind == kPlain)) {
-      const float2 ts = row_stat(a, (b / a.draws) * a.rpb + j.row);
-      j.tM = ts.x;
-      j.tInvS = ts.y;
-      if (j.kind == kResid) {
-        const float2 ds = row_stat(a, (b / a.draws) * a.rpb + K + 1 + j.row);
-        j.dM = ds.x;
-        j.dInvS = ds.y;
-      }
-    }
-    a.jobs[b] = j;
-    a.res[b] = MwRes{0.0f, 0, -1, 0};
-    a.badcnt[b] = 0;
-    a.badcnt[a.B + b] = 0;
-  }
+  for (int b = threadIdx.x; b < a.B; b += blockDim.x)
+    write_job(a, b, nmin, (nmin < K) ? kResid : kPyBonus, (nmin < K) ? nmin : K, 0, a.ufin[b]);
 }
 
 // ---------------------------------------------------------------------------
@@ -810,6 +815,8 @@ __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
 
 constexpr int kMwWin = 256;  // chunk records staged in LDS at a time
 
+__device__ void finish_one(const Args &a, int b, const MwJob &j, int idx);
+
 __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
   using namespace seq;
   __shared__ MwChunk cr[kMwWin];
@@ -838,7 +845,10 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
   const MwJob j = a.jobs[b];
   const int nbad = min(a.badcnt[rowrec], kMwMaxBad);
   __syncthreads();
-  if (!mw_active(j, pass)) return;
+  if (!mw_active(j, pass)) {
+    if (pass == kPassCdf && a.mode == CFA_MODE_CPP && lane == 0) finish_one(a, b, j, -1);
+    return;
+  }
   const MwElem e = mw_elem(a, b, j, pass);
   const bool cdf = (pass == kPassCdf);
   const float r = j.u;
@@ -993,7 +1003,9 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
       a.res[b].S = s;
       a.res[b].fallback = (s <= 1e-6f) ? 1 : 0;  // speculative.cpp:37
     } else {
-      a.res[b].idx = (found < 0 || found >= a.V) ? a.V - 1 : (int)found;
+      const int idx = (found < 0 || found >= a.V) ? a.V - 1 : (int)found;
+      a.res[b].idx = idx;
+      if (a.mode == CFA_MODE_CPP) finish_one(a, b, j, idx);
     }
   }
 }
@@ -1027,13 +1039,11 @@ __global__ __launch_bounds__(kSampleNT) void pybonus_kernel(Args a) {
 // finish: per-sequence outputs.
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(64) void finish_kernel(Args a) {
-  const int b = blockIdx.x * 64 + threadIdx.x;
-  if (b >= a.B) return;
+// Outputs of sequence b; idx is the drawn token (ignored without a draw).
+__device__ void finish_one(const Args &a, int b, const MwJob &j, int idx) {
   const int K = a.K;
-  const MwJob j = a.jobs[b];
   const int n = j.n, eos_acc = j.eos_acc;
-  int fin = (j.kind == kNone) ? -1 : a.res[b].idx;
+  int fin = (j.kind == kNone) ? -1 : idx;
   int32_t *ot = a.out_tokens + (long long)b * (K + 1);
   for (int q = 0; q <= K; ++q) {
     int v = -1;
@@ -1046,6 +1056,14 @@ __global__ __launch_bounds__(64) void finish_kernel(Args a) {
   a.out_final[b] = fin;
   a.out_eos[b] = (a.mode == CFA_MODE_CPP) ? ((eos_acc || fin == a.eos) ? 1 : 0) : 0;
   a.out_num_emitted[b] = eos_acc ? n : n + 1;
+}
+
+// Python mode (cpp mode finishes each sequence at the end of its last walk).
+__global__ __launch_bounds__(64) void finish_kernel(Args a) {
+  const int b = blockIdx.x * 64 + threadIdx.x;
+  if (b >= a.B) return;
+  const MwJob j = a.jobs[b];
+  finish_one(a, b, j, a.res[b].idx);
 }
 
 // Optional: write the probabilities the verification used.
@@ -1327,7 +1345,7 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   CFA_LAUNCH("chain_decide", decide_kernel, dim3(B), dim3(64), 0, st, a);
   if (mode != CFA_MODE_GREEDY) {
     const dim3 cg((a.NC + kMwNT / 64 - 1) / (kMwNT / 64), B);
-    CFA_LAUNCH("chain_plan", plan_kernel, dim3(1), dim3(256), 0, st, a);
+    if (mode == CFA_MODE_PYTHON) CFA_LAUNCH("chain_plan", plan_kernel, dim3(1), dim3(256), 0, st, a);
     CFA_LAUNCH("chain_mw_sums", mw_sums_kernel, cg, dim3(kMwNT), 0, st, a);
     CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassSum);
     CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassSum);
@@ -1335,7 +1353,8 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
     CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassCdf);
     if (mode == CFA_MODE_PYTHON)
       CFA_LAUNCH("chain_pybonus", pybonus_kernel, dim3(B), dim3(kSampleNT), 0, st, a);
-    CFA_LAUNCH("chain_finish", finish_kernel, dim3((B + 63) / 64), dim3(64), 0, st, a);
+    if (mode == CFA_MODE_PYTHON)
+      CFA_LAUNCH("chain_finish", finish_kernel, dim3((B + 63) / 64), dim3(64), 0, st, a);
   }
   if (out_target_probs || out_draft_probs) {
     const int gx = std::min(64, (V + 255) / 256);
