@@ -325,14 +325,9 @@ __device__ long long walk(int count, float &s, bool cdf, float r, const Item &it
       const uint32_t tot = lane_bcast(inc, nvalid - 1);
       s = value_of(a + tot, rs);
       t += nvalid;
-      // an item without a function ended the run: replay it now instead of
-      // after another scan
-      if (nvalid < 64 && ((nonem >> nvalid) & 1ull)) {
-        const long long f2 = descend(t, s);
-        if (f2 >= 0) return f2;
-        ++t;
-      }
-      continue;
+      // an item without a function that ends the run is replayed right away
+      // (one descend call site: the replay is inlined once)
+      if (nvalid == 64 || ((nonem >> nvalid) & 1ull) == 0ull || t >= count) continue;
     }
     const long long f2 = descend(t, s);
     if (f2 >= 0) return f2;
