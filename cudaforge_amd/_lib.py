@@ -113,7 +113,7 @@ SIGNATURES: dict[str, tuple] = {
     "cfa_tree_attention_workspace_size": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "cfa_tree_attention": (
         _i,
-        [_p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _p, _i64, _i, _i, _i, _i, _i, _f, _i, _i,
+        [_p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _p, _i64, _i, _i, _i, _i, _i, _i, _f, _i, _i,
          _p, _p, _sz, _p],
     ),
     "cfa_tree_verify": (

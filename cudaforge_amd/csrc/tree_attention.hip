@@ -8,10 +8,13 @@
 //   pool[block][layer][kv_head][slot][head_dim]  (bf16)
 // -- the per-block layer stride of csrc/src/memory/paged_kv_cache.cpp:13-21
 // and the block addressing of :409-421 -- and the tree's own K/V have already
-// been appended at positions ctx_b .. ctx_b + N - 1.
+// been appended at positions ctx_b .. ctx_b + N - 1.  The queries are the
+// nodes first_node .. N - 1 (all of them for a verify step; the newest tree
+// level for a draft model growing its tree).  head_dim is 128 or 64 (a
+// template parameter).
 //
-// One work-group = (split, kv head, sequence); its 8 waves hold all G*N query
-// rows (two 16-row tiles each, Q^T in registers, pre-scaled by
+// One work-group = (split, kv head, sequence); its 8 waves hold all the
+// G * (N - first_node) query rows (two 16-row tiles each, Q^T in registers, pre-scaled by
 // scale*log2(e)).  64-key K and V tiles move HBM -> LDS with direct 16-byte
 // global_load_lds transfers (no register staging) into two rings (K: 4
 // stages, V: 5), three tiles ahead of the tile being computed; the split's
@@ -34,11 +37,11 @@
 // SIMD and run one phase apart, so one's exponentials overlap the other's
 // MFMAs.
 //
-// LDS layouts (256-byte rows, 16-byte chunks XOR-swizzled so that the MFMA
-// operand reads of one wave hit distinct banks):
+// LDS layouts (2 * head_dim-byte rows, 16-byte chunks XOR-swizzled so that
+// the MFMA operand reads of one wave hit distinct banks; k_swz / v_swz):
 //   K: row R holds key 32*(R/32) + 8*((R/4)%4) + 4*((R/16)%2) + R%4 (each
-//      16-row MFMA tile reads consecutive rows); chunk c sits at c ^ (R % 16).
-//   V: row = key; chunk c sits at c ^ 2*((key % 4) | 4*((key / 8) % 2)).
+//      16-row MFMA tile reads consecutive rows).
+//   V: row = key.
 //
 // Softmax rescaling is lazy: a column's exponent base b only moves when its
 // running maximum exceeds it by more than kRescaleSlack (log2 units), so P^T
@@ -61,18 +64,29 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kD = 128;                       // head_dim
 constexpr int kKT = 64;                       // keys per tile
 constexpr int kWaves = 8;
 constexpr int kNT = kWaves * 64;              // threads per work-group
 constexpr int kQT = 2;                        // 16-row query tiles per wave
 constexpr int kMaxRows = kWaves * kQT * 16;   // 256 query rows per work-group
-constexpr int kRowBytes = kD * 2;             // one K or V row, bf16
-constexpr int kTileBytes = kKT * kRowBytes;   // 16 KiB
 constexpr int kKStages = 4;                   // K-tile ring (tile u: stage u % 4)
 constexpr int kVStages = 5;                   // V-tile ring (read one iteration after K)
-constexpr int kLoadsPerTile = 4;              // global_load_lds per wave per tile
 constexpr float kRescaleSlack = 8.0f;         // log2 units
+
+// Layout constants of head size D (64 or 128): K / V rows of D bf16 values,
+// D / 8 16-byte chunks each.
+template <int D>
+struct Geo {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static constexpr int kRowBytes = D * 2;             // one K or V row
+  static constexpr int kTileBytes = kKT * kRowBytes;  // 8 or 16 KiB
+  static constexpr int kChunks = D / 8;               // 16-byte chunks per row
+  static constexpr int kRowsPerLoad = 1024 / kRowBytes;  // rows per 1 KiB transfer
+  static constexpr int kLoadsPerTile = 2 * (8 / kRowsPerLoad);  // K + V transfers per wave
+  static constexpr int kKK = D / 32;                  // k-slices of the QK product
+  static constexpr int kDT = D / 16;                  // 16-row blocks of O^T
+  static constexpr int kMfma = 2 * kDT * kQT + 2 * kQT + 4 * kKK * kQT;  // per MFMA phase
+};
 #ifndef CFA_TA_SGB
 #define CFA_TA_SGB 1
 #endif
@@ -80,17 +94,18 @@ constexpr int kMaxGroups = 1024;              // 16-key groups per split (page l
 constexpr int kMaxTilesPerSplit = kMaxGroups / (kKT / 16);
 
 struct Args {
-  const uint16_t *q;       // [B, N, Hq, D]
+  const uint16_t *q;       // [B, Nq, Hq, D]
   const uint16_t *kpool;   // [blocks, layers, Hkv, bs, D]
   const uint16_t *vpool;
   const int32_t *bt;       // [B, max_blocks]
   const int32_t *ctx;      // [B]
   const uint64_t *mask;    // [N] or [B, N]
   long long mask_sb;
-  uint16_t *out;           // [B, N, Hq, D]
+  uint16_t *out;           // [B, Nq, Hq, D]
   uint16_t *part_o;        // [S, B, Hkv, rows, D] partial outputs O / l, bf16
   float2 *part_ml;         // [S, B, Hkv, rows] (exponent base in log2 units, sum)
   int B, N, Hq, Hkv, G, rows;
+  int q0, Nq;              // query nodes q0 .. N - 1 (Nq = N - q0 of them)
   int max_blocks, num_blocks, num_layers, layer, bs;
   int splits, tiles_per_split;
   float scale_log2;        // sm_scale * log2(e)
@@ -105,20 +120,34 @@ __device__ __forceinline__ int k_key_of_row(int R) {
   return (R & ~31) + ((R >> 2) & 3) * 8 + ((R >> 4) & 1) * 4 + (R & 3);
 }
 
-// Swizzle of V-tile row `key`: 2 * ((key % 4) | 4 * ((key / 8) % 2)).
-__device__ __forceinline__ int v_swz(int key) { return ((key & 3) | ((key >> 1) & 4)) << 1; }
+// LDS swizzles (16-byte chunk c of a row sits at position c ^ swizzle):
+//   K-tile row R:  D = 128: R % 16;  D = 64: (R / 2) % 8.  A 16-row MFMA
+//     operand read then touches every bank once per 16 lanes.
+//   V-tile row key: twice the 32-byte block swizzle vh, the same for keys k
+//     and k + 4 (one transposed-read pair); D = 128: (key % 4) | 4 ((key / 8)
+//     % 2); D = 64: ((key / 2) % 2) | 2 ((key / 8) % 2).  The four rows of one
+//     transposed read then land in distinct banks.
+template <int D>
+__device__ __forceinline__ int k_swz(int R) {
+  return D == 128 ? (R & 15) : ((R >> 1) & 7);
+}
+template <int D>
+__device__ __forceinline__ int v_swz(int key) {
+  return D == 128 ? (((key & 3) | ((key >> 1) & 4)) << 1) : ((((key >> 1) & 1) | ((key >> 2) & 2)) << 1);
+}
 
 // Pool element offset of the row holding position gstart = min(16 gi,
 // nkeys - 1), the first row 16-key group gi reads.  Page index and block id
 // are clamped into the table and the pool, so a corrupt table can never send
 // a load outside the pool.
+template <int D>
 __device__ __forceinline__ long long group_row_offset(const Args &a, const int32_t *btb, int gi,
                                                       int nkeys, int h) {
   const int gstart = min(gi * 16, nkeys - 1);
   const int page = min(gstart / a.bs, a.max_blocks - 1);
   const int blk = min(max(btb[page], 0), a.num_blocks - 1);
-  return (((long long)blk * a.num_layers + a.layer) * a.Hkv + h) * (long long)(a.bs * kD) +
-         (long long)(gstart - page * a.bs) * kD;
+  return (((long long)blk * a.num_layers + a.layer) * a.Hkv + h) * (long long)(a.bs * D) +
+         (long long)(gstart - page * a.bs) * D;
 }
 
 __device__ __forceinline__ long long uniform_i64(long long v) {
@@ -127,28 +156,31 @@ __device__ __forceinline__ long long uniform_i64(long long v) {
   return (long long)(((unsigned long long)hi << 32) | lo);
 }
 
-// Issue this wave's share of the tile at key kbase: two 1 KiB K transfers
-// (K-tile LDS rows 8w..8w+7) and two 1 KiB V transfers (keys 8w..8w+7).  Each
-// transfer covers four keys of one 16-key group, and a group never straddles
-// a page (block_size % 16 == 0).  Keys at or past nkeys re-read key
-// nkeys - 1: a finite, in-bounds row that the mask then hides.  gtab holds
-// the split's group row offsets (group_row_offset) from group g0 on.
+// Issue this wave's share of the tile at key kbase: K-tile LDS rows 8w..8w+7
+// and V keys 8w..8w+7, in 1 KiB transfers of 1024 / (2 D) rows.  Each
+// transfer stays inside one 16-key group, and a group never straddles a page
+// (block_size % 16 == 0).  Keys at or past nkeys re-read key nkeys - 1: a
+// finite, in-bounds row that the mask then hides.  gtab holds the split's
+// group row offsets (group_row_offset) from group g0 on.
+template <int D>
 __device__ __forceinline__ void issue_tile(const Args &a, const long long *gtab, int g0, int kbase,
                                            int nkeys, uint8_t *kdst, uint8_t *vdst, int wave,
                                            int lane) {
-  const int sub = lane >> 4, pc = lane & 15;
+  using Gm = Geo<D>;
+  constexpr int RPL = Gm::kRowsPerLoad;
+  const int sub = lane / Gm::kChunks, pc = lane % Gm::kChunks;
   {
     // K: the wave's rows hold keys of the tile's 16-group 2 (w / 4) + (w % 2)
     const int gi = kbase / 16 + 2 * (wave >> 2) + (wave & 1);
     const int gstart = min(gi * 16, nkeys - 1);
     const uint16_t *base = a.kpool + uniform_i64(gtab[gi - g0]);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int R = 8 * wave + 4 * j + sub;
-      const int c = pc ^ (R & 15);
+    for (int j = 0; j < 8 / RPL; ++j) {
+      const int R = 8 * wave + RPL * j + sub;
+      const int c = pc ^ k_swz<D>(R);
       const int pos = min(kbase + k_key_of_row(R), nkeys - 1);
-      dma16(base + ((pos - gstart) * kD + c * 8),
-            (CFA_LDS void *)(kdst + (8 * wave + 4 * j) * kRowBytes));
+      dma16(base + ((pos - gstart) * D + c * 8),
+            (CFA_LDS void *)(kdst + (8 * wave + RPL * j) * Gm::kRowBytes));
     }
   }
   {
@@ -157,12 +189,12 @@ __device__ __forceinline__ void issue_tile(const Args &a, const long long *gtab,
     const int gstart = min(gi * 16, nkeys - 1);
     const uint16_t *base = a.vpool + uniform_i64(gtab[gi - g0]);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int key = 8 * wave + 4 * j + sub;
-      const int c = pc ^ v_swz(key);
+    for (int j = 0; j < 8 / RPL; ++j) {
+      const int key = 8 * wave + RPL * j + sub;
+      const int c = pc ^ v_swz<D>(key);
       const int pos = min(kbase + key, nkeys - 1);
-      dma16(base + ((pos - gstart) * kD + c * 8),
-            (CFA_LDS void *)(vdst + (8 * wave + 4 * j) * kRowBytes));
+      dma16(base + ((pos - gstart) * D + c * 8),
+            (CFA_LDS void *)(vdst + (8 * wave + RPL * j) * Gm::kRowBytes));
     }
   }
 }
@@ -200,17 +232,19 @@ struct Probs {
   bf16x8 p[kQT][2];
 };
 
+template <int D>
 struct Lane {
-  bf16x8 qf[kQT][4];   // Q^T columns pre-scaled by scale*log2(e)
-  uint64_t anc[kQT];   // ancestor-or-self masks of the wave's columns
-  int koff[4];         // K-tile LDS byte offsets of this lane's operand reads
-  int vbase, vh;       // V-tile transposed-read offset and swizzle
-  int g;               // lane / 16
+  bf16x8 qf[kQT][D / 32];  // Q^T columns pre-scaled by scale*log2(e)
+  uint64_t anc[kQT];       // ancestor-or-self masks of the wave's columns
+  int koff[D / 32];        // K-tile LDS byte offsets of this lane's operand reads
+  int vbase, vh;           // V-tile transposed-read offset and swizzle
+  int g;                   // lane / 16
 };
 
 // S^T = K Q^T - base: the accumulators start at -b so that the products come
 // out relative to the column's exponent base.
-__device__ __forceinline__ void qk_tile(const Lane &ln, const uint8_t *Ks, const float *b,
+template <int D>
+__device__ __forceinline__ void qk_tile(const Lane<D> &ln, const uint8_t *Ks, const float *b,
                                         Scores &S) {
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt)
@@ -219,13 +253,13 @@ __device__ __forceinline__ void qk_tile(const Lane &ln, const uint8_t *Ks, const
 #pragma unroll
       for (int T = 0; T < 2; ++T) S.s[qt][blk][T] = f32x4{-b[qt], -b[qt], -b[qt], -b[qt]};
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk)
+  for (int kk = 0; kk < D / 32; ++kk)
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
       for (int T = 0; T < 2; ++T) {
-        const uint4 kv =
-            *reinterpret_cast<const uint4 *>(Ks + (blk * 32 + T * 16) * kRowBytes + ln.koff[kk]);
+        const uint4 kv = *reinterpret_cast<const uint4 *>(Ks + (blk * 32 + T * 16) * Geo<D>::kRowBytes +
+                                                          ln.koff[kk]);
         const bf16x8 kf = __builtin_bit_cast(bf16x8, kv);
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt)
@@ -245,8 +279,9 @@ struct Softmax {
 // scores relative to each column's exponent base b; the base only moves when
 // a column's maximum exceeds it by more than kRescaleSlack, which also
 // rescales O and l (they hold tiles < t, so this precedes tile t's PV).
-__device__ __forceinline__ void valu_phase(const Lane &ln, int kbase, int ctx, Scores &S,
-                                           Softmax &sm, f32x4 (&o)[kQT][kD / 16],
+template <int D>
+__device__ __forceinline__ void valu_phase(const Lane<D> &ln, int kbase, int ctx, Scores &S,
+                                           Softmax &sm, f32x4 (&o)[kQT][D / 16],
                                            f32x4 (&lacc)[kQT], Probs &P) {
   if (kbase + kKT > ctx) {
 #pragma unroll
@@ -289,7 +324,7 @@ __device__ __forceinline__ void valu_phase(const Lane &ln, int kbase, int ctx, S
       sm.valid[qt] = sm.valid[qt] || resc[qt];
       lacc[qt] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < kD / 16; ++dt) o[qt][dt] *= alpha;
+      for (int dt = 0; dt < D / 16; ++dt) o[qt][dt] *= alpha;
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
@@ -317,9 +352,11 @@ __device__ __forceinline__ void valu_phase(const Lane &ln, int kbase, int ctx, S
 // issued right behind its predecessor stalls the matrix pipe.  Lane (g, col)
 // reads V rows blk*32 + 8g + 0..7 at d = dt*16 + col through two transposed
 // 4x16 reads.
-__device__ __forceinline__ void mfma_phase(const Lane &ln, const uint8_t *Knext, const uint8_t *Vs,
+template <int D>
+__device__ __forceinline__ void mfma_phase(const Lane<D> &ln, const uint8_t *Knext, const uint8_t *Vs,
                                            const float *b, const Probs &P, Scores &S,
-                                           f32x4 (&o)[kQT][kD / 16], f32x4 (&lacc)[kQT]) {
+                                           f32x4 (&o)[kQT][D / 16], f32x4 (&lacc)[kQT]) {
+  constexpr int RB = Geo<D>::kRowBytes;
   bf16x8 ones;
 #pragma unroll
   for (int j = 0; j < 8; ++j) ones[j] = (__bf16)1.0f;
@@ -329,10 +366,10 @@ __device__ __forceinline__ void mfma_phase(const Lane &ln, const uint8_t *Knext,
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
-    for (int dt = 0; dt < kD / 16; ++dt) {
-      const uint8_t *vp = Vs + blk * 32 * kRowBytes + ln.vbase + ((dt ^ ln.vh) << 5);
+    for (int dt = 0; dt < D / 16; ++dt) {
+      const uint8_t *vp = Vs + blk * 32 * RB + ln.vbase + ((dt ^ ln.vh) << 5);
       const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((CFA_LDS i16x4 *)vp);
-      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((CFA_LDS i16x4 *)(vp + 4 * kRowBytes));
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((CFA_LDS i16x4 *)(vp + 4 * RB));
       const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt)
@@ -345,13 +382,13 @@ __device__ __forceinline__ void mfma_phase(const Lane &ln, const uint8_t *Knext,
     for (int qt = 0; qt < kQT; ++qt)
       lacc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, P.p[qt][blk], lacc[qt], 0, 0, 0);
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk)
+  for (int kk = 0; kk < D / 32; ++kk)
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
       for (int T = 0; T < 2; ++T) {
         const bf16x8 kf = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const uint4 *>(Knext + (blk * 32 + T * 16) * kRowBytes + ln.koff[kk]));
+            bf16x8, *reinterpret_cast<const uint4 *>(Knext + (blk * 32 + T * 16) * RB + ln.koff[kk]));
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt)
           S.s[qt][blk][T] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -362,14 +399,18 @@ __device__ __forceinline__ void mfma_phase(const Lane &ln, const uint8_t *Knext,
   // reads after every pair of MFMAs
   __builtin_amdgcn_sched_group_barrier(0x0100, 8, 0);
 #pragma unroll
-  for (int j = 0; j < 34; ++j) {
+  for (int j = 0; j < Geo<D>::kMfma / 2; ++j) {
     __builtin_amdgcn_sched_group_barrier(0x0008, 2, 0);
     __builtin_amdgcn_sched_group_barrier(0x0100, 2, 0);
   }
 #endif
 }
 
+template <int D>
 __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
+  using Gm = Geo<D>;
+  constexpr int kTileBytes = Gm::kTileBytes;
+  constexpr int kLoadsPerTile = Gm::kLoadsPerTile;
   __shared__ __align__(16) uint8_t kring[kKStages * kTileBytes];
   __shared__ __align__(16) uint8_t vring[kVStages * kTileBytes];
   __shared__ long long gtab[kMaxGroups];
@@ -387,9 +428,9 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
   const int t1 = min(ntiles, t0 + a.tiles_per_split);
   const int g0 = t0 * (kKT / 16);
 
-  // query rows of this wave: r = node * G + head-in-group; Q^T is scaled by
-  // scale*log2(e) once here so that scores come out in log2 units
-  Lane ln;
+  // query rows of this wave: r = (node - q0) * G + head-in-group; Q^T is
+  // scaled by scale*log2(e) once here so that scores come out in log2 units
+  Lane<D> ln;
   ln.g = g;
   bool qvalid[kQT];
   {
@@ -398,12 +439,12 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
     for (int qt = 0; qt < kQT; ++qt) {
       const int r = (wave * kQT + qt) * 16 + col;
       qvalid[qt] = r < a.rows;
-      const int node = qvalid[qt] ? r / a.G : 0, hg = r % a.G;
-      ln.anc[qt] = qvalid[qt] ? a.mask[(long long)b * a.mask_sb + node] & node_bits : 0ull;
+      const int nl = qvalid[qt] ? r / a.G : 0, hg = r % a.G;
+      ln.anc[qt] = qvalid[qt] ? a.mask[(long long)b * a.mask_sb + a.q0 + nl] & node_bits : 0ull;
       const uint16_t *qp =
-          a.q + (((long long)b * a.N + node) * a.Hq + (long long)h * a.G + hg) * kD;
+          a.q + (((long long)b * a.Nq + nl) * a.Hq + (long long)h * a.G + hg) * D;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
+      for (int kk = 0; kk < D / 32; ++kk) {
         const uint4 v = qvalid[qt] ? ld_g16(qp + kk * 32 + g * 8) : make_uint4(0, 0, 0, 0);
         const bf16x8 raw = __builtin_bit_cast(bf16x8, v);
 #pragma unroll
@@ -412,25 +453,26 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
     }
   }
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) ln.koff[kk] = col * kRowBytes + (((kk * 4 + g) ^ col) << 4);
+  for (int kk = 0; kk < D / 32; ++kk)
+    ln.koff[kk] = col * Gm::kRowBytes + (((kk * 4 + g) ^ k_swz<D>(col)) << 4);
   {
     const int vrow = 8 * g + (col >> 2);
-    ln.vh = v_swz(vrow) >> 1;
-    ln.vbase = vrow * kRowBytes + ((col >> 1) & 1) * 16 + (col & 1) * 8;
+    ln.vh = v_swz<D>(vrow) >> 1;
+    ln.vbase = vrow * Gm::kRowBytes + ((col >> 1) & 1) * 16 + (col & 1) * 8;
   }
 
   // the split's page lookups, once
   {
     const int32_t *btb = a.bt + (long long)b * a.max_blocks;
     const int ng = (t1 - t0) * (kKT / 16);
-    for (int i = tid; i < ng; i += kNT) gtab[i] = group_row_offset(a, btb, g0 + i, nkeys, h);
+    for (int i = tid; i < ng; i += kNT) gtab[i] = group_row_offset<D>(a, btb, g0 + i, nkeys, h);
   }
   // Q and the table are in; settling every load here also tells the compiler
   // that nothing it issued is outstanding inside the loop below
   wait_vmcnt<0>();
   __syncthreads();
 
-  f32x4 o[kQT][kD / 16];
+  f32x4 o[kQT][D / 16];
   f32x4 lacc[kQT];
   Softmax sm;
 #pragma unroll
@@ -439,12 +481,12 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
     sm.valid[qt] = false;
     lacc[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int dt = 0; dt < kD / 16; ++dt) o[qt][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int dt = 0; dt < D / 16; ++dt) o[qt][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
   if (t0 < t1) {
     for (int u = t0; u < min(t0 + 3, t1); ++u)
-      issue_tile(a, gtab, g0, u * kKT, nkeys, kring + ((u - t0) % kKStages) * kTileBytes,
+      issue_tile<D>(a, gtab, g0, u * kKT, nkeys, kring + ((u - t0) % kKStages) * kTileBytes,
                  vring + ((u - t0) % kVStages) * kTileBytes, wave, lane);
     // tile t0 has landed once at most the other prologue tiles are in flight
     const int later = min(t0 + 3, t1) - 1 - t0;
@@ -474,7 +516,7 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
         block_barrier();
         if (t + 3 < t1) {
           const int u = t + 3 - t0;
-          issue_tile(a, gtab, g0, (t + 3) * kKT, nkeys, kring + (u % kKStages) * kTileBytes,
+          issue_tile<D>(a, gtab, g0, (t + 3) * kKT, nkeys, kring + (u % kKStages) * kTileBytes,
                      vring + (u % kVStages) * kTileBytes, wave, lane);
         }
       } else {
@@ -483,7 +525,7 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
         block_barrier();
         if (t + 3 < t1) {
           const int u = t + 3 - t0;
-          issue_tile(a, gtab, g0, (t + 3) * kKT, nkeys, kring + (u % kKStages) * kTileBytes,
+          issue_tile<D>(a, gtab, g0, (t + 3) * kKT, nkeys, kring + (u % kKStages) * kTileBytes,
                      vring + (u % kVStages) * kTileBytes, wave, lane);
         }
       }
@@ -509,11 +551,11 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
     if (!qvalid[qt]) continue;
     const int r = (wave * kQT + qt) * 16 + col;
     if (a.splits == 1) {
-      const int node = r / a.G, hg = r % a.G;
-      uint16_t *op = a.out + (((long long)b * a.N + node) * a.Hq + (long long)h * a.G + hg) * kD;
+      const int nl = r / a.G, hg = r % a.G;
+      uint16_t *op = a.out + (((long long)b * a.Nq + nl) * a.Hq + (long long)h * a.G + hg) * D;
       const float inv = (ls > 0.0f) ? 1.0f / ls : 0.0f;
 #pragma unroll
-      for (int dt = 0; dt < kD / 16; ++dt) {
+      for (int dt = 0; dt < D / 16; ++dt) {
         uint16_t v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = __builtin_bit_cast(uint16_t, (__bf16)(o[qt][dt][i] * inv));
@@ -525,10 +567,10 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
     } else {
       // normalised partial in bf16 (the merge weighs it by its sum l)
       const long long prow = (((long long)split * a.B + b) * a.Hkv + h) * a.rows + r;
-      uint16_t *pp = a.part_o + prow * kD;
+      uint16_t *pp = a.part_o + prow * D;
       const float inv = (ls > 0.0f) ? 1.0f / ls : 0.0f;
 #pragma unroll
-      for (int dt = 0; dt < kD / 16; ++dt) {
+      for (int dt = 0; dt < D / 16; ++dt) {
         uint2 w;
         w.x = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(o[qt][dt][0] * inv)) |
               ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(o[qt][dt][1] * inv)) << 16);
@@ -542,14 +584,16 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
 }
 
 // Log-sum-exp merge of the splits: out = sum_s w_s l_s o_s / sum_s w_s l_s
-// with w_s = 2^(m_s - max m) and o_s the normalised bf16 partial; 16 threads
-// per query row, eight d-values (one 16-byte load per split) per thread,
-// sixteen rows per work-group.  Up to kMergeRegs splits are loaded in one
-// round before any arithmetic.
+// with w_s = 2^(m_s - max m) and o_s the normalised bf16 partial; D / 8
+// threads per query row, eight d-values (one 16-byte load per split) per
+// thread, 2048 / D rows per work-group.  Up to kMergeRegs splits are loaded in
+// one round before any arithmetic.
 constexpr int kMergeRegs = 4;  // splits merged from registers in one round of loads
+template <int D>
 __global__ __launch_bounds__(256) void tree_merge_kernel(Args a) {
-  const long long row_g = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int q8 = threadIdx.x & 15;
+  constexpr int kTPR = D / 8;  // threads per row
+  const long long row_g = (long long)blockIdx.x * (256 / kTPR) + threadIdx.x / kTPR;
+  const int q8 = threadIdx.x % kTPR;
   const long long total = (long long)a.B * a.Hkv * a.rows;
   if (row_g >= total) return;
   const int r = (int)(row_g % a.rows);
@@ -576,7 +620,7 @@ __global__ __launch_bounds__(256) void tree_merge_kernel(Args a) {
       if (s < a.splits) {
         const long long prow = prow0 + s * split_stride;
         ml[s] = a.part_ml[prow];
-        v[s] = *reinterpret_cast<const uint4 *>(a.part_o + prow * kD + 8 * q8);
+        v[s] = *reinterpret_cast<const uint4 *>(a.part_o + prow * D + 8 * q8);
       }
     }
     float M = -INFINITY;
@@ -600,15 +644,15 @@ __global__ __launch_bounds__(256) void tree_merge_kernel(Args a) {
     for (int s = 0; s < a.splits; ++s) {
       const long long prow = prow0 + s * split_stride;
       const float2 ml = a.part_ml[prow];
-      const uint4 v = *reinterpret_cast<const uint4 *>(a.part_o + prow * kD + 8 * q8);
+      const uint4 v = *reinterpret_cast<const uint4 *>(a.part_o + prow * D + 8 * q8);
       const float w = __builtin_amdgcn_exp2f(ml.x - base) * ml.y;
       L += w;
       add(w, v);
     }
   }
   const float inv = (L > 0.0f) ? 1.0f / L : 0.0f;
-  const int node = r / a.G, hg = r % a.G;
-  uint16_t *op = a.out + (((long long)b * a.N + node) * a.Hq + (long long)h * a.G + hg) * kD;
+  const int nl = r / a.G, hg = r % a.G;
+  uint16_t *op = a.out + (((long long)b * a.Nq + nl) * a.Hq + (long long)h * a.G + hg) * D;
   uint4 w;
   uint32_t *ws = reinterpret_cast<uint32_t *>(&w);
 #pragma unroll
@@ -643,21 +687,23 @@ static void split_plan(int B, int Hkv, int max_keys, int splits_req, int &splits
 
 extern "C" size_t cfa_tree_attention_workspace_size(int B, int N, int n_q_heads, int n_kv_heads,
                                                     int head_dim, int max_keys, int num_splits) {
-  if (B <= 0 || N <= 0 || n_kv_heads <= 0 || n_q_heads <= 0 || head_dim != kD) return 0;
+  if (B <= 0 || N <= 0 || n_kv_heads <= 0 || n_q_heads <= 0 || (head_dim != 64 && head_dim != 128))
+    return 0;
   int splits = 1, tps = 1;
   split_plan(B, n_kv_heads, max_keys, num_splits, splits, tps);
   if (splits == 1) return 256;
   const int G = n_q_heads / n_kv_heads;
   const size_t rows = (size_t)G * N;
   const size_t prows = (size_t)splits * B * n_kv_heads * rows;
-  return align256(prows * kD * sizeof(uint16_t)) + align256(prows * sizeof(float2));
+  return align256(prows * head_dim * sizeof(uint16_t)) + align256(prows * sizeof(float2));
 }
 
 extern "C" int cfa_tree_attention(const void *q, const void *k_pool, const void *v_pool,
                                   const int32_t *block_tables, int max_blocks_per_seq,
                                   const int32_t *ctx_lens, int num_blocks, int num_layers,
                                   int layer, int block_size, const uint64_t *tree_mask,
-                                  int64_t tree_mask_stride_b, int B, int N, int n_q_heads,
+                                  int64_t tree_mask_stride_b, int B, int N, int first_node,
+                                  int n_q_heads,
                                   int n_kv_heads, int head_dim, float sm_scale, int max_keys,
                                   int num_splits, void *out, void *workspace,
                                   size_t workspace_bytes, void *stream) {
@@ -666,11 +712,14 @@ extern "C" int cfa_tree_attention(const void *q, const void *k_pool, const void 
   if (!q || !k_pool || !v_pool || !block_tables || !ctx_lens || !tree_mask || !out)
     return fail_arg("null pointer argument");
   if (B <= 0 || N <= 0 || N > 64) return fail_arg("need B > 0 and 0 < N <= 64 tree nodes");
-  if (head_dim != kD) return fail_arg("head_dim must be 128");
+  if (first_node < 0 || first_node >= N) return fail_arg("need 0 <= first_node < N");
+  if (head_dim != 64 && head_dim != 128) return fail_arg("head_dim must be 64 or 128");
   if (n_kv_heads <= 0 || n_q_heads <= 0 || n_q_heads % n_kv_heads)
     return fail_arg("n_q_heads must be a positive multiple of n_kv_heads");
   const int G = n_q_heads / n_kv_heads;
-  if (G * N > kMaxRows) return fail_arg("(n_q_heads / n_kv_heads) * N must be at most 256");
+  const int Nq = N - first_node;
+  if (G * Nq > kMaxRows)
+    return fail_arg("(n_q_heads / n_kv_heads) * (N - first_node) must be at most 256");
   if (block_size <= 0 || block_size % 16) return fail_arg("block_size must be a multiple of 16");
   if (num_blocks <= 0 || num_layers <= 0 || layer < 0 || layer >= num_layers)
     return fail_arg("bad pool geometry (num_blocks, num_layers, layer)");
@@ -692,7 +741,9 @@ extern "C" int cfa_tree_attention(const void *q, const void *k_pool, const void 
   a.Hq = n_q_heads;
   a.Hkv = n_kv_heads;
   a.G = G;
-  a.rows = G * N;
+  a.q0 = first_node;
+  a.Nq = Nq;
+  a.rows = G * Nq;
   a.max_blocks = max_blocks_per_seq;
   a.num_blocks = num_blocks;
   a.num_layers = num_layers;
@@ -700,21 +751,28 @@ extern "C" int cfa_tree_attention(const void *q, const void *k_pool, const void 
   a.bs = block_size;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   split_plan(B, n_kv_heads, max_keys, num_splits, a.splits, a.tiles_per_split);
-  const size_t need = cfa_tree_attention_workspace_size(B, N, n_q_heads, n_kv_heads, head_dim,
+  const size_t need = cfa_tree_attention_workspace_size(B, Nq, n_q_heads, n_kv_heads, head_dim,
                                                         max_keys, num_splits);
   if (a.splits > 1) {
     if (!workspace || workspace_bytes < need)
       return fail_arg("workspace too small (see cfa_tree_attention_workspace_size)");
     const size_t prows = (size_t)a.splits * B * n_kv_heads * a.rows;
     a.part_o = (uint16_t *)workspace;
-    a.part_ml = (float2 *)((char *)workspace + align256(prows * kD * sizeof(uint16_t)));
+    a.part_ml = (float2 *)((char *)workspace + align256(prows * head_dim * sizeof(uint16_t)));
   }
   hipStream_t st = (hipStream_t)stream;
-  CFA_LAUNCH("tree_attn", tree_attn_kernel, dim3(a.splits, n_kv_heads, B), dim3(kNT), 0, st, a);
-  if (a.splits > 1) {
-    const long long rows = (long long)B * n_kv_heads * a.rows;
-    CFA_LAUNCH("tree_attn_merge", tree_merge_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256),
-               0, st, a);
+  const dim3 grid(a.splits, n_kv_heads, B);
+  const long long rows = (long long)B * n_kv_heads * a.rows;
+  if (head_dim == 128) {
+    CFA_LAUNCH("tree_attn", tree_attn_kernel<128>, grid, dim3(kNT), 0, st, a);
+    if (a.splits > 1)
+      CFA_LAUNCH("tree_attn_merge", tree_merge_kernel<128>, dim3((unsigned)((rows + 15) / 16)),
+                 dim3(256), 0, st, a);
+  } else {
+    CFA_LAUNCH("tree_attn", tree_attn_kernel<64>, grid, dim3(kNT), 0, st, a);
+    if (a.splits > 1)
+      CFA_LAUNCH("tree_attn_merge", tree_merge_kernel<64>, dim3((unsigned)((rows + 31) / 32)),
+                 dim3(256), 0, st, a);
   }
   return CFA_OK;
 }

@@ -167,21 +167,26 @@ def tree_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                    tree_mask: torch.Tensor, *, layer: int = 0,
                    sm_scale: Optional[float] = None, max_keys: Optional[int] = None,
                    num_splits: int = 0, out: Optional[torch.Tensor] = None,
-                   workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Tree-masked attention of N draft-tree nodes over a paged KV cache.
+                   workspace: Optional[torch.Tensor] = None, first_node: int = 0) -> torch.Tensor:
+    """Tree-masked attention of draft-tree nodes over a paged KV cache.
 
-    q [B, N, Hq, D] bf16; k_pool / v_pool [num_blocks, num_layers, Hkv, block_size, D]
-    bf16 (the reference's per-block layout); block_tables [B, max_blocks] int32;
+    q [B, Nq, Hq, D] bf16 (D = 128 or 64): the queries of tree nodes
+    first_node .. first_node + Nq - 1 of an N = first_node + Nq node tree;
+    k_pool / v_pool [num_blocks, num_layers, Hkv, block_size, D] bf16 (the
+    reference's per-block layout); block_tables [B, max_blocks] int32;
     ctx_lens [B] int32 (tokens before the tree; the tree's K/V sit at
-    ctx_len + i); tree_mask int64 [N] or [B, N] holding each node's 64-bit
-    ancestor-or-self mask.  max_keys bounds ctx_len + N on the host (computed
-    with one sync when omitted).  Returns [B, N, Hq, D] bf16.
+    ctx_len + i, i < N); tree_mask int64 [N] or [B, N] holding each node's
+    64-bit ancestor-or-self mask.  max_keys bounds ctx_len + N on the host
+    (computed with one sync when omitted).  Returns [B, Nq, Hq, D] bf16.
     """
     _require_cuda("q", q, torch.bfloat16)
     dev = q.device
     if q.dim() != 4:
-        raise ValueError("q must be [B, N, Hq, D]")
-    B, N, Hq, D = q.shape
+        raise ValueError("q must be [B, Nq, Hq, D]")
+    B, Nq, Hq, D = q.shape
+    if first_node < 0:
+        raise ValueError("first_node must be >= 0")
+    N = first_node + Nq
     q = q.contiguous()
     for name, pool in (("k_pool", k_pool), ("v_pool", v_pool)):
         _require_cuda(name, pool, torch.bfloat16, dev)
@@ -215,14 +220,14 @@ def tree_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     if out is None:
         out = torch.empty_like(q)
     lib = _lib.load()
-    need = int(lib.cfa_tree_attention_workspace_size(B, N, Hq, Hkv, D, max_keys, num_splits))
+    need = int(lib.cfa_tree_attention_workspace_size(B, Nq, Hq, Hkv, D, max_keys, num_splits))
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         rc = lib.cfa_tree_attention(
             q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
             block_tables.shape[1], ctx_lens.data_ptr(), nblk, nlayers, int(layer), bs,
-            tree_mask.data_ptr(), mstride, B, N, Hq, Hkv, D, ctypes.c_float(sm_scale),
+            tree_mask.data_ptr(), mstride, B, N, int(first_node), Hq, Hkv, D, ctypes.c_float(sm_scale),
             int(max_keys), int(num_splits), out.data_ptr(), workspace.data_ptr(),
             workspace.numel(), _stream_ptr(dev))
     _lib.check(rc, "cfa_tree_attention")

@@ -147,17 +147,22 @@ int cfa_sample(const float *rows, int64_t row_stride, int input_kind, int R, int
  * and value pools) and its pool layout (paged_kv_cache.cpp:13-21, 409-421):
  *   pool[block][layer][kv_head][slot][head_dim]  bf16
  *
- *   q        [B, N, n_q_heads, 128] bf16 -- queries of the N draft-tree nodes
+ *   head_dim   128 or 64
+ *   q          [B, N - first_node, n_q_heads, head_dim] bf16 -- queries of the
+ *              tree nodes first_node .. N - 1 (first_node = 0: every node, as
+ *              a verify step needs; a drafter growing its tree level by level
+ *              passes the newest level)
  *   block_tables [B, max_blocks_per_seq] int32, ctx_lens [B] int32
  *   the tree's own K/V sit at positions ctx_len .. ctx_len + N - 1
  *   tree_mask  uint64 per node (bit j: node j is an ancestor of, or is, the
  *              node), [N] shared (stride 0) or [B, N] (stride N)
  *   max_keys   host-side bound on ctx_len + N over the batch (plans the splits)
  *   num_splits key-range splits (0: automatic); splits > 1 need workspace
- *   out        [B, N, n_q_heads, 128] bf16
+ *   out        [B, N - first_node, n_q_heads, head_dim] bf16
  * Query (node i, head hq) attends to context positions [0, ctx_len) and to
  * tree positions ctx_len + j with bit j of tree_mask[i]; scores scale by
- * sm_scale; fp32 softmax and accumulation.
+ * sm_scale; fp32 softmax and accumulation.  The workspace size takes N as the
+ * number of query nodes (N - first_node; the full N is an upper bound).
  */
 size_t cfa_tree_attention_workspace_size(int B, int N, int n_q_heads, int n_kv_heads,
                                          int head_dim, int max_keys, int num_splits);
@@ -166,8 +171,8 @@ int cfa_tree_attention(const void *q, const void *k_pool, const void *v_pool,
                        const int32_t *block_tables, int max_blocks_per_seq,
                        const int32_t *ctx_lens, int num_blocks, int num_layers, int layer,
                        int block_size, const uint64_t *tree_mask, int64_t tree_mask_stride_b,
-                       int B, int N, int n_q_heads, int n_kv_heads, int head_dim,
-                       float sm_scale, int max_keys, int num_splits, void *out,
+                       int B, int N, int first_node, int n_q_heads, int n_kv_heads,
+                       int head_dim, float sm_scale, int max_keys, int num_splits, void *out,
                        void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
