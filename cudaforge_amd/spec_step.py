@@ -19,13 +19,12 @@ kernels:
                     format, ``int4_gemm_dequant.cu:20-31``) feeding
                     PyTorch-ROCm GEMMs;
 * fused layers      ``cfa_rmsnorm`` (with the residual add),
-                    ``cfa_rope_kv_paged`` / ``_strided`` (rotary embedding
-                    plus the KV-cache write), ``cfa_silu_mul``; the draft's
-                    own attention runs in PyTorch.
+                    ``cfa_rope_kv_paged`` (rotary embedding plus the KV-cache
+                    write), ``cfa_silu_mul``.
 
-The draft keeps a contiguous KV cache (``[layers, B, Hkv, head_dim, slots]``
-for K, so the score product reads a contiguous operand) because its head size
-(64) is not the tree-attention kernel's.
+The draft keeps its own paged pools (head_dim 64, each sequence's pages
+contiguous) and attends with the same tree-attention kernel, one tree level
+at a time (``first_node``); its accepted nodes move with ``cfa_kv_commit``.
 """
 from __future__ import annotations
 
@@ -41,7 +40,8 @@ from . import _lib
 from . import tree as T
 from .kv_cache import KVCacheConfig, PagedKVCache
 from .sampling import expand_tree_level
-from .verify import _stream_ptr, tree_attention, tree_attention_workspace_bytes, tree_verify
+from .verify import (_stream_ptr, kv_commit, tree_attention, tree_attention_workspace_bytes,
+                     tree_verify)
 from .w4a16 import W4A16Linear
 
 __all__ = ["LlamaShape", "TARGET_8B", "DRAFT_1B", "TargetModel", "DraftModel", "TreeSpeculator",
@@ -90,18 +90,25 @@ def silu_mul(gu: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def rope_kv_pools(qkv: torch.Tensor, pos: torch.Tensor, B: int, n: int, s: "LlamaShape",
+                  q_out: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, layer: int,
+                  block_tables: torch.Tensor, base: torch.Tensor) -> None:
+    """Rotary embedding of q and k from qkv [B*n, (Hq+2Hkv)*D]; q -> q_out,
+    k and v -> slots base + j of `layer` in the paged pools
+    [blocks, layers, Hkv, block_size, D]."""
+    rc = _lib.load().cfa_rope_kv_paged(
+        qkv.data_ptr(), pos.data_ptr(), B, n, s.n_heads, s.n_kv_heads, s.head_dim,
+        float(s.rope_theta), q_out.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+        layer, k_pool.shape[1], k_pool.shape[3], block_tables.data_ptr(), block_tables.shape[1],
+        base.data_ptr(), _stream_ptr(qkv.device))
+    _lib.check(rc, "cfa_rope_kv_paged")
+
+
 def rope_kv_paged(qkv: torch.Tensor, pos: torch.Tensor, B: int, n: int, s: "LlamaShape",
                   q_out: torch.Tensor, kv: PagedKVCache, layer: int, block_tables: torch.Tensor,
                   base: torch.Tensor) -> None:
-    """Rotary embedding of q and k from qkv [B*n, (Hq+2Hkv)*D]; q -> q_out,
-    k and v -> slots base + j of `layer` in the paged pools."""
-    cfg = kv.get_config()
-    rc = _lib.load().cfa_rope_kv_paged(
-        qkv.data_ptr(), pos.data_ptr(), B, n, s.n_heads, s.n_kv_heads, s.head_dim,
-        float(s.rope_theta), q_out.data_ptr(), kv.key_pool.data_ptr(), kv.value_pool.data_ptr(),
-        layer, cfg.num_layers, cfg.block_size, block_tables.data_ptr(), block_tables.shape[1],
-        base.data_ptr(), _stream_ptr(qkv.device))
-    _lib.check(rc, "cfa_rope_kv_paged")
+    """rope_kv_pools into a PagedKVCache's pools."""
+    rope_kv_pools(qkv, pos, B, n, s, q_out, kv.key_pool, kv.value_pool, layer, block_tables, base)
 
 
 def rope_kv_strided(qkv: torch.Tensor, pos: torch.Tensor, B: int, n: int, s: "LlamaShape",
@@ -183,10 +190,18 @@ class TargetModel:
 
 
 # ---------------------------------------------------------------------------
-# draft: bf16 Llama shape, contiguous KV cache, attention in PyTorch
+# draft: bf16 Llama shape, its own paged pools, the tree-attention kernel
 # ---------------------------------------------------------------------------
 
 class DraftModel:
+    """A bf16 Llama-shape drafter.  Its KV cache is a pair of paged pools
+    [B * pages, layers, Hkv, 16, head_dim] whose block table gives sequence b
+    the pages b * pages .. (b + 1) * pages - 1, so a tree level attends
+    through ``cfa_tree_attention`` (queries: the level's nodes) and accepted
+    nodes move with ``cfa_kv_commit``, exactly as in the target's cache."""
+
+    block_size = 16
+
     def __init__(self, shape: LlamaShape, device, B: int, max_slots: int, seed: int = 1):
         s = self.shape = shape
         g = torch.Generator(device=device).manual_seed(seed)
@@ -204,57 +219,61 @@ class DraftModel:
                 wdown=_randn((s.ffn, d), g, device, 1.0 / math.sqrt(s.ffn))))
         self.norm = torch.ones(d, dtype=torch.bfloat16, device=device)
         self.lm_head = self.embed.t().contiguous()              # tied embeddings
-        self.kT = torch.zeros(s.n_layers, B, s.n_kv_heads, hd, max_slots, dtype=torch.bfloat16,
-                              device=device)
-        self.v = torch.zeros(s.n_layers, B, s.n_kv_heads, max_slots, hd, dtype=torch.bfloat16,
-                             device=device)
-        self.max_slots = max_slots
+        bs = self.block_size
+        pages = (max_slots + bs - 1) // bs
+        self.B, self.pages = B, pages
+        self.max_slots = pages * bs
+        self.k_pool = torch.zeros(B * pages, s.n_layers, s.n_kv_heads, bs, hd,
+                                  dtype=torch.bfloat16, device=device)
+        self.v_pool = torch.zeros_like(self.k_pool)
+        self.block_tables = torch.arange(B * pages, dtype=torch.int32,
+                                         device=device).view(B, pages).contiguous()
+        # one workspace for every level, sized for the most query rows a call
+        # takes: captured graphs keep using it
+        max_q = min(64, 256 // (s.n_heads // s.n_kv_heads))
+        need = tree_attention_workspace_bytes(B, max_q, s.n_heads, s.n_kv_heads, hd, self.max_slots)
+        self.attn_ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
 
-    def forward_nodes(self, tokens: torch.Tensor, positions: torch.Tensor, slots: torch.Tensor,
-                      visible: torch.Tensor) -> torch.Tensor:
-        """tokens / positions / slots [B, n]; visible [B, n, max_slots] bool
-        (every cache slot, so both products read whole contiguous caches);
-        returns fp32 logits [B, n, V]."""
+    def forward_level(self, tokens: torch.Tensor, positions: torch.Tensor, base: torch.Tensor,
+                      lo: int, masks: torch.Tensor) -> torch.Tensor:
+        """Tree nodes lo .. lo + n - 1 (tokens / positions [B, n]; their K/V go
+        to slots base + node) attend to the context [0, base) and to their
+        ancestors among nodes 0 .. lo + n - 1 (masks: the tree's ancestor
+        masks, int64 [N]).  Returns fp32 logits [B, n, V]."""
         s = self.shape
         B, n = tokens.shape
         hd, Hq, Hkv = s.head_dim, s.n_heads, s.n_kv_heads
-        G = Hq // Hkv
-        bias = torch.zeros(visible.shape, dtype=torch.float32, device=tokens.device)
-        bias.masked_fill_(~visible, float("-inf"))
+        dev = tokens.device
+        hi = lo + n
         pos = positions.reshape(-1).to(torch.int32).contiguous()
-        sl = slots.reshape(-1).to(torch.int32).contiguous()
-        S = self.max_slots
+        base_i = base.to(torch.int32).contiguous()
+        slot0 = (base_i + lo).contiguous()                      # slot of node lo
+        lvl_masks = masks[:hi].contiguous()
         h = self.embed[tokens.reshape(-1).long()]
         x = torch.empty_like(h)
-        q = torch.empty(B * n, Hq, hd, dtype=torch.bfloat16, device=tokens.device)
+        q = torch.empty(B, n, Hq, hd, dtype=torch.bfloat16, device=dev)
         delta = None
         for li, L in enumerate(self.layers):
             rmsnorm_(h, delta, L["attn_norm"], s.eps, x)
             qkv = x @ L["wqkv"]
-            rope_kv_strided(qkv, pos, B, n, s, q, self.kT[li], self.v[li], sl)
-            # scores [B, Hkv, G*n, S]: q grouped by KV head, K^T contiguous
-            qg = q.view(B, n, Hkv, G, hd).permute(0, 2, 3, 1, 4).reshape(B, Hkv, G * n, hd)
-            sc = torch.matmul(qg, self.kT[li]).float()
-            sc = sc.view(B, Hkv, G, n, S) * (1.0 / math.sqrt(hd)) + bias[:, None, None]
-            p = torch.softmax(sc, dim=-1).to(torch.bfloat16).view(B, Hkv, G * n, S)
-            o = torch.matmul(p, self.v[li])                       # [B, Hkv, G*n, hd]
-            o = o.view(B, Hkv, G, n, hd).permute(0, 3, 1, 2, 4).reshape(B * n, Hq * hd)
-            delta = o @ L["wo"]
+            rope_kv_pools(qkv, pos, B, n, s, q, self.k_pool, self.v_pool, li, self.block_tables,
+                          slot0)
+            # max_keys is the cache capacity: a bound that stays valid when
+            # this call is replayed from a graph at later context lengths
+            o = tree_attention(q, self.k_pool, self.v_pool, self.block_tables, base_i, lvl_masks,
+                               layer=li, max_keys=self.max_slots, workspace=self.attn_ws,
+                               first_node=lo)
+            delta = o.view(B * n, Hq * hd) @ L["wo"]
             rmsnorm_(h, delta, L["ffn_norm"], s.eps, x)
             delta = silu_mul(x @ L["wgu"]) @ L["wdown"]
         rmsnorm_(h, delta, self.norm, s.eps, x)
         return (x @ self.lm_head).float().view(B, n, s.vocab)
 
-    def commit(self, base: torch.Tensor, paths: torch.Tensor, path_lens: List[int]) -> None:
-        """Move the accepted nodes (slot base + node) to base + j, as
-        cfa_kv_commit does for the paged target cache."""
-        for b, L in enumerate(path_lens):
-            if L <= 1:
-                continue
-            src = base[b] + paths[b, :L].long()
-            dst = base[b] + torch.arange(L, device=base.device)
-            self.kT[:, b, :, :, dst] = self.kT[:, b, :, :, src].clone()
-            self.v[:, b, :, dst, :] = self.v[:, b, :, src, :].clone()
+    def commit(self, base: torch.Tensor, paths: torch.Tensor, path_lens: torch.Tensor) -> None:
+        """Move the accepted nodes (slot base + node) to base + j in every
+        layer (cfa_kv_commit, on the device)."""
+        kv_commit(self.k_pool, self.v_pool, self.block_tables, base.to(torch.int32), paths,
+                  path_lens)
 
 
 # ---------------------------------------------------------------------------
@@ -307,8 +326,8 @@ class TreeSpeculator:
             self.kv.register_sequence_with_prefix(b, rng.integers(0, s.vocab, context).tolist())
         self.kv.key_pool.normal_(generator=self.gen)
         self.kv.value_pool.normal_(generator=self.gen)
-        draft.kT.normal_(generator=self.gen)
-        draft.v.normal_(generator=self.gen)
+        draft.k_pool.normal_(generator=self.gen)
+        draft.v_pool.normal_(generator=self.gen)
         self.ctx = [context] * B
         self.root = torch.randint(0, s.vocab, (B,), device=dev, generator=self.gen,
                                   dtype=torch.int32)
@@ -318,19 +337,9 @@ class TreeSpeculator:
     def _level_forward(self, lvl: int, base: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
         """Draft logits [B, n, V] of the nodes of level `lvl` (tokens toks
         [B, n]), each seeing the context and its ancestors' tree slots."""
-        B, dev = self.B, toks.device
         lo, hi = 2 ** lvl - 1, 2 ** (lvl + 1) - 1
-        n_keys = self.max_slots
-        key_ix = torch.arange(n_keys, device=dev)
-        nodes = torch.arange(lo, hi, device=dev)
-        slots = base[:, None] + nodes[None, :]
-        pos = base[:, None] + self.depths[nodes][None, :]
-        rel = key_ix[None, None, :] - base[:, None, None]         # [B, 1, keys]
-        in_tree = (rel >= 0) & (rel < self.N)
-        anc = self.anc[nodes][None, :, :].expand(B, -1, -1)       # [B, n, N]
-        tree_vis = torch.gather(anc, 2, rel.clamp(0, self.N - 1).expand(B, hi - lo, n_keys))
-        visible = (rel < 0) | (in_tree & tree_vis)
-        return self.d.forward_nodes(toks, pos, slots, visible)
+        pos = base[:, None] + self.depths[lo:hi][None, :]
+        return self.d.forward_level(toks, pos, base, lo, self.masks)
 
     def _level_graph(self, lvl: int, base: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
         """_level_forward replayed from a HIP graph captured on first use
@@ -404,7 +413,7 @@ class TreeSpeculator:
         mark()
         new_lens = self.kv.commit_tree_paths(list(range(B)), desc, base, res.path, res.path_len)
         plen = [n - c for n, c in zip(new_lens, self.ctx)]
-        self.d.commit(base, res.path, plen)
+        self.d.commit(base, res.path, res.path_len)
         toks = res.tokens.cpu().tolist()
         ne = res.num_emitted.cpu().tolist()
         final = res.final.cpu().tolist()

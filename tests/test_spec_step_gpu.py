@@ -78,6 +78,85 @@ def _ref_forward(tm: TargetModel, tokens, positions, kv, tables, base, N):
     return (h @ tm.lm_head.float()).view(B, N, s.vocab)
 
 
+def _rms(x, w, eps):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+
+
+def _rope(x, pos, theta):
+    D = x.shape[-1]
+    inv = theta ** (-torch.arange(0, D, 2, device=x.device, dtype=torch.float32) / D)
+    ang = pos.float()[..., None] * inv
+    cos = torch.cat([ang.cos(), ang.cos()], -1)[..., None, :]
+    sin = torch.cat([ang.sin(), ang.sin()], -1)[..., None, :]
+    rot = torch.cat([-x[..., D // 2:], x[..., : D // 2]], -1)
+    return x * cos + rot * sin
+
+
+def _ref_draft_level(dm: DraftModel, tokens, positions, base, lo, N):
+    """fp32 reference of DraftModel.forward_level for tree nodes lo..lo+n-1 of
+    an N-node binary tree, given the pool contents before the call (context
+    and nodes < lo from the pools, this level's K/V from this forward)."""
+    s = dm.shape
+    B, n = tokens.shape
+    hi = lo + n
+    hd, Hq, Hkv = s.head_dim, s.n_heads, s.n_kv_heads
+    G = Hq // Hkv
+    anc = T.ancestor_masks(T.binary_tree_parents(N))
+    allow = torch.tensor([[bool((int(anc[i]) >> j) & 1) for j in range(hi)] for i in range(lo, hi)],
+                         device=tokens.device)
+    bs = dm.block_size
+    h = dm.embed[tokens.reshape(-1).long()].float()
+    for li, L in enumerate(dm.layers):
+        x = _rms(h, L["attn_norm"], s.eps)
+        qkv = (x @ L["wqkv"].float()).view(B, n, Hq + 2 * Hkv, hd)
+        q = _rope(qkv[:, :, :Hq], positions, s.rope_theta)
+        k = _rope(qkv[:, :, Hq:Hq + Hkv], positions, s.rope_theta)
+        v = qkv[:, :, Hq + Hkv:]
+        o = torch.empty(B, n, Hq, hd, device=tokens.device)
+        for b in range(B):
+            ctx = int(base[b])
+            old = torch.arange(ctx + lo, device=tokens.device)
+            blk = dm.block_tables[b].long()[old // bs]
+            kc = dm.k_pool[blk, li][torch.arange(ctx + lo), :, old % bs].float()
+            vc = dm.v_pool[blk, li][torch.arange(ctx + lo), :, old % bs].float()
+            kk = torch.cat([kc, k[b]], 0)
+            vv = torch.cat([vc, v[b]], 0)
+            mask = torch.ones(n, ctx + hi, dtype=torch.bool, device=tokens.device)
+            mask[:, ctx:] = allow
+            for hh in range(Hq):
+                sc = (q[b, :, hh] @ kk[:, hh // G].T) / math.sqrt(hd)
+                sc = sc.masked_fill(~mask, float("-inf"))
+                o[b, :, hh] = torch.softmax(sc, -1) @ vv[:, hh // G]
+        h = h + o.reshape(B * n, Hq * hd) @ L["wo"].float()
+        x = _rms(h, L["ffn_norm"], s.eps)
+        gu = x @ L["wgu"].float()
+        h = h + (torch.nn.functional.silu(gu[:, : s.ffn]) * gu[:, s.ffn:]) @ L["wdown"].float()
+    h = _rms(h, dm.norm, s.eps)
+    return (h @ dm.lm_head.float()).view(B, n, s.vocab)
+
+
+def test_draft_levels_vs_fp32(device):
+    """The drafter's level forwards (paged pools, tree-attention kernel at
+    head_dim 64 on the level's nodes) against an fp32 forward over gathered
+    pages, level by level as propose() runs them."""
+    B, ctx0, depth = 3, 40, 3
+    N = 2 ** (depth + 1) - 1
+    tm = TargetModel(SMALL_T, device, seed=9)
+    dm = DraftModel(SMALL_D, device, B, max_slots=ctx0 + 64 + 64)
+    sp = TreeSpeculator(tm, dm, B, ctx0, depth=depth, max_steps=8, seed=10)
+    base = torch.tensor([40, 23, 57], dtype=torch.int32, device=device)
+    for lvl in range(depth):
+        lo, hi = 2 ** lvl - 1, 2 ** (lvl + 1) - 1
+        toks = torch.randint(0, SMALL_D.vocab, (B, hi - lo), device=device, dtype=torch.int32)
+        pos = base[:, None] + sp.depths[lo:hi][None, :]
+        want = _ref_draft_level(dm, toks, pos, base, lo, N)
+        got = sp._level_forward(lvl, base, toks)
+        torch.cuda.synchronize()
+        err = (got - want).abs().max().item()
+        scale = want.abs().max().item()
+        assert err <= 3e-2 * max(1.0, scale), (lvl, err, scale)
+
+
 def test_target_tree_forward_vs_fp32(device):
     B, ctx0, N = 3, 50, 15
     tm = TargetModel(SMALL_T, device, seed=3)
@@ -133,12 +212,12 @@ def test_draft_level_graphs_match_eager(device):
         for lvl in range(3):
             n = 2 ** lvl
             toks = torch.randint(0, SMALL_D.vocab, (B, n), device=device, dtype=torch.int32)
-            kT0, v0 = dm.kT.clone(), dm.v.clone()
+            k0, v0 = dm.k_pool.clone(), dm.v_pool.clone()
             eager = sp._level_forward(lvl, base, toks).clone()
-            kT1, v1 = dm.kT.clone(), dm.v.clone()
-            dm.kT.copy_(kT0)
-            dm.v.copy_(v0)
+            k1, v1 = dm.k_pool.clone(), dm.v_pool.clone()
+            dm.k_pool.copy_(k0)
+            dm.v_pool.copy_(v0)
             graph = sp._level_graph(lvl, base, toks).clone()
             torch.cuda.synchronize()
             assert torch.equal(graph, eager), (rep, lvl, (graph - eager).abs().max().item())
-            assert torch.equal(dm.kT, kT1) and torch.equal(dm.v, v1)
+            assert torch.equal(dm.k_pool, k1) and torch.equal(dm.v_pool, v1)
