@@ -63,6 +63,20 @@ def test_argument_errors_map_to_valueerror():
     assert "positive" in _lib.last_error()
 
 
+@pytest.mark.parametrize("first_node,head_dim,msg", [(15, 128, "first_node"), (-1, 128, "first_node"),
+                                                   (0, 96, "head_dim")])
+def test_tree_attention_argument_errors(first_node, head_dim, msg):
+    """Shape checks run before anything touches a device (dummy pointers)."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    rc = lib.cfa_tree_attention(p, p, p, p, 4, p, 8, 1, 0, 16, p, 0, 2, 15, first_node, 8, 2,
+                                head_dim, ctypes.c_float(0.1), 64, 0, p, p, 1 << 20, None)
+    assert rc == _lib.CFA_ERR_ARG
+    assert msg in _lib.last_error()
+    ws = lib.cfa_tree_attention_workspace_size(2, 15, 8, 2, head_dim, 64, 0)
+    assert (ws == 0) == (head_dim == 96)
+
+
 def test_host_validation_rejects_cpu_tensors():
     from cudaforge_amd.verify import chain_verify
 
