@@ -509,7 +509,10 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
     if (lag) block_barrier();
     Scores S;
     Probs P;
-    qk_tile(ln, kring, sm.b, S);
+    // a wave without query rows (few query nodes) only moves data and keeps
+    // the barriers; its products would be discarded
+    const bool busy = wave * kQT * 16 < a.rows;  // wave-uniform
+    if (busy) qk_tile(ln, kring, sm.b, S);
     for (int t = t0; t < t1; ++t) {
       const int kbase = t * kKT;
       if (!lag) {
@@ -529,7 +532,7 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
                      vring + (u % kVStages) * kTileBytes, wave, lane);
         }
       }
-      valu_phase(ln, kbase, ctx, S, sm, o, lacc, P);
+      if (busy) valu_phase(ln, kbase, ctx, S, sm, o, lacc, P);
       if (!lag) {
         if (t + 3 < t1) wait_vmcnt<2 * kLoadsPerTile>();
         else if (t + 2 < t1) wait_vmcnt<kLoadsPerTile>();
@@ -538,7 +541,8 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
       } else {
         block_barrier();
       }
-      mfma_phase(ln, kring + ((t + 1 - t0) % kKStages) * kTileBytes,
+      if (busy)
+        mfma_phase(ln, kring + ((t + 1 - t0) % kKStages) * kTileBytes,
                  vring + ((t - t0) % kVStages) * kTileBytes, sm.b, P, S, o, lacc);
     }
     if (!lag) block_barrier();
