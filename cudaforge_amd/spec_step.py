@@ -20,7 +20,9 @@ kernels:
                     PyTorch-ROCm GEMMs;
 * fused layers      ``cfa_rmsnorm`` (with the residual add),
                     ``cfa_rope_kv_paged`` (rotary embedding plus the KV-cache
-                    write), ``cfa_silu_mul``.
+                    write), ``cfa_silu_mul``;
+* draft projections ``cfa_gemm_bf16_skinny`` (few-row split-K GEMM that
+                    streams the weights once) for levels of <= 128 rows.
 
 The draft keeps its own paged pools (head_dim 64, each sequence's pages
 contiguous) and attends with the same tree-attention kernel, one tree level
@@ -87,6 +89,34 @@ def silu_mul(gu: torch.Tensor) -> torch.Tensor:
     out = torch.empty(M, F2 // 2, dtype=gu.dtype, device=gu.device)
     rc = _lib.load().cfa_silu_mul(gu.data_ptr(), out.data_ptr(), M, F2 // 2, _stream_ptr(gu.device))
     _lib.check(rc, "cfa_silu_mul")
+    return out
+
+
+def skinny_gemm_workspace_bytes(M: int, N: int, K: int, splits: int = 0) -> int:
+    """Bytes of workspace cfa_gemm_bf16_skinny needs (0: none)."""
+    return int(_lib.load().cfa_gemm_bf16_skinny_workspace_size(M, N, K, splits))
+
+
+def skinny_gemm(a: torch.Tensor, w: torch.Tensor, workspace: Optional[torch.Tensor] = None, *,
+                splits: int = 0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """a [M, K] @ w [K, N] in bf16 for M <= 128 (cfa_gemm_bf16_skinny).
+    `workspace` must have been zeroed before its first use and is left
+    reusable; calls sharing it must not overlap."""
+    M, K = a.shape
+    N = w.shape[1]
+    if w.shape[0] != K:
+        raise ValueError("inner dimensions differ")
+    if a.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError("a and w must be bfloat16")
+    if not (a.is_contiguous() and w.is_contiguous()):
+        raise ValueError("a and w must be contiguous (row-major)")
+    if out is None:
+        out = torch.empty(M, N, dtype=a.dtype, device=a.device)
+    ws_ptr, ws_n = (workspace.data_ptr(), workspace.numel() * workspace.element_size()) \
+        if workspace is not None else (None, 0)
+    rc = _lib.load().cfa_gemm_bf16_skinny(a.data_ptr(), w.data_ptr(), out.data_ptr(), M, N, K,
+                                          splits, ws_ptr, ws_n, _stream_ptr(a.device))
+    _lib.check(rc, "cfa_gemm_bf16_skinny")
     return out
 
 
@@ -233,6 +263,16 @@ class DraftModel:
         max_q = min(64, 256 // (s.n_heads // s.n_kv_heads))
         need = tree_attention_workspace_bytes(B, max_q, s.n_heads, s.n_kv_heads, hd, self.max_slots)
         self.attn_ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+        # the projections of levels with B * n <= 128 rows run on
+        # cfa_gemm_bf16_skinny; one zeroed workspace serves all of them
+        gemm_need = max(skinny_gemm_workspace_bytes(128, w.shape[1], w.shape[0])
+                        for w in self.layers[0].values() if w.dim() == 2)
+        self.gemm_ws = torch.zeros(max(gemm_need, 65536), dtype=torch.uint8, device=device)
+
+    def _mm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        if x.shape[0] <= 128:
+            return skinny_gemm(x, w, self.gemm_ws)
+        return x @ w
 
     def forward_level(self, tokens: torch.Tensor, positions: torch.Tensor, base: torch.Tensor,
                       lo: int, masks: torch.Tensor) -> torch.Tensor:
@@ -255,7 +295,7 @@ class DraftModel:
         delta = None
         for li, L in enumerate(self.layers):
             rmsnorm_(h, delta, L["attn_norm"], s.eps, x)
-            qkv = x @ L["wqkv"]
+            qkv = self._mm(x, L["wqkv"])
             rope_kv_pools(qkv, pos, B, n, s, q, self.k_pool, self.v_pool, li, self.block_tables,
                           slot0)
             # max_keys is the cache capacity: a bound that stays valid when
@@ -263,9 +303,9 @@ class DraftModel:
             o = tree_attention(q, self.k_pool, self.v_pool, self.block_tables, base_i, lvl_masks,
                                layer=li, max_keys=self.max_slots, workspace=self.attn_ws,
                                first_node=lo)
-            delta = o.view(B * n, Hq * hd) @ L["wo"]
+            delta = self._mm(o.view(B * n, Hq * hd), L["wo"])
             rmsnorm_(h, delta, L["ffn_norm"], s.eps, x)
-            delta = silu_mul(x @ L["wgu"]) @ L["wdown"]
+            delta = self._mm(silu_mul(self._mm(x, L["wgu"])), L["wdown"])
         rmsnorm_(h, delta, self.norm, s.eps, x)
         return (x @ self.lm_head).float().view(B, n, s.vocab)
 

@@ -286,6 +286,20 @@ int cfa_rope_kv_strided(const void *qkv, const int32_t *positions, int B, int n,
                         void *stream);
 int cfa_silu_mul(const void *gu, void *out, int M, int F, void *stream);
 
+/* Few-row bf16 GEMM: c [M, N] = a [M, K] x w [K, N], all row-major bf16, fp32
+ * accumulation on MFMA, 1 <= M <= 128, N % 64 == 0, K % 128 == 0, pointers
+ * 16-byte aligned.  Streams w once, split over `splits` equal k ranges
+ * (0: the library's choice; otherwise a divisor of K / 128).  With more
+ * than one split it needs `workspace` (cfa_gemm_bf16_skinny_workspace_size
+ * bytes, 256-byte aligned) whose first 64 KiB are ZERO before its first
+ * use: they hold per-tile arrival counters (N / 64 <= 16384) that every call
+ * leaves at zero, so calls of any shape may share one workspace but must not
+ * overlap.  Sums run in a fixed order (bitwise
+ * reproducible).  Takes the place of the draft model's PyTorch GEMMs. */
+size_t cfa_gemm_bf16_skinny_workspace_size(int M, int N, int K, int splits);
+int cfa_gemm_bf16_skinny(const void *a, const void *w, void *c, int M, int N, int K, int splits,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Paged KV cache page tables (host metadata).
  *

@@ -110,3 +110,32 @@ def test_compat_config_defaults_and_no_reseed():
     seeds, draws = H.mt_stream()
     idx = list(seeds).index(42)
     np.testing.assert_array_equal(eng._peek(8), draws[idx][:8])  # still seeded with 42
+
+
+@pytest.mark.parametrize("M,N,K,splits,msg", [
+    (0, 64, 128, 1, "M must be"),
+    (129, 64, 128, 1, "M must be"),
+    (8, 100, 128, 1, "N must be"),
+    (8, 64, 100, 1, "K must be"),
+    (8, 64, 512, 3, "splits must divide"),
+    (8, 64, 512, 8, "splits must divide"),
+    (8, 64, 512, 2, "workspace smaller"),
+])
+def test_skinny_gemm_argument_errors(M, N, K, splits, msg):
+    """Shape, split and workspace checks run before anything touches a device
+    (dummy pointers)."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    rc = lib.cfa_gemm_bf16_skinny(p, p, p, M, N, K, splits, p, 16, None)
+    assert rc == _lib.CFA_ERR_ARG
+    assert msg in _lib.last_error()
+
+
+def test_skinny_gemm_workspace_size():
+    lib = _lib.load()
+    # one split needs none; S splits need the 64 KiB counter region plus S
+    # fp32 partial tiles of 16 * m_tiles rows x 64 columns per column tile
+    assert lib.cfa_gemm_bf16_skinny_workspace_size(8, 3072, 2048, 1) == 0
+    assert lib.cfa_gemm_bf16_skinny_workspace_size(8, 3072, 2048, 4) == 65536 + 48 * 4 * 4096
+    assert lib.cfa_gemm_bf16_skinny_workspace_size(100, 2048, 8192, 8) == 65536 + 32 * 8 * 32 * 1024
+    assert lib.cfa_gemm_bf16_skinny_workspace_size(129, 64, 128, 1) == 0
