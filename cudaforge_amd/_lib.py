@@ -126,6 +126,7 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _p, _p, _i, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p],
     ),
     "cfa_w4a16_dequant": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _p]),
+    "cfa_w4a16_dequant_t": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _p]),
     "cfa_w4a16_gemm": (_i, [_p, _p, _p, _i, _i, _i, _i, _i, _p, _p]),
     "cfa_rmsnorm": (_i, [_p, _p, _p, _p, _i, _i, _f, _p]),
     "cfa_rope_kv_paged": (

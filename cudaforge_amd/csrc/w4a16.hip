@@ -111,8 +111,136 @@ __global__ __launch_bounds__(256) void dequant4_kernel(Args a) {
   }
 }
 
+// Transposed output out [N, K] (K contiguous, the layout hipBLASLt
+// multiplies fastest as the second operand).  A work-group covers 64 packed
+// rows x CT columns (CT = 64 for large matrices, 16 where 64 would leave
+// fewer than 1024 work-groups).  Load phase: the words (16 bytes per thread when
+// VEC) go into an LDS block padded to CT + 1 words a row, with the
+// block's scale (and zero-point) rows when there are at most kDqtGroups of
+// them.  Store phase, LDS only: lane l of wave w takes packed row kb0 + l
+// of columns n0 + (CT/4) w .. n0 + (CT/4)(w + 1) - 1 (the odd row pitch keeps those column
+// reads free of bank conflicts), and each output store of the wave writes
+// 64 consecutive 16-byte chunks of one row of out (1 KiB contiguous).
+// Consecutive work-groups take consecutive k-blocks of the same rows of
+// out, so the writes in flight fill whole rows.
+constexpr int kDqtGroups = 8;
+
+template <int CT, bool VEC>
+__global__ __launch_bounds__(256) void dequant_t_kernel(Args a) {
+  constexpr int kDqtCols = CT, kDqtPitch = CT + 1;
+  __shared__ uint32_t blk[64 * kDqtPitch];
+  __shared__ __half sblk[kDqtGroups * kDqtCols], zblk[kDqtGroups * kDqtCols];  // [group - g0][column]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kb0 = blockIdx.x * 64, n0 = blockIdx.y * kDqtCols;
+  const int KB = a.K / 8;
+  const int g0 = (kb0 * 8) / a.group;
+  const int g1 = (min(kb0 + 64, KB) * 8 - 1) / a.group;  // last group of the block
+  if (VEC) {
+#pragma unroll
+    for (int j = 0; j < CT / 16; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / (CT / 4), c = 4 * (i % (CT / 4));
+      const int kb = kb0 + r, n = n0 + c;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (kb < KB && n < a.N) v = *reinterpret_cast<const uint4 *>(a.q + (long long)kb * a.N + n);
+      uint32_t *d = blk + r * kDqtPitch + c;
+      d[0] = v.x;
+      d[1] = v.y;
+      d[2] = v.z;
+      d[3] = v.w;
+    }
+  } else {
+    for (int i = tid; i < 64 * kDqtCols; i += 256) {
+      const int r = i / kDqtCols, c = i % kDqtCols;
+      const int kb = kb0 + r, n = n0 + c;
+      blk[r * kDqtPitch + c] = (kb < KB && n < a.N) ? a.q[(long long)kb * a.N + n] : 0u;
+    }
+  }
+  const bool staged = g1 - g0 < kDqtGroups;
+  for (int i = tid; staged && i < (g1 - g0 + 1) * kDqtCols; i += 256) {
+    const int gi = i / kDqtCols, n = n0 + i % kDqtCols;
+    const long long src = (long long)(g0 + gi) * a.N + n;
+    sblk[i] = n < a.N ? a.s[src] : __float2half(0.0f);
+    zblk[i] = (a.z && n < a.N) ? a.z[src] : __float2half(0.0f);
+  }
+  __syncthreads();
+  const int kb = kb0 + lane;
+  if (kb >= KB) return;
+  const int gi = (kb * 8) / a.group - g0;
+  uint16_t *o = reinterpret_cast<uint16_t *>(a.out);
+#pragma unroll
+  for (int c = 0; c < kDqtCols / 4; ++c) {
+    const int col = (kDqtCols / 4) * wave + c, n = n0 + col;
+    if (n >= a.N) break;
+    const uint32_t w = blk[lane * kDqtPitch + col];
+    __half sh, zh;
+    if (staged) {
+      sh = sblk[gi * kDqtCols + col];
+      zh = zblk[gi * kDqtCols + col];
+    } else {
+      sh = a.s[(long long)(g0 + gi) * a.N + n];
+      zh = a.z ? a.z[(long long)(g0 + gi) * a.N + n] : __float2half(0.0f);
+    }
+    uint16_t r[8];
+    if (a.bf16) {
+      const float sf = __half2float(sh), zf = __half2float(zh);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] = to_bf16_bits(((float)((w >> (4 * i)) & 15u) - zf) * sf);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const __half nib = __float2half((float)((w >> (4 * i)) & 15u));
+        r[i] = __half_as_ushort(__hmul(__hsub(nib, zh), sh));
+      }
+    }
+    uint4 v;
+    v.x = (uint32_t)r[0] | ((uint32_t)r[1] << 16);
+    v.y = (uint32_t)r[2] | ((uint32_t)r[3] << 16);
+    v.z = (uint32_t)r[4] | ((uint32_t)r[5] << 16);
+    v.w = (uint32_t)r[6] | ((uint32_t)r[7] << 16);
+    *reinterpret_cast<uint4 *>(o + (long long)n * a.K + (long long)kb * 8) = v;
+  }
+}
+
 }  // namespace w4
 }  // namespace cfa
+
+extern "C" int cfa_w4a16_dequant_t(const uint32_t *b_quant, const void *scales, const void *zeros,
+                                   int K, int N, int group_size, int out_bf16, void *out,
+                                   void *stream) {
+  using namespace cfa::abi;
+  clear_error();
+  if (K <= 0 || N <= 0 || group_size <= 0) return fail_arg("K, N and group_size must be positive");
+  if (K % 8 != 0) return fail_arg("K must be a multiple of 8");
+  if (group_size % 8 != 0 || K % group_size != 0)
+    return fail_arg("group_size must be a multiple of 8 that divides K");
+  if (!b_quant || !scales || !out) return fail_arg("null pointer");
+  if ((uintptr_t)out & 15) return fail_arg("out must be 16-byte aligned");
+  cfa::w4::Args a{};
+  a.q = b_quant;
+  a.s = (const __half *)scales;
+  a.z = (const __half *)zeros;
+  a.out = out;
+  a.K = K;
+  a.N = N;
+  a.group = group_size;
+  a.bf16 = out_bf16 ? 1 : 0;
+  const unsigned kblocks = (unsigned)((K / 8 + 63) / 64);
+  const bool wide = (long long)kblocks * ((N + 63) / 64) >= 1024;
+  const int ct = wide ? 64 : 16;
+  const dim3 grid(kblocks, (unsigned)((N + ct - 1) / ct));
+  const bool vec = N % 4 == 0 && ((uintptr_t)b_quant & 15) == 0;
+  hipStream_t st = (hipStream_t)stream;
+  if (wide && vec)
+    CFA_LAUNCH("w4a16_dequant_t", (cfa::w4::dequant_t_kernel<64, true>), grid, dim3(256), 0, st, a);
+  else if (wide)
+    CFA_LAUNCH("w4a16_dequant_t", (cfa::w4::dequant_t_kernel<64, false>), grid, dim3(256), 0, st, a);
+  else if (vec)
+    CFA_LAUNCH("w4a16_dequant_t", (cfa::w4::dequant_t_kernel<16, true>), grid, dim3(256), 0, st, a);
+  else
+    CFA_LAUNCH("w4a16_dequant_t", (cfa::w4::dequant_t_kernel<16, false>), grid, dim3(256), 0, st, a);
+  return CFA_OK;
+}
 
 extern "C" int cfa_w4a16_dequant(const uint32_t *b_quant, const void *scales, const void *zeros,
                                  int K, int N, int group_size, int out_bf16, void *out,

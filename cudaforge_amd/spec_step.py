@@ -15,9 +15,9 @@ kernels:
                     longest accepted path, bonus token);
 * KV commit         ``cfa_kv_commit`` plus the page-table rollback of
                     ``PagedKVCache.truncate_sequence``;
-* W4A16 weights     ``cfa_w4a16_dequant`` (the reference's packed INT4
-                    format, ``int4_gemm_dequant.cu:20-31``) feeding
-                    PyTorch-ROCm GEMMs;
+* W4A16 weights     ``cfa_w4a16_dequant_t`` (the reference's packed INT4
+                    format, ``int4_gemm_dequant.cu:20-31``, dequantised as
+                    [N, K]) feeding PyTorch-ROCm GEMMs;
 * fused layers      ``cfa_rmsnorm`` (with the residual add),
                     ``cfa_rope_kv_paged`` (rotary embedding plus the KV-cache
                     write), ``cfa_silu_mul``;

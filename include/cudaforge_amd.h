@@ -246,6 +246,11 @@ int cfa_kv_commit(void *k_pool, void *v_pool, const int32_t *block_tables,
  */
 int cfa_w4a16_dequant(const uint32_t *b_quant, const void *scales, const void *zeros, int K,
                       int N, int group_size, int out_bf16, void *out, void *stream);
+/* As cfa_w4a16_dequant with the transposed output out [N, K] (K contiguous,
+ * 16-byte aligned): the same values, in the layout the GEMM that follows
+ * (x @ out^T) runs fastest on. */
+int cfa_w4a16_dequant_t(const uint32_t *b_quant, const void *scales, const void *zeros, int K,
+                        int N, int group_size, int out_bf16, void *out, void *stream);
 
 /* Fused W4A16 GEMM: c [M, N] = a [M, K] x dequant(b_quant, scales) with the
  * dequantisation of cfa_w4a16_dequant (no zero points) done in registers and

@@ -1,4 +1,5 @@
-"""GPU tier: W4A16 dequantisation (cfa_w4a16_dequant) bit-exact against a
+"""GPU tier: W4A16 dequantisation (cfa_w4a16_dequant, and its transposed
+output cfa_w4a16_dequant_t) bit-exact against a
 numpy restatement of the reference formula (int4_gemm_dequant.cu:20-31,
 int4_dequant_triton.py:74-78), and the reference's own GEMM parity test
 (tests/unit/test_int4_dequant.py:18-53: atol = rtol = 1e-2 against an fp16
@@ -35,8 +36,11 @@ def _np_dequant(w_int4, scales, zeros, group, dtype):
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("with_zeros", [False, True])
 @pytest.mark.parametrize("K,N,group", [(128, 256, 128), (512, 96, 64), (1024, 48, 128),
-                                       (256, 50, 128)])
-def test_dequant_bit_exact(device, dtype, with_zeros, K, N, group):
+                                       (256, 50, 128), (136, 300, 8)])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_dequant_bit_exact(device, dtype, with_zeros, K, N, group, transposed):
+    """Both output layouts: [K, N] (cfa_w4a16_dequant) and [N, K]
+    (cfa_w4a16_dequant_t, 16 packed rows per thread: K = 136 leaves a tail)."""
     g = torch.Generator().manual_seed(K + N)
     w = torch.randint(0, 16, (K, N), generator=g, dtype=torch.int32)
     scales = (torch.rand(K // group, N, generator=g) * 0.1 + 1e-3).half()
@@ -44,11 +48,14 @@ def test_dequant_bit_exact(device, dtype, with_zeros, K, N, group):
     q = pack_int4_weights(w)
     out = w4a16_dequant(q.to(device), scales.to(device),
                         zeros.to(device) if zeros is not None else None, group_size=group,
-                        dtype=torch.float16 if dtype == "fp16" else torch.bfloat16)
+                        dtype=torch.float16 if dtype == "fp16" else torch.bfloat16,
+                        transposed=transposed)
     want = _np_dequant(w.numpy(), scales.numpy(), zeros.numpy() if zeros is not None else None,
                        group, dtype)
     got = out.cpu().view(torch.int16).numpy().view(np.uint16)
     exp = want.view(np.uint16)
+    if transposed:
+        exp = np.ascontiguousarray(exp.T)
     assert np.array_equal(got, exp)
 
 
@@ -110,3 +117,20 @@ def test_fused_gemm_rejects_bad_shapes(device):
     s = torch.ones(1, 100, dtype=torch.float16, device=device)
     with pytest.raises(ValueError):
         w4a16_gemm(a, q, s)
+
+
+@pytest.mark.parametrize("K,N,with_zeros", [(4096, 8192, False), (4096, 8190, True)])
+def test_dequant_t_wide_tiles_bit_exact(device, K, N, with_zeros):
+    """Shapes large enough for the 64-column tiles of cfa_w4a16_dequant_t (at
+    least 1024 work-groups), with aligned 16-byte word loads and, at N = 8190,
+    the one-word path; bit-exact against the [K, N] dequantisation."""
+    g = torch.Generator().manual_seed(N)
+    w = torch.randint(0, 16, (K, N), generator=g, dtype=torch.int32)
+    scales = (torch.rand(K // 128, N, generator=g) * 0.1 + 1e-3).half()
+    zeros = torch.randint(0, 16, (K // 128, N), generator=g).half() if with_zeros else None
+    q = pack_int4_weights(w).to(device)
+    sd = scales.to(device)
+    zd = zeros.to(device) if zeros is not None else None
+    kn = w4a16_dequant(q, sd, zd, group_size=128)
+    nk = w4a16_dequant(q, sd, zd, group_size=128, transposed=True)
+    assert torch.equal(nk.view(torch.int16), kn.t().contiguous().view(torch.int16))
