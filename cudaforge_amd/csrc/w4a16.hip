@@ -449,6 +449,177 @@ __global__ __launch_bounds__(256, 2) void w4gemm_kernel(GArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Fused W4A16 GEMM with cooperative dequantisation (bf16 activations), the
+// form for many rows (the verify step's M = 504).  Work-group tile 128 x BN
+// (BN = 128, or 64 where 128 would leave CUs idle), K in steps of 64, four
+// waves of 64 x BN/2.  Each step's A tile (128 rows x 64 k, 16-byte chunks
+// XOR-swizzled by row), packed words (8 rows x BN) and scale row move by
+// direct HBM -> LDS transfers into a 3-stage ring two steps ahead.  The 256
+// threads then dequantise the step's 64 x BN weights once, into an LDS tile
+// laid out [n][k] (one 16-byte write per packed word, chunks swizzled by
+// column), from which every wave reads its B operands with 16-byte reads.
+// Dequantisation is bf16(nibble * scale) formed in fp32, as
+// cfa_w4a16_dequant, so the result equals dequantise-then-GEMM up to the
+// order of the fp32 accumulation.  Two work-groups share a CU, so one's
+// dequantisation overlaps the other's MFMAs.
+// ---------------------------------------------------------------------------
+constexpr int kW2BM = 128, kW2BK = 64;
+
+template <int BN>
+struct W2Cfg {
+  static constexpr int kABytes = kW2BM * kW2BK * 2;     // 16 KiB
+  static constexpr int kQBytes = (kW2BK / 8) * BN * 4;  // 8 packed rows
+  static constexpr int kSBytes = BN * 2;                // one scale row
+  static constexpr int kStage = kABytes + kQBytes + kSBytes;
+  static constexpr int kStages = 3;
+  static constexpr int kBBytes = BN * kW2BK * 2;        // dequantised tile [n][k]
+  static constexpr int kLPI = 4 + 1 + 1;                // transfers per wave per stage
+  static constexpr int kNB = BN / 32;                   // 16-column blocks per wave
+  static constexpr int kWords = BN / 32;                // packed words per thread per stage
+  static_assert(kStages * kStage + kBBytes <= 80 * 1024, "two work-groups per CU");
+};
+
+template <int N>
+__device__ __forceinline__ void w2_wait() {  // vmcnt(N) lgkmcnt(0)
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | (((N >> 4) & 3) << 14));
+}
+
+template <int BN>
+__global__ __launch_bounds__(256, 2) void w4g2_kernel(GArgs a) {
+  using Cf = W2Cfg<BN>;
+  constexpr int kS = Cf::kStages, kP = kS - 1, LPI = Cf::kLPI, NB = Cf::kNB, NW = Cf::kWords;
+  __shared__ __align__(16) uint8_t ring[kS * Cf::kStage];
+  __shared__ __align__(16) uint8_t btile[Cf::kBBytes];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  // the m-tiles of one n-tile take linear indices 8 apart: one XCD, whose
+  // L2 then serves their common packed weights
+  const int L = blockIdx.x;
+  const int ntile = (L % 8) + 8 * (L / (8 * a.mtiles));
+  const int mti = (L / 8) % a.mtiles;
+  if (ntile >= a.ntiles) return;
+  const int m0 = mti * kW2BM, n0 = ntile * BN;
+  const int iters = a.K / kW2BK;
+
+  // transfer sources (the step's k offset is added per issue)
+  const uint16_t *asrc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * (4 * wave + j) + (lane >> 3);  // 1 KiB = 8 rows of A
+    const int c = (lane & 7) ^ (row & 7);
+    asrc[j] = a.A + (long long)min(m0 + row, a.M - 1) * a.K + 8 * c;
+  }
+  // packed rows 2w, 2w + 1 of the step: BN / 2 lanes of 16 bytes
+  const uint32_t *qsrc = a.q + (long long)(2 * wave + lane / (BN / 4)) * a.N + n0 + 4 * (lane % (BN / 4));
+  // the scale row: BN / 32 lanes of 16 bytes (8 columns) per wave
+  const __half *ssrc = a.s + n0 + (wave * (BN / 32) + lane) * 8;
+  auto issue = [&](int u) {
+    uint8_t *st = ring + (u % kS) * Cf::kStage;
+    const int k0 = u * kW2BK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(asrc[j] + k0, (CFA_LDS void *)(st + 1024 * (4 * wave + j)));
+    if (lane < BN / 2)
+      dma16(qsrc + (long long)(k0 / 8) * a.N, (CFA_LDS void *)(st + Cf::kABytes + wave * (8 * BN)));
+    if (lane < BN / 32)
+      dma16(ssrc + (long long)(k0 / a.group) * a.N,
+            (CFA_LDS void *)(st + Cf::kABytes + Cf::kQBytes + wave * (BN / 32) * 16));
+  };
+
+  // dequantisation share: packed row pr, words wc .. wc + NW - 1
+  const int pr = tid >> 5, wc = (tid & 31) * NW;
+  // operand read offsets: A row m / B row n hold 64 k (128 bytes), chunk c
+  // at position c ^ (row % 8)
+  const int g = lane >> 4, col = lane & 15;
+  int aoff[4][2], boff[NB][2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = wm * 64 + 16 * i + col;
+      aoff[i][kk] = row * 128 + (((kk * 4 + g) ^ (row & 7)) << 4);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int n = wn * (BN / 2) + 16 * j + col;
+      boff[j][kk] = n * 128 + (((kk * 4 + g) ^ (n & 7)) << 4);
+    }
+  }
+
+  f32x4 acc[4][NB];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int u = 0; u < min(kP, iters); ++u) issue(u);
+  for (int it = 0; it < iters; ++it) {
+    // this wave's part of stage `it` has landed and its LDS reads of step
+    // it - 1 have returned; after the barrier the dequantised tile and the
+    // ring slot refilled below (last read in step it - 1) are free
+    if (it + 1 < iters) w2_wait<LPI>();
+    else w2_wait<0>();
+    block_barrier();
+    if (it + kP < iters) issue(it + kP);
+    const uint8_t *st = ring + (it % kS) * Cf::kStage;
+    {
+      uint32_t w[NW];
+      const uint8_t *qp = st + Cf::kABytes + pr * (BN * 4) + wc * 4;
+      if (NW == 4) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(qp);
+        w[0] = v.x; w[1] = v.y; w[2 % NW] = v.z; w[3 % NW] = v.w;
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2 *>(qp);
+        w[0] = v.x; w[1 % NW] = v.y;
+      }
+      const __half *sp = reinterpret_cast<const __half *>(st + Cf::kABytes + Cf::kQBytes) + wc;
+#pragma unroll
+      for (int j = 0; j < NW; ++j) {
+        const float sf = __half2float(sp[j]);
+        uint32_t o[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const float f0 = (float)((w[j] >> (8 * p)) & 15u) * sf;
+          const float f1 = (float)((w[j] >> (8 * p + 4)) & 15u) * sf;
+          o[p] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f0) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f1) << 16);
+        }
+        const int n = wc + j;
+        *reinterpret_cast<uint4 *>(btile + n * 128 + ((pr ^ (n & 7)) << 4)) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    block_barrier();  // the dequantised tile is complete
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf16x8 bfr[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) bfr[j] = *reinterpret_cast<const bf16x8 *>(btile + boff[j][kk]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bf16x8 af = *reinterpret_cast<const bf16x8 *>(st + aoff[i][kk]);
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // C[row][col]: acc[i][j][e], row = m0 + 64 wm + 16 i + 4 g + e,
+  // col = n0 + (BN / 2) wn + 16 j + lane % 16
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = m0 + wm * 64 + 16 * i + 4 * g + e;
+      if (row >= a.M) continue;
+      uint16_t *cr = a.C + (long long)row * a.N + n0 + wn * (BN / 2) + col;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) cr[16 * j] = __builtin_bit_cast(uint16_t, (__bf16)acc[i][j][e]);
+    }
+}
+
 }  // namespace w4
 }  // namespace cfa
 
@@ -457,7 +628,7 @@ extern "C" int cfa_w4a16_gemm(const void *a, const uint32_t *b_quant, const void
   using namespace cfa::abi;
   clear_error();
   if (M <= 0 || N <= 0 || K <= 0) return fail_arg("M, N and K must be positive");
-  if (N % cfa::w4::kGBN != 0) return fail_arg("N must be a multiple of 256");
+  if (N % 64 != 0) return fail_arg("N must be a multiple of 64");
   if (group_size <= 0 || group_size % cfa::w4::kGBK != 0 || K % group_size != 0)
     return fail_arg("group_size must be a multiple of 64 that divides K");
   if (!a || !b_quant || !scales || !c) return fail_arg("null pointer");
@@ -472,8 +643,25 @@ extern "C" int cfa_w4a16_gemm(const void *a, const uint32_t *b_quant, const void
   g.N = N;
   g.K = K;
   g.group = group_size;
-  g.ntiles = N / cfa::w4::kGBN;
   const int cus = device_cu_count();
+  // bf16 with many rows: the cooperative-dequantisation kernel
+  if (!fp16 && N % 64 == 0 && group_size % cfa::w4::kW2BK == 0 && K % group_size == 0 &&
+      ((uintptr_t)scales & 15) == 0 && M > 64) {
+    const int mt = (M + cfa::w4::kW2BM - 1) / cfa::w4::kW2BM;
+    const int bn = (N % 128 == 0 && (long long)mt * (N / 128) >= cus) ? 128 : 64;
+    g.mtiles = mt;
+    g.ntiles = N / bn;
+    const long long blocks = (long long)mt * ((g.ntiles + 7) / 8) * 8;
+    if (blocks > 0x7fffffffLL) return fail_arg("problem too large");
+    hipStream_t st = (hipStream_t)stream;
+    if (bn == 128)
+      CFA_LAUNCH("w4a16_gemm", cfa::w4::w4g2_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, st, g);
+    else
+      CFA_LAUNCH("w4a16_gemm", cfa::w4::w4g2_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, st, g);
+    return CFA_OK;
+  }
+  if (N % cfa::w4::kGBN != 0) return fail_arg("N must be a multiple of 256 (64 for bf16 with M > 64)");
+  g.ntiles = N / cfa::w4::kGBN;
   const bool small = ((M + 63) / 64) * g.ntiles < cus;  // 32-row tiles fill the chip better
   const int BM = small ? 32 : 64;
   g.mtiles = (M + BM - 1) / BM;

@@ -73,7 +73,9 @@ def w4a16_dequant(b_quant: torch.Tensor, scales: torch.Tensor, zeros: Optional[t
 def fused_gemm_ok(a: torch.Tensor, b_quant: torch.Tensor, zeros, group_size: int) -> bool:
     """Whether cfa_w4a16_gemm takes this problem (else dequantise + GEMM)."""
     N = b_quant.shape[1]
-    return (zeros is None and N % 256 == 0 and group_size % 64 == 0 and a.is_contiguous()
+    many_rows_bf16 = a.dtype == torch.bfloat16 and a.shape[0] > 64 and N % 64 == 0
+    return (zeros is None and (N % 256 == 0 or many_rows_bf16) and group_size % 64 == 0
+            and a.is_contiguous()
             and b_quant.is_contiguous() and a.data_ptr() % 16 == 0 and b_quant.data_ptr() % 16 == 0)
 
 
