@@ -253,11 +253,13 @@ int cfa_w4a16_dequant_t(const uint32_t *b_quant, const void *scales, const void 
                         int N, int group_size, int out_bf16, void *out, void *stream);
 
 /* Fused W4A16 GEMM: c [M, N] = a [M, K] x dequant(b_quant, scales) with the
- * dequantisation of cfa_w4a16_dequant (no zero points) done in registers and
- * fp32 accumulation on MFMA.  fp16 = 1: a and c fp16 (int4_gemm_dequant.cu /
- * int4_dequant_triton.py semantics); fp16 = 0: bf16.  N % 256 == 0,
- * group_size % 64 == 0, K % group_size == 0; a, b_quant, c 16-byte aligned,
- * scales 8-byte aligned. */
+ * dequantisation of cfa_w4a16_dequant (no zero points) done on the device
+ * (in LDS for bf16 with M > 64, in registers otherwise) and fp32
+ * accumulation on MFMA.  fp16 = 1: a and c fp16 (int4_gemm_dequant.cu /
+ * int4_dequant_triton.py semantics); fp16 = 0: bf16.  N % 256 == 0 (bf16
+ * with M > 64 and 16-byte aligned scales: N % 64 == 0), group_size % 64 == 0,
+ * K % group_size == 0; a, b_quant, c 16-byte aligned, scales 8-byte
+ * aligned. */
 int cfa_w4a16_gemm(const void *a, const uint32_t *b_quant, const void *scales, int M, int N,
                    int K, int group_size, int fp16, void *c, void *stream);
 
