@@ -85,21 +85,23 @@ def test_reference_gemm_parity(device, M, N, K):
     torch.testing.assert_close(c, c_ref, atol=1e-2, rtol=1e-2)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("M,N,K", [(1, 256, 128), (37, 1024, 512), (504, 512, 4096),
-                                   (64, 768, 256), (200, 256, 1024), (504, 8192, 256),
-                                   (130, 192, 512)])
+_FUSED_SHAPES = [(1, 256, 128), (37, 1024, 512), (504, 512, 4096), (64, 768, 256),
+                 (200, 256, 1024), (504, 8192, 256)]
+
+
+@pytest.mark.parametrize("dtype,M,N,K",
+                         [(d, *shape) for d in (torch.bfloat16, torch.float16) for shape in _FUSED_SHAPES]
+                         + [(torch.bfloat16, 130, 192, 512)])
 def test_fused_gemm_vs_dequantised_fp32(device, dtype, M, N, K):
     """cfa_w4a16_gemm against an fp32 product of the bit-exact dequantised
     weights: differences come from the fp32 accumulation order and the final
     rounding to 16 bits (tolerance 1e-2 of the output scale + 2^-7 relative).
     bf16 with M > 64 takes the cooperative-dequantisation kernel: 64-column
-    tiles at (504, 512), (200, 256), (130, 192: a partial last m-tile),
-    128-column tiles at (504, 8192)."""
+    tiles at (504, 512), (200, 256), (130, 192: a partial last m-tile; bf16
+    only, as the fp16 kernel takes N % 256 == 0), 128-column tiles at
+    (504, 8192)."""
     from cudaforge_amd.w4a16 import w4a16_gemm
 
-    if dtype == torch.float16 and N % 256:
-        pytest.skip("the fp16 kernel takes N % 256 == 0 (the bf16 one N % 64 == 0 for M > 64)")
     g = torch.Generator().manual_seed(M + N + K)
     group = 128
     a = torch.randn(M, K, generator=g).to(dtype).to(device)
