@@ -466,28 +466,39 @@ __global__ __launch_bounds__(256, 2) void w4gemm_kernel(GArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kW2BM = 128, kW2BK = 64;
 
-template <int BN>
+template <int BN, int ST>
 struct W2Cfg {
   static constexpr int kABytes = kW2BM * kW2BK * 2;     // 16 KiB
   static constexpr int kQBytes = (kW2BK / 8) * BN * 4;  // 8 packed rows
   static constexpr int kSBytes = BN * 2;                // one scale row
   static constexpr int kStage = kABytes + kQBytes + kSBytes;
-  static constexpr int kStages = 3;
+  static constexpr int kStages = ST;
   static constexpr int kBBytes = BN * kW2BK * 2;        // dequantised tile [n][k]
   static constexpr int kLPI = 4 + 1 + 1;                // transfers per wave per stage
   static constexpr int kNB = BN / 32;                   // 16-column blocks per wave
   static constexpr int kWords = BN / 32;                // packed words per thread per stage
-  static_assert(kStages * kStage + kBBytes <= 80 * 1024, "two work-groups per CU");
+  static_assert(ST > 3 || kStages * kStage + kBBytes <= 80 * 1024, "two work-groups per CU");
+  static_assert(kStages * kStage + kBBytes <= 160 * 1024, "LDS");
 };
 
 template <int N>
 __device__ __forceinline__ void w2_wait() {  // vmcnt(N) lgkmcnt(0)
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | (((N >> 4) & 3) << 14));
 }
+// vmcnt(n * LPI) lgkmcnt(0) for a run-time 0 <= n <= N
+template <int LPI, int N>
+__device__ __forceinline__ void w2_wait_stages(int n) {
+  if constexpr (N == 0) {
+    w2_wait<0>();
+  } else {
+    if (n >= N) w2_wait<N * LPI>();
+    else w2_wait_stages<LPI, N - 1>(n);
+  }
+}
 
-template <int BN>
+template <int BN, int ST>
 __global__ __launch_bounds__(256, 2) void w4g2_kernel(GArgs a) {
-  using Cf = W2Cfg<BN>;
+  using Cf = W2Cfg<BN, ST>;
   constexpr int kS = Cf::kStages, kP = kS - 1, LPI = Cf::kLPI, NB = Cf::kNB, NW = Cf::kWords;
   __shared__ __align__(16) uint8_t ring[kS * Cf::kStage];
   __shared__ __align__(16) uint8_t btile[Cf::kBBytes];
@@ -558,8 +569,7 @@ __global__ __launch_bounds__(256, 2) void w4g2_kernel(GArgs a) {
     // this wave's part of stage `it` has landed and its LDS reads of step
     // it - 1 have returned; after the barrier the dequantised tile and the
     // ring slot refilled below (last read in step it - 1) are free
-    if (it + 1 < iters) w2_wait<LPI>();
-    else w2_wait<0>();
+    w2_wait_stages<LPI, kP - 1>(min(kP - 1, iters - 1 - it));
     block_barrier();
     if (it + kP < iters) issue(it + kP);
     const uint8_t *st = ring + (it % kS) * Cf::kStage;
@@ -654,10 +664,16 @@ extern "C" int cfa_w4a16_gemm(const void *a, const uint32_t *b_quant, const void
     const long long blocks = (long long)mt * ((g.ntiles + 7) / 8) * 8;
     if (blocks > 0x7fffffffLL) return fail_arg("problem too large");
     hipStream_t st = (hipStream_t)stream;
-    if (bn == 128)
-      CFA_LAUNCH("w4a16_gemm", cfa::w4::w4g2_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, st, g);
+    // at most one work-group per CU: spend the second one's LDS on a deeper ring
+    const bool deep = blocks <= cus;
+    if (bn == 128 && deep)
+      CFA_LAUNCH("w4a16_gemm", (cfa::w4::w4g2_kernel<128, 5>), dim3((unsigned)blocks), dim3(256), 0, st, g);
+    else if (bn == 128)
+      CFA_LAUNCH("w4a16_gemm", (cfa::w4::w4g2_kernel<128, 3>), dim3((unsigned)blocks), dim3(256), 0, st, g);
+    else if (deep)
+      CFA_LAUNCH("w4a16_gemm", (cfa::w4::w4g2_kernel<64, 5>), dim3((unsigned)blocks), dim3(256), 0, st, g);
     else
-      CFA_LAUNCH("w4a16_gemm", cfa::w4::w4g2_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, st, g);
+      CFA_LAUNCH("w4a16_gemm", (cfa::w4::w4g2_kernel<64, 3>), dim3((unsigned)blocks), dim3(256), 0, st, g);
     return CFA_OK;
   }
   if (N % cfa::w4::kGBN != 0) return fail_arg("N must be a multiple of 256 (64 for bf16 with M > 64)");

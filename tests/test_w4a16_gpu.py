@@ -86,7 +86,7 @@ def test_reference_gemm_parity(device, M, N, K):
 
 
 _FUSED_SHAPES = [(1, 256, 128), (37, 1024, 512), (504, 512, 4096), (64, 768, 256),
-                 (200, 256, 1024), (504, 8192, 256)]
+                 (200, 256, 1024), (504, 8192, 256), (504, 28672, 128), (504, 6144, 256)]
 
 
 @pytest.mark.parametrize("dtype,M,N,K",
@@ -99,7 +99,9 @@ def test_fused_gemm_vs_dequantised_fp32(device, dtype, M, N, K):
     bf16 with M > 64 takes the cooperative-dequantisation kernel: 64-column
     tiles at (504, 512), (200, 256), (130, 192: a partial last m-tile; bf16
     only, as the fp16 kernel takes N % 256 == 0), 128-column tiles at
-    (504, 8192)."""
+    (504, 8192); grids of at most one work-group per CU use the 5-stage
+    ring, (504, 28672) and (504, 6144) the 3-stage one at 128 and 64
+    columns."""
     from cudaforge_amd.w4a16 import w4a16_gemm
 
     g = torch.Generator().manual_seed(M + N + K)
