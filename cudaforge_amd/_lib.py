@@ -136,6 +136,7 @@ SIGNATURES: dict[str, tuple] = {
     "cfa_silu_mul": (_i, [_p, _p, _i, _i, _p]),
     "cfa_gemm_bf16_skinny_workspace_size": (_sz, [_i, _i, _i, _i]),
     "cfa_gemm_bf16_skinny": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _sz, _p]),
+    "cfa_gemm_bf16_skinny_silu": (_i, [_p, _p, _p, _i, _i, _i, _i, _p, _sz, _p]),
     "cfa_kv_cache_create": (_i, [ctypes.POINTER(KVCacheConfigC), ctypes.POINTER(_p)]),
     "cfa_kv_cache_destroy": (None, [_p]),
     "cfa_kv_cache_register_sequence": (_i, [_p, _u64, _i32p, _i64, _u32p]),

@@ -43,7 +43,7 @@ constexpr int kMaxM = 128;
 struct Args {
   const uint16_t *A;  // [M, K]
   const uint16_t *W;  // [K, N]
-  uint16_t *C;        // [M, N]
+  uint16_t *C;        // [M, N]; with the SiLU epilogue [M, N / 2]
   float *part;        // [tiles][S][4 MT blocks][4 elements][64 lanes]
   int *cnt;           // [tiles] arrival counters, zero between calls
   int M, N, K, S, tiles, steps;  // steps: pipeline steps per split
@@ -71,7 +71,16 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | (((N >> 4) & 3) << 14));
 }
 
-template <int MT>
+// The SiLU-gated epilogue rounds exactly as a bf16 GEMM followed by
+// cfa_silu_mul: g and u to bf16, then bf16(bf16(silu(g)) * u).
+__device__ __forceinline__ float bf16_round(float f) { return (float)(__bf16)f; }
+__device__ __forceinline__ uint16_t f2bf_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+template <int MT, bool SILU>
 __global__ __launch_bounds__(256) void skinny_gemm_kernel(Args a) {
   using Cf = Cfg<MT>;
   constexpr int kS = Cf::kStages, kP = kS - 1, LPI = Cf::kLPI;
@@ -189,8 +198,41 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(Args a) {
         if (row < a.M) a.C[(long long)row * a.N + ccol] = __builtin_bit_cast(uint16_t, (__bf16)v[i][e]);
       }
   };
+  // SILU: tile t of W holds gate features 32t .. 32t + 31 in its columns
+  // 0..31 and the matching up features in 32..63, so wave w < 2 pairs its
+  // gate block with wave w + 2's up block (exchanged through LDS) and
+  // writes out[row][32t + 16w + col].
+  auto finish = [&](const f32x4 (&v)[MT]) {
+    if (!SILU) {
+      store_c(v);
+      return;
+    }
+    __syncthreads();  // the reduction's LDS reads are done
+    f32x4 *xch = reinterpret_cast<f32x4 *>(lds);
+    if (wave >= 2) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) xch[((wave - 2) * MT + i) * 64 + lane] = v[i];
+    }
+    __syncthreads();
+    if (wave < 2) {
+      const int F = a.N / 2;
+      const int fcol = (n0 / 2) + 16 * wave + col;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const f32x4 up = xch[(wave * MT + i) * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = 16 * i + 4 * g + e;
+          if (row >= a.M) continue;
+          const float gv = bf16_round(v[i][e]), uv = bf16_round(up[e]);
+          const float sv = __uint_as_float((uint32_t)f2bf_rne(gv / (1.0f + expf(-gv))) << 16);
+          a.C[(long long)row * F + fcol] = f2bf_rne(sv * uv);
+        }
+      }
+    }
+  };
   if (a.S == 1) {
-    store_c(sum);
+    finish(sum);
     return;
   }
   // Partials cross XCDs, whose L2s are not coherent with each other: they
@@ -223,7 +265,7 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(Args a) {
         sum[i][e] = q == 0 ? v : sum[i][e] + v;
       }
   }
-  store_c(sum);
+  finish(sum);
   if (tid == 0) __hip_atomic_store(a.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -262,9 +304,8 @@ extern "C" size_t cfa_gemm_bf16_skinny_workspace_size(int M, int N, int K, int s
   return cfa::sg::workspace_bytes(M, N, S);
 }
 
-extern "C" int cfa_gemm_bf16_skinny(const void *a, const void *w, void *c, int M, int N, int K,
-                                    int splits, void *workspace, size_t workspace_bytes,
-                                    void *stream) {
+static int skinny_launch(const void *a, const void *w, void *c, int M, int N, int K, int splits,
+                         void *workspace, size_t workspace_bytes, void *stream, bool silu) {
   using namespace cfa::abi;
   namespace sg = cfa::sg;
   clear_error();
@@ -298,19 +339,32 @@ extern "C" int cfa_gemm_bf16_skinny(const void *a, const void *w, void *c, int M
   const long long blocks = (long long)(g.tiles + 7) / 8 * 8 * S;
   if (blocks > 0x7fffffffLL) return fail_arg("problem too large");
   hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)blocks), block(256);
+#define CFA_SKINNY(MT)                                                                         \
+  do {                                                                                         \
+    if (silu)                                                                                  \
+      CFA_LAUNCH("gemm_bf16_skinny", (sg::skinny_gemm_kernel<MT, true>), grid, block, 0, st, g);  \
+    else                                                                                       \
+      CFA_LAUNCH("gemm_bf16_skinny", (sg::skinny_gemm_kernel<MT, false>), grid, block, 0, st, g); \
+  } while (0)
   switch (sg::m_tiles(M)) {
-    case 1:
-      CFA_LAUNCH("gemm_bf16_skinny", sg::skinny_gemm_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, st, g);
-      break;
-    case 2:
-      CFA_LAUNCH("gemm_bf16_skinny", sg::skinny_gemm_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, st, g);
-      break;
-    case 4:
-      CFA_LAUNCH("gemm_bf16_skinny", sg::skinny_gemm_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, st, g);
-      break;
-    default:
-      CFA_LAUNCH("gemm_bf16_skinny", sg::skinny_gemm_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, st, g);
-      break;
+    case 1: CFA_SKINNY(1); break;
+    case 2: CFA_SKINNY(2); break;
+    case 4: CFA_SKINNY(4); break;
+    default: CFA_SKINNY(8); break;
   }
+#undef CFA_SKINNY
   return CFA_OK;
+}
+
+extern "C" int cfa_gemm_bf16_skinny(const void *a, const void *w, void *c, int M, int N, int K,
+                                    int splits, void *workspace, size_t workspace_bytes,
+                                    void *stream) {
+  return skinny_launch(a, w, c, M, N, K, splits, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int cfa_gemm_bf16_skinny_silu(const void *a, const void *w, void *out, int M, int N,
+                                         int K, int splits, void *workspace,
+                                         size_t workspace_bytes, void *stream) {
+  return skinny_launch(a, w, out, M, N, K, splits, workspace, workspace_bytes, stream, true);
 }

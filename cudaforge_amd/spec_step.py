@@ -120,6 +120,48 @@ def skinny_gemm(a: torch.Tensor, w: torch.Tensor, workspace: Optional[torch.Tens
     return out
 
 
+def interleave_gate_up(w: torch.Tensor) -> torch.Tensor:
+    """[K, 2F] = [gate | up] -> the layout cfa_gemm_bf16_skinny_silu takes:
+    64-column tile t = gate features 32t .. 32t + 31, then their up columns."""
+    K, F2 = w.shape
+    F = F2 // 2
+    if F % 32:
+        raise ValueError("F must be a multiple of 32")
+    return torch.stack([w[:, :F].reshape(K, F // 32, 32), w[:, F:].reshape(K, F // 32, 32)],
+                       dim=2).reshape(K, F2).contiguous()
+
+
+def deinterleave_gate_up(w: torch.Tensor) -> torch.Tensor:
+    """Inverse of interleave_gate_up (columns of a [.., 2F] tensor)."""
+    lead, F2 = w.shape[:-1], w.shape[-1]
+    v = w.reshape(*lead, F2 // 64, 2, 32)
+    return torch.cat([v[..., 0, :].reshape(*lead, F2 // 2), v[..., 1, :].reshape(*lead, F2 // 2)],
+                     dim=-1)
+
+
+def skinny_gemm_silu(a: torch.Tensor, w_il: torch.Tensor, workspace: Optional[torch.Tensor] = None,
+                     *, splits: int = 0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """silu(a @ W_gate) * (a @ W_up) for M <= 128 with the gate/up weights in
+    the interleave_gate_up layout (cfa_gemm_bf16_skinny_silu): bit-identical
+    to silu_mul(skinny_gemm(a, W)) on the [gate | up] weights."""
+    M, K = a.shape
+    N = w_il.shape[1]
+    if w_il.shape[0] != K:
+        raise ValueError("inner dimensions differ")
+    if a.dtype != torch.bfloat16 or w_il.dtype != torch.bfloat16:
+        raise ValueError("a and w must be bfloat16")
+    if not (a.is_contiguous() and w_il.is_contiguous()):
+        raise ValueError("a and w must be contiguous (row-major)")
+    if out is None:
+        out = torch.empty(M, N // 2, dtype=a.dtype, device=a.device)
+    ws_ptr, ws_n = (workspace.data_ptr(), workspace.numel() * workspace.element_size()) \
+        if workspace is not None else (None, 0)
+    rc = _lib.load().cfa_gemm_bf16_skinny_silu(a.data_ptr(), w_il.data_ptr(), out.data_ptr(), M,
+                                               N, K, splits, ws_ptr, ws_n, _stream_ptr(a.device))
+    _lib.check(rc, "cfa_gemm_bf16_skinny_silu")
+    return out
+
+
 def rope_kv_pools(qkv: torch.Tensor, pos: torch.Tensor, B: int, n: int, s: "LlamaShape",
                   q_out: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, layer: int,
                   block_tables: torch.Tensor, base: torch.Tensor) -> None:
@@ -245,7 +287,9 @@ class DraftModel:
                 wqkv=_randn((d, qkv_n), g, device, 1.0 / math.sqrt(d)),
                 wo=_randn((s.n_heads * hd, d), g, device, 1.0 / math.sqrt(s.n_heads * hd)),
                 ffn_norm=torch.ones(d, dtype=torch.bfloat16, device=device),
-                wgu=_randn((d, 2 * s.ffn), g, device, 1.0 / math.sqrt(d)),
+                # gate/up in the interleave_gate_up layout (the fused
+                # SiLU-gated projection's)
+                wgu=interleave_gate_up(_randn((d, 2 * s.ffn), g, device, 1.0 / math.sqrt(d))),
                 wdown=_randn((s.ffn, d), g, device, 1.0 / math.sqrt(s.ffn))))
         self.norm = torch.ones(d, dtype=torch.bfloat16, device=device)
         self.lm_head = self.embed.t().contiguous()              # tied embeddings
@@ -273,6 +317,12 @@ class DraftModel:
         if x.shape[0] <= 128:
             return skinny_gemm(x, w, self.gemm_ws)
         return x @ w
+
+    def _ffn_up(self, x: torch.Tensor, w_il: torch.Tensor) -> torch.Tensor:
+        """silu(x @ W_gate) * (x @ W_up), W in the interleave_gate_up layout."""
+        if x.shape[0] <= 128:
+            return skinny_gemm_silu(x, w_il, self.gemm_ws)
+        return silu_mul(deinterleave_gate_up(x @ w_il).contiguous())
 
     def forward_level(self, tokens: torch.Tensor, positions: torch.Tensor, base: torch.Tensor,
                       lo: int, masks: torch.Tensor) -> torch.Tensor:
@@ -305,7 +355,7 @@ class DraftModel:
                                first_node=lo)
             delta = self._mm(o.view(B * n, Hq * hd), L["wo"])
             rmsnorm_(h, delta, L["ffn_norm"], s.eps, x)
-            delta = self._mm(silu_mul(self._mm(x, L["wgu"])), L["wdown"])
+            delta = self._mm(self._ffn_up(x, L["wgu"]), L["wdown"])
         rmsnorm_(h, delta, self.norm, s.eps, x)
         return (x @ self.lm_head).float().view(B, n, s.vocab)
 

@@ -306,6 +306,14 @@ int cfa_silu_mul(const void *gu, void *out, int M, int F, void *stream);
 size_t cfa_gemm_bf16_skinny_workspace_size(int M, int N, int K, int splits);
 int cfa_gemm_bf16_skinny(const void *a, const void *w, void *c, int M, int N, int K, int splits,
                          void *workspace, size_t workspace_bytes, void *stream);
+/* The same product with a SiLU-gated epilogue: w [K, N] holds, in each
+ * 64-column tile t, gate columns for features 32t .. 32t + 31 followed by
+ * the up columns of the same features; out [M, N / 2] = bf16(bf16(silu(g))
+ * * u) with g and u the product's columns rounded to bf16, bit-identical to
+ * cfa_gemm_bf16_skinny on the de-interleaved [g | u] weights followed by
+ * cfa_silu_mul.  Workspace as cfa_gemm_bf16_skinny. */
+int cfa_gemm_bf16_skinny_silu(const void *a, const void *w, void *out, int M, int N, int K,
+                              int splits, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
  * Paged KV cache page tables (host metadata).

@@ -5,7 +5,8 @@ order."""
 import pytest
 import torch
 
-from cudaforge_amd.spec_step import skinny_gemm, skinny_gemm_workspace_bytes
+from cudaforge_amd.spec_step import (deinterleave_gate_up, interleave_gate_up, silu_mul,
+                                     skinny_gemm, skinny_gemm_silu, skinny_gemm_workspace_bytes)
 
 pytestmark = pytest.mark.gpu
 
@@ -81,3 +82,29 @@ def test_rejects_bad_operands(device):
         skinny_gemm(a, w)
     with pytest.raises(ValueError):
         skinny_gemm(a.bfloat16(), w.t().contiguous().t())
+
+
+def test_gate_up_layout_round_trip():
+    w = torch.arange(3 * 256, dtype=torch.float32).view(3, 256)
+    il = interleave_gate_up(w)
+    assert torch.equal(il[:, :32], w[:, :32]) and torch.equal(il[:, 32:64], w[:, 128:160])
+    assert torch.equal(deinterleave_gate_up(il), w)
+
+
+@pytest.mark.parametrize("M", [1, 8, 17, 64, 128])
+@pytest.mark.parametrize("splits", [1, 2, 0])
+def test_silu_epilogue_bit_exact(device, M, splits):
+    """cfa_gemm_bf16_skinny_silu equals the plain product on the same
+    interleaved weights, de-interleaved, followed by cfa_silu_mul -- bit for
+    bit (the same sums, the same roundings)."""
+    K, F = 512, 384
+    g = torch.Generator().manual_seed(100 + M)
+    a = torch.randn(M, K, generator=g).bfloat16().to(device)
+    w = (torch.randn(K, 2 * F, generator=g) * 2 / K ** 0.5).bfloat16()
+    w_il = interleave_gate_up(w).to(device)
+    ws = _workspace(device, M, 2 * F, K, splits)
+    fused = skinny_gemm_silu(a, w_il, ws, splits=splits)
+    plain = silu_mul(deinterleave_gate_up(skinny_gemm(a, w_il, ws, splits=splits)).contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), plain.view(torch.int16))
+    assert int(ws[:65536].count_nonzero()) == 0

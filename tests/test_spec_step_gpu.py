@@ -10,7 +10,8 @@ import pytest
 import torch
 
 from cudaforge_amd import tree as T
-from cudaforge_amd.spec_step import DraftModel, LlamaShape, TargetModel, TreeSpeculator
+from cudaforge_amd.spec_step import (DraftModel, LlamaShape, TargetModel, TreeSpeculator,
+                                     deinterleave_gate_up)
 from cudaforge_amd.w4a16 import w4a16_dequant
 
 pytestmark = pytest.mark.gpu
@@ -129,7 +130,7 @@ def _ref_draft_level(dm: DraftModel, tokens, positions, base, lo, N):
                 o[b, :, hh] = torch.softmax(sc, -1) @ vv[:, hh // G]
         h = h + o.reshape(B * n, Hq * hd) @ L["wo"].float()
         x = _rms(h, L["ffn_norm"], s.eps)
-        gu = x @ L["wgu"].float()
+        gu = deinterleave_gate_up(x @ L["wgu"].float())     # stored gate/up-interleaved
         h = h + (torch.nn.functional.silu(gu[:, : s.ffn]) * gu[:, s.ffn:]) @ L["wdown"].float()
     h = _rms(h, dm.norm, s.eps)
     return (h @ dm.lm_head.float()).view(B, n, s.vocab)
