@@ -187,6 +187,33 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *gu, uint1
   out[t] = f2bf(s * u);
 }
 
+// The same, eight features per thread with 16-byte loads and stores
+// (F % 8 == 0, 16-byte aligned gu and out).
+__global__ __launch_bounds__(256) void silu_mul8_kernel(const uint16_t *gu, uint16_t *out, int M,
+                                                        int F) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  const int F8 = F / 8;
+  if (t >= (long long)M * F8) return;
+  const long long m = t / F8, f = (t % F8) * 8;
+  const uint4 gv = *reinterpret_cast<const uint4 *>(gu + m * 2 * F + f);
+  const uint4 uv = *reinterpret_cast<const uint4 *>(gu + m * 2 * F + F + f);
+  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t ow[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float g = bf2f((uint16_t)(gw[j] >> (16 * h)));
+      const float u = bf2f((uint16_t)(uw[j] >> (16 * h)));
+      const float s = bf2f(f2bf(g / (1.0f + expf(-g))));
+      r |= (uint32_t)f2bf(s * u) << (16 * h);
+    }
+    ow[j] = r;
+  }
+  *reinterpret_cast<uint4 *>(out + m * F + f) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+}
+
 }  // namespace ops
 }  // namespace cfa
 
@@ -287,7 +314,13 @@ extern "C" int cfa_silu_mul(const void *gu, void *out, int M, int F, void *strea
   if (M <= 0 || F <= 0) return fail_arg("bad shape");
   if (!gu || !out) return fail_arg("null pointer");
   const long long total = (long long)M * F;
-  CFA_LAUNCH("silu_mul", silu_mul_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-             (hipStream_t)stream, (const uint16_t *)gu, (uint16_t *)out, M, F);
+  if (F % 8 == 0 && (((uintptr_t)gu | (uintptr_t)out) & 15) == 0) {
+    const long long items = total / 8;
+    CFA_LAUNCH("silu_mul", silu_mul8_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+               (hipStream_t)stream, (const uint16_t *)gu, (uint16_t *)out, M, F);
+  } else {
+    CFA_LAUNCH("silu_mul", silu_mul_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+               (hipStream_t)stream, (const uint16_t *)gu, (uint16_t *)out, M, F);
+  }
   return CFA_OK;
 }

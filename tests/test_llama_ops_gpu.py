@@ -55,6 +55,26 @@ def test_silu_mul(device):
     assert err <= 2 * ULP, err
 
 
+def test_silu_mul_vector_path_bit_exact(device):
+    """The 8-wide kernel (F % 8 == 0, aligned) and the one-element kernel
+    (taken here through a 2-byte-misaligned output) give identical bits."""
+    from cudaforge_amd import _lib
+    from cudaforge_amd.verify import _stream_ptr
+
+    M, F = 7, 4096
+    gu = (3 * torch.randn(M, 2 * F, generator=torch.Generator().manual_seed(5))).bfloat16().to(device)
+    buf = torch.empty(2 * M * F + 16, dtype=torch.bfloat16, device=device)
+    aligned = buf[: M * F]
+    shifted = buf[M * F + 1: 2 * M * F + 1]
+    lib = _lib.load()
+    for out in (aligned, shifted):
+        _lib.check(lib.cfa_silu_mul(gu.data_ptr(), out.data_ptr(), M, F, _stream_ptr(gu.device)),
+                   "cfa_silu_mul")
+    torch.cuda.synchronize()
+    assert shifted.data_ptr() % 16 != 0
+    assert torch.equal(aligned.view(torch.int16), shifted.view(torch.int16))
+
+
 def test_rope_kv_paged(device):
     s = LlamaShape(2, 512, 4, 2, 128, 256, 100)
     B, n, bs = 3, 5, 16
