@@ -43,14 +43,16 @@ constexpr int kMwMaxBad = 64;               // cached serial tiles per row and p
 constexpr int kMwMaxNC = 4096;              // chunks per row (V <= 4M)
 struct MwJob {  // what sequence b still has to draw
   int kind, row, n, eos_acc;
-  float u;
+  float u;          // the draw's threshold (python mode: see py_threshold)
   float tM, tInvS;  // (max, 1/S) of the target row (logits input)
   float dM, dInvS;  // and of the draft row of a residual draw
-  int pad[3];
+  int extra;        // python mode: a bonus draw follows the resample
+  float u2;         // and its threshold
+  int pad;
 };
-struct MwRes {  // per sequence: residual sum, fallback flag, drawn index
+struct MwRes {  // per sequence: residual sum, fallback flag, drawn index(es)
   float S;
-  int fallback, idx, pad;
+  int fallback, idx, idx2;
 };
 struct MwRec {  // a tile's function of the entry parity, its region guess, pad = 1: replay
   uint32_t e, o;
@@ -76,7 +78,8 @@ struct Args {
   const float *drf;
   long long d_sb, d_sk;
   const int32_t *tokens;  // [B,K]
-  const float *U;         // [B,K+1]
+  const float *U;         // [B,ustride]
+  int ustride;            // uniforms per sequence: K+1, or K+2 in python mode
   int B, K, V, rpb;       // rows per sequence: K+1 (greedy) or 2K+1
   int draws;              // jobs per input row (sequence b reads row b / draws)
   int R;                  // distinct rows: (B / draws) * rpb
@@ -316,7 +319,8 @@ __device__ int row_argmax(const Args &a, int r) {
 
 constexpr int kMaxK = 64;
 
-__device__ void write_job(const Args &a, int b, int n, int kind, int row, int eos_acc, float u);
+__device__ void write_job(const Args &a, int b, int n, int kind, int row, int eos_acc, float u,
+                          int extra = 0, float u2 = 0.0f);
 
 __global__ __launch_bounds__(64) void decide_kernel(Args a) {
   const int b = blockIdx.x, lane = threadIdx.x;
@@ -340,7 +344,7 @@ __global__ __launch_bounds__(64) void decide_kernel(Args a) {
     for (int i = lane; i <= K; i += 64) am[i] = row_argmax(a, (b / a.draws) * a.rpb + i);
   __syncthreads();
   if (lane != 0) return;
-  const float *U = a.U + (long long)b * (K + 1);
+  const float *U = a.U + (long long)b * a.ustride;
   int n = 0, kind = kNone, row = -1, eos_acc = 0;
   float uf = 0.0f;
   if (a.mode == CFA_MODE_CPP) {
@@ -506,10 +510,22 @@ __device__ float topk_threshold(const Dist &t, int V, int top_k, double *red) {
 // are per sequence, so decide writes them directly.
 // ---------------------------------------------------------------------------
 
-// The job of sequence b: its draw (n, kind, row, eos_acc, uniform u) and the
-// statistics of the draw's rows, once for every kernel that reads them; also
-// resets the walk state of b.
-__device__ void write_job(const Args &a, int b, int n, int kind, int row, int eos_acc, float u) {
+// Python-mode draws take the first index whose sequential prefix sum
+// EXCEEDS u (so u = 0 never selects a zero-weight entry, as torch.multinomial
+// never does); the inverse-CDF walks test `r <= prefix`, and for floats
+// u < x <=> succ(u) <= x.  The floor FLT_MIN keeps r out of the denormals.
+__device__ __forceinline__ float py_threshold(float u) {
+  // for finite u >= 0 the next float up is the next bit pattern
+  const float s = (u >= 0.0f && u < INFINITY) ? __uint_as_float(__float_as_uint(u) + 1u) : u;
+  return fmaxf(s, 1.17549435e-38f);
+}
+
+// The job of sequence b: its draw (n, kind, row, eos_acc, threshold u; a
+// python-mode bonus after the resample when extra) and the statistics of the
+// draw's rows, once for every kernel that reads them; also resets the walk
+// state of b.
+__device__ void write_job(const Args &a, int b, int n, int kind, int row, int eos_acc, float u,
+                          int extra, float u2) {
   const int K = a.K;
   MwJob j;
   j.n = n;
@@ -517,7 +533,9 @@ __device__ void write_job(const Args &a, int b, int n, int kind, int row, int eo
   j.row = row;
   j.eos_acc = eos_acc;
   j.u = u;
-  j.pad[0] = j.pad[1] = j.pad[2] = 0;
+  j.extra = extra;
+  j.u2 = u2;
+  j.pad = 0;
   j.tM = j.dM = 0.0f;
   j.tInvS = j.dInvS = 1.0f;
   if (a.logits && (j.kind == kResid || j.kind == kPlain)) {
@@ -531,7 +549,7 @@ __device__ void write_job(const Args &a, int b, int n, int kind, int row, int eo
     }
   }
   a.jobs[b] = j;
-  a.res[b] = MwRes{0.0f, 0, -1, 0};
+  a.res[b] = MwRes{0.0f, 0, -1, -1};
   a.badcnt[b] = 0;
   a.badcnt[a.B + b] = 0;
 }
@@ -546,8 +564,15 @@ __global__ __launch_bounds__(256) void plan_kernel(Args a) {
   for (int q = threadIdx.x; q < a.B; q += blockDim.x) local = min(local, a.dec[q].x);
   atomicMin(&nmin, local);
   __syncthreads();
-  for (int b = threadIdx.x; b < a.B; b += blockDim.x)
-    write_job(a, b, nmin, (nmin < K) ? kResid : kPyBonus, (nmin < K) ? nmin : K, 0, a.ufin[b]);
+  // A rejection at the last position (n = K - 1) brings the reference's
+  // num_accepted to K, so its `num_accepted == self.k` branch
+  // (speculative.py:188-195) appends a bonus draw after the resample.
+  const int extra = (K > 0 && nmin == K - 1) ? 1 : 0;
+  for (int b = threadIdx.x; b < a.B; b += blockDim.x) {
+    const float u2 = extra ? py_threshold(a.U[(long long)b * a.ustride + K + 1]) : 0.0f;
+    write_job(a, b, nmin, (nmin < K) ? kResid : kPyBonus, (nmin < K) ? nmin : K, 0,
+              py_threshold(a.ufin[b]), extra, u2);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -815,7 +840,21 @@ __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
 
 constexpr int kMwWin = 256;  // chunk records staged in LDS at a time
 
-__device__ void finish_one(const Args &a, int b, const MwJob &j, int idx);
+__device__ void finish_one(const Args &a, int b, const MwJob &j, int idx, int idx2 = -1);
+
+// Last index of positive weight of a (job, pass) row, V - 1 if none; one
+// wave scans down from the end (python mode's rare fallback draw).
+__device__ long long mw_last_positive(const Args &a, const MwElem &e) {
+  const int lane = threadIdx.x & 63;
+  for (long long base = ((long long)(a.V - 1) / 64) * 64; base >= 0; base -= 64) {
+    const long long i = base + lane;
+    bool pos = false;
+    if (i < a.V) pos = e.eval(e.t.load(i), e.fn != 2 ? e.d.load(i) : 0.0f) > 0.0f;
+    const unsigned long long m = __ballot(pos);
+    if (m) return base + 63 - __builtin_clzll(m);
+  }
+  return a.V - 1;
+}
 
 __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
   using namespace seq;
@@ -1008,6 +1047,12 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
       if (a.mode == CFA_MODE_CPP) finish_one(a, b, j, idx);
     }
   }
+  // Python mode: past the end of the prefix sums, the last entry of
+  // positive weight (the reference's C++ rule, V - 1, is kept in cpp mode).
+  if (cdf && a.mode == CFA_MODE_PYTHON && found < 0) {
+    const long long last = mw_last_positive(a, e);
+    if (lane == 0) a.res[b].idx = (int)last;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1017,22 +1062,52 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
 
 constexpr int kSampleNT = 1024;
 
+// Last index of positive weight (V - 1 if none): the block scans down from
+// the end, NT elements per step (the rare fallback past the prefix sums).
+template <int NT, class XF>
+__device__ long long block_last_positive(const XF &xf, int V, int *slot) {
+  for (long long base = ((long long)(V - 1) / NT) * NT; base >= 0; base -= NT) {
+    __syncthreads();
+    if (threadIdx.x == 0) *slot = -1;
+    __syncthreads();
+    const long long i = base + threadIdx.x;
+    if (i < V && xf.eval(xf.load(i)) > 0.0f) atomicMax(slot, (int)i);
+    __syncthreads();
+    const int f = *slot;
+    if (f >= 0) return f;
+  }
+  return V - 1;
+}
+
 __global__ __launch_bounds__(kSampleNT) void pybonus_kernel(Args a) {
   __shared__ seq::Shared<kSampleNT> sh;
   __shared__ double red[kSampleNT / 64];
+  __shared__ int last;
   const int b = blockIdx.x, V = a.V;
   const MwJob j = a.jobs[b];
-  if (j.kind != kPyBonus) return;
-  const Dist t = make_dist(a, b, j.row);
+  // the bonus of a full acceptance, or the one after a rejection at K - 1
+  if (j.kind != kPyBonus && !j.extra) return;
+  const float u = (j.kind == kPyBonus) ? j.u : j.u2;
+  const Dist t = make_dist(a, b, a.K);
   long long idx = -1;
   float vstar = (a.top_p < 1.0f) ? topp_threshold<kSampleNT>(t, V, a.top_p, red) : 0.0f;
   if (a.top_k > 0 && a.top_k < V) vstar = fmaxf(vstar, topk_threshold<kSampleNT>(t, V, a.top_k, red));
   const float S = seq::run<kSampleNT>(XKeep{t, vstar}, V, false, 0.0f, sh, nullptr);
-  if (S > 0.0f)
-    seq::run<kSampleNT>(XKeepNorm{t, vstar, S}, V, true, j.u, sh, &idx);
-  else
-    seq::run<kSampleNT>(XKeep{t, vstar}, V, true, j.u, sh, &idx);
-  if (threadIdx.x == 0) a.res[b].idx = (idx < 0) ? V - 1 : (int)idx;
+  if (S > 0.0f) {
+    const XKeepNorm xf{t, vstar, S};
+    seq::run<kSampleNT>(xf, V, true, u, sh, &idx);
+    if (idx < 0) idx = block_last_positive<kSampleNT>(xf, V, &last);
+  } else {
+    const XKeep xf{t, vstar};
+    seq::run<kSampleNT>(xf, V, true, u, sh, &idx);
+    if (idx < 0) idx = block_last_positive<kSampleNT>(xf, V, &last);
+  }
+  if (threadIdx.x == 0) {
+    if (j.kind == kPyBonus)
+      a.res[b].idx = (int)idx;
+    else
+      a.res[b].idx2 = (int)idx;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1040,7 +1115,8 @@ __global__ __launch_bounds__(kSampleNT) void pybonus_kernel(Args a) {
 // ---------------------------------------------------------------------------
 
 // Outputs of sequence b; idx is the drawn token (ignored without a draw).
-__device__ void finish_one(const Args &a, int b, const MwJob &j, int idx) {
+// idx2: the python-mode bonus that follows a resample (j.extra).
+__device__ void finish_one(const Args &a, int b, const MwJob &j, int idx, int idx2) {
   const int K = a.K;
   const int n = j.n, eos_acc = j.eos_acc;
   int fin = (j.kind == kNone) ? -1 : idx;
@@ -1049,13 +1125,15 @@ __device__ void finish_one(const Args &a, int b, const MwJob &j, int idx) {
     int v = -1;
     if (q < n) v = a.tokens[(long long)b * K + q];
     if (q == n && !eos_acc) v = fin;
+    if (q == n + 1 && j.extra) v = idx2;
     ot[q] = v;
   }
   if (eos_acc) fin = a.eos;
+  if (j.extra) fin = idx2;  // the last token emitted
   a.out_accept_len[b] = n;
   a.out_final[b] = fin;
   a.out_eos[b] = (a.mode == CFA_MODE_CPP) ? ((eos_acc || fin == a.eos) ? 1 : 0) : 0;
-  a.out_num_emitted[b] = eos_acc ? n : n + 1;
+  a.out_num_emitted[b] = eos_acc ? n : n + 1 + (j.extra ? 1 : 0);
 }
 
 // Python mode (cpp mode finishes each sequence at the end of its last walk).
@@ -1063,7 +1141,8 @@ __global__ __launch_bounds__(64) void finish_kernel(Args a) {
   const int b = blockIdx.x * 64 + threadIdx.x;
   if (b >= a.B) return;
   const MwJob j = a.jobs[b];
-  finish_one(a, b, j, a.res[b].idx);
+  const MwRes r = a.res[b];
+  finish_one(a, b, j, r.idx, r.idx2);
 }
 
 // Optional: write the probabilities the verification used.
@@ -1273,6 +1352,7 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
   a.d_sk = d_stride_k;
   a.tokens = draft_tokens;
   a.U = uniforms;
+  a.ustride = (mode == CFA_MODE_PYTHON) ? K + 2 : K + 1;
   a.B = B;
   a.K = K;
   a.V = V;
@@ -1282,7 +1362,9 @@ extern "C" int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t
   a.c = a.logits ? (float)(1.4426950408889634 / (double)temperature) : 1.0f;
   a.mode = mode;
   a.eos = eos_token_id;
-  a.top_p = top_p;
+  // top_p <= 0 keeps only the most probable token, as speculative.py:72-76
+  // does for any top_p below the largest probability; NaN filters nothing
+  a.top_p = (top_p != top_p) ? 1.0f : fmaxf(top_p, 0.0f);
   a.top_k = 0;
   a.out_accept_len = out_accept_len;
   a.out_tokens = out_tokens;
@@ -1436,6 +1518,7 @@ extern "C" int cfa_sample(const float *rows, int64_t row_stride, int input_kind,
   a.drf = nullptr;
   a.tokens = nullptr;
   a.U = uniforms;
+  a.ustride = 1;  // one uniform per draw
   a.B = B;
   a.K = 0;
   a.V = V;

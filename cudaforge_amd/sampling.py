@@ -84,7 +84,8 @@ def sample(rows: torch.Tensor, *, mode: str = "multinomial", temperature: float 
     mode "multinomial": softmax(row / T), sequential fp32 inverse CDF;
     "filtered": the top-p keep rule and top-k (<= 0: off), renormalised;
     "greedy": the `draws` largest values, largest first.  uniforms [R, draws]
-    fp32 (drawn in (0, 1] from `generator` when omitted).  Returns int32
+    fp32 (drawn from `generator` when omitted: in (0, 1] for multinomial, in
+    [0, 1) for filtered).  Returns int32
     [R, draws] (and the probabilities used, [R, V], with return_probs).
     """
     if mode not in _SMODES:
@@ -103,9 +104,13 @@ def sample(rows: torch.Tensor, *, mode: str = "multinomial", temperature: float 
     u = None
     if mode != "greedy":
         if uniforms is None:
-            # (0, 1], the range of curand_uniform: u = 0 would meet
-            # `u <= cumulative` at index 0 whatever its probability
-            u = 1.0 - torch.rand(R, draws, device=dev, generator=generator, dtype=torch.float32)
+            u = torch.rand(R, draws, device=dev, generator=generator, dtype=torch.float32)
+            if mode == "multinomial":
+                # (0, 1], the range of curand_uniform: u = 0 would meet
+                # `u <= cumulative` at index 0 whatever its probability
+                # (the filtered draw takes the first prefix sum exceeding u
+                # instead, so [0, 1) is right there)
+                u = 1.0 - u
         else:
             _require_cuda("uniforms", uniforms, torch.float32, dev)
             if tuple(uniforms.shape) != (R, draws):

@@ -17,16 +17,27 @@ the host synchronises once, to learn the accept length.
 
 Randomness.  The reference draws acceptance uniforms with ``torch.rand_like``
 (:161) and resamples with ``torch.multinomial`` (:182, :84).  Here one
-``torch.rand([B, K+1])`` from the same global generator supplies both: columns
-0..K-1 are the acceptance draws, column K drives an inverse-CDF draw for the
-resample / bonus token.  Acceptance decisions therefore follow the reference
-rule exactly for the same uniforms; resampled and bonus ids follow the same
-distributions as ``torch.multinomial`` but are not the same ids for a seed.
+``torch.rand([B, K+2])`` supplies all of them: columns 0..K-1 are the
+acceptance draws, column K drives an inverse-CDF draw for the resample /
+bonus token and column K+1 the bonus that follows a rejection at the last
+position.  Acceptance decisions therefore follow the reference rule exactly
+for the same uniforms; resampled and bonus ids follow the same distributions
+as ``torch.multinomial`` but are not the same ids for a seed.  An optional
+``generator`` (keyword-only, default: torch's global generator, as the
+reference) drives the draft draws and these uniforms; the uniforms of each
+step are returned in ``SpeculativeBatchResult.uniforms``.
+
+Reference behaviour kept: ``num_accepted`` counts the resampled or bonus token
+(:184, :195) and ``acceptance_rate = num_accepted / K`` can exceed 1; a
+rejection at the last draft position (i = K-1) brings num_accepted to K, so
+the ``num_accepted == self.k`` branch (:188) appends a bonus token as well
+(K+1 tokens, rate (K+1)/K); K = 0 raises ``ZeroDivisionError`` (:202).
 
 ``verify_mode="python"`` (default) keeps the reference's batch lock-step rule
 (one accept count n for the whole batch, :166).  ``verify_mode="cpp"`` applies
 the per-sequence rule of ``csrc/src/scheduler/speculative.cpp:50-103`` instead;
-rows then accept different counts and ``accepted_tokens`` is padded with -1.
+rows then accept different counts, ``accepted_tokens`` is padded with -1 and
+``num_accepted`` is the widest row's count.
 """
 from __future__ import annotations
 
@@ -52,6 +63,8 @@ class SpeculativeBatchResult:
     target_latency_ms: float
     # per-row emitted counts ("cpp" verify mode; None in the reference's mode)
     num_emitted_per_row: Optional[torch.Tensor] = None
+    # the step's uniforms [B, K+2] (python mode) / [B, K+1] (cpp mode)
+    uniforms: Optional[torch.Tensor] = None
 
 
 def _sync(device: torch.device) -> None:
@@ -70,6 +83,8 @@ class SpeculativeEngine:
         temperature: float = 1.0,
         top_p: float = 0.9,
         verify_mode: str = "python",
+        *,
+        generator: Optional[torch.Generator] = None,
     ) -> None:
         if verify_mode not in ("python", "cpp"):
             raise ValueError("verify_mode must be 'python' or 'cpp'")
@@ -79,9 +94,13 @@ class SpeculativeEngine:
         self.temperature = max(temperature, 1e-5)  # speculative.py:50
         self.top_p = top_p
         self.verify_mode = verify_mode
+        self.generator = generator
 
         self.total_draft_tokens: int = 0
         self.total_accepted_tokens: int = 0
+
+    def _rand(self, *shape: int, device: torch.device) -> torch.Tensor:
+        return torch.rand(*shape, device=device, dtype=torch.float32, generator=self.generator)
 
     @torch.no_grad()
     def _sample_next_token(
@@ -99,9 +118,9 @@ class SpeculativeEngine:
             raise ValueError("logits must be [B, V]")
         B = logits.shape[0]
         x = logits.float().contiguous().unsqueeze(1)
-        u = torch.rand(B, 1, device=logits.device, dtype=torch.float32)
+        u = self._rand(B, 2, device=logits.device)
         tok = torch.empty(B, 0, dtype=torch.int32, device=logits.device)
-        out = chain_verify(x, None if B == 0 else x[:, :0], tok, u, input_kind="logits",
+        out = chain_verify(x, x[:, :0], tok, u, input_kind="logits",
                            temperature=temperature, top_p=top_p, mode="python")
         return out.final.long().unsqueeze(1)
 
@@ -126,7 +145,7 @@ class SpeculativeEngine:
             draft_logits = self.draft_runner.forward(draft_input_ids, kv_cache_handles)
             next_logits = draft_logits[:, -1, :].float()
             probs = F.softmax(next_logits / self.temperature, dim=-1)
-            next_token = torch.multinomial(probs, num_samples=1)
+            next_token = torch.multinomial(probs, num_samples=1, generator=self.generator)
             draft_tokens_list.append(next_token)
             draft_logits_list.append(next_logits)
             draft_input_ids = torch.cat([draft_input_ids, next_token], dim=-1)
@@ -150,25 +169,21 @@ class SpeculativeEngine:
         t_target_ms = (time.perf_counter() - t1) * 1000.0
 
         if K == 0:
-            draft_logits = window.new_empty(batch_size, 0, window.shape[-1])
+            draft_logits = window[:, :0]
 
         # Phase 3: fused softmax + rejection sampling + resample/bonus.
-        uniforms = torch.rand(batch_size, K + 1, device=device, dtype=torch.float32)
+        python = self.verify_mode == "python"
+        uniforms = self._rand(batch_size, K + (2 if python else 1), device=device)
         res = chain_verify(
             window, draft_logits, draft_tokens.to(torch.int32), uniforms,
             input_kind="logits", temperature=self.temperature, top_p=self.top_p,
             mode=self.verify_mode)
 
-        if self.verify_mode == "python":
-            n = int(res.accept_len[0].item()) if batch_size > 0 else K  # one host sync
-            accepted_tokens = res.tokens[:, : n + 1].long()
-            num_accepted = n + 1
-            per_row = None
-        else:
-            per_row = res.num_emitted
-            width = int(per_row.max().item()) if batch_size > 0 else 1
-            accepted_tokens = res.tokens[:, :width].long()
-            num_accepted = width
+        # one host sync: the emitted count (equal on every row in python mode)
+        width = int(res.num_emitted.max().item())
+        accepted_tokens = res.tokens[:, :width].long()
+        num_accepted = width
+        per_row = None if python else res.num_emitted
         self.total_draft_tokens += K
         self.total_accepted_tokens += num_accepted
         acceptance_rate = num_accepted / K  # K = 0 raises, as speculative.py:202 does
@@ -181,6 +196,7 @@ class SpeculativeEngine:
             draft_latency_ms=t_draft_ms,
             target_latency_ms=t_target_ms,
             num_emitted_per_row=per_row,
+            uniforms=uniforms,
         )
 
     def get_aggregate_acceptance_rate(self) -> float:

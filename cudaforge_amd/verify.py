@@ -84,7 +84,9 @@ def chain_verify(target: torch.Tensor, draft: Optional[torch.Tensor],
 
     target [B, K+1, V] fp32 and draft [B, K, V] fp32 (None in greedy mode) may be
     strided views (the last dimension must be contiguous); draft_tokens [B, K]
-    int32; uniforms [B, K+1] fp32 in [0, 1) (None in greedy mode).
+    int32; uniforms fp32 in [0, 1): [B, K+1] in cpp mode, [B, K+2] in python
+    mode (column K+1 drives the bonus that follows a rejection at the last
+    position, speculative.py:188), None in greedy mode.
 
     input_kind "logits": probabilities are softmax(row / temperature), fused
     into the kernel; "probs": rows are probabilities (temperature unused).
@@ -117,8 +119,10 @@ def chain_verify(target: torch.Tensor, draft: Optional[torch.Tensor],
         if K > 0 and draft.stride(2) != 1:
             raise ValueError("draft's vocabulary dimension must be contiguous")
         _require_cuda("uniforms", uniforms, torch.float32, dev)
-        if tuple(uniforms.shape) != (B, K + 1):
-            raise ValueError(f"uniforms must be [B, K+1] = [{B}, {K + 1}]")
+        nu = K + 2 if mode == "python" else K + 1
+        if tuple(uniforms.shape) != (B, nu):
+            cols = "K+2" if mode == "python" else "K+1"
+            raise ValueError(f"uniforms must be [B, {cols}] = [{B}, {nu}] in {mode} mode")
         uniforms = uniforms.contiguous()
     if input_kind == "logits" and not temperature > 0.0:
         raise ValueError("temperature must be > 0")

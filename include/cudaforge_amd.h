@@ -69,11 +69,18 @@ int cfa_version(void);
  *   input_kind  CFA_INPUT_PROBS or CFA_INPUT_LOGITS (softmax of row / temperature)
  *   draft_tokens [B, K] int32 (token ids in [0, V); an id outside that range
  *            is never accepted and never dereferenced)
- *   uniforms [B, K+1] fp32 in [0, 1):
- *     CFA_MODE_CPP: the draws the reference takes from its mt19937, in order
- *       (one per acceptance test, then one for the resample / bonus draw);
- *     CFA_MODE_PYTHON: columns 0..K-1 replace torch.rand_like at
- *       speculative.py:161, column K drives the resample / bonus draw.
+ *   uniforms fp32 in [0, 1):
+ *     CFA_MODE_CPP: [B, K+1], the draws the reference takes from its mt19937,
+ *       in order (one per acceptance test, then one for the resample / bonus
+ *       draw);
+ *     CFA_MODE_PYTHON: [B, K+2]; columns 0..K-1 replace torch.rand_like at
+ *       speculative.py:161, column K drives the resample / bonus draw, column
+ *       K+1 the bonus that follows a rejection at the last position (there
+ *       the reference's num_accepted reaches K, so speculative.py:188 appends
+ *       a bonus after the resampled token).  Python-mode draws take the first
+ *       index whose sequential fp32 prefix sum exceeds u (never an index of
+ *       zero weight, as torch.multinomial), and past the end of the sums the
+ *       last index of positive weight.
  *   top_p    nucleus threshold of the python-mode bonus draw (speculative.py:67-81)
  *   eos_token_id  (< 0: none) CFA_MODE_CPP / GREEDY only
  *
@@ -81,8 +88,11 @@ int cfa_version(void);
  *   out_accept_len  [B]    accepted draft tokens (the reference's num_accepted;
  *                          python mode: the batch-wide count n, speculative.py:166)
  *   out_tokens      [B, K+1] accepted drafts then the final token, -1 padded
+ *                          (python mode, n = K - 1: the K - 1 drafts, the
+ *                          resampled token and the bonus)
  *   out_num_emitted [B]    valid entries of out_tokens
- *   out_final       [B]    final_token (resample or bonus draw)
+ *   out_final       [B]    final_token (resample or bonus draw; the last
+ *                          token emitted)
  *   out_eos         [B]    end_of_sequence
  *   out_target_probs / out_draft_probs (optional, may be NULL): contiguous
  *     [B,K+1,V] / [B,K,V] copies of the probabilities the decisions used.
@@ -117,7 +127,9 @@ int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t t_stride_k
  *     kernel ignores them.
  *   CFA_SAMPLE_FILTERED  keep p_i >= the top-p threshold of
  *     cudaforge/speculative.py:67-81 and >= the top_k-th largest p (top_k <= 0:
- *     no top-k), renormalise by the kept mass, then the same draw.
+ *     no top-k), renormalise by the kept mass, then the python-mode draw of
+ *     cfa_chain_verify (first i whose prefix sum exceeds u, never a token
+ *     that was filtered out).
  *   CFA_SAMPLE_GREEDY  the `draws` (<= 8) largest raw values, largest first,
  *     equal values by lower index (sampling.h:107-135 for draws = 1); no
  *     uniforms, no temperature.

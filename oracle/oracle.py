@@ -71,8 +71,11 @@ def lib() -> ctypes.CDLL:
         L.orc_verify_python.restype = ctypes.c_int
         L.orc_verify_python.argtypes = [
             ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
-            ctypes.c_int64, c_f32p, c_f32p, c_i32p, c_f32p, c_f32p, ctypes.c_float,
-            c_i32p, c_i32p]
+            ctypes.c_int64, c_f32p, c_f32p, c_i32p, c_f32p, ctypes.c_float,
+            c_i32p, c_i32p, c_i32p]
+        L.orc_py_sample_adjusted.restype = ctypes.c_int32
+        L.orc_py_sample_adjusted.argtypes = [c_f32p, c_f32p, ctypes.c_int64, ctypes.c_float,
+                                             ctypes.POINTER(ctypes.c_int)]
         L.orc_topp_keep.restype = None
         L.orc_topp_keep.argtypes = [c_f32p, ctypes.c_int64, ctypes.c_float, c_u8p]
         L.orc_sample_weights.restype = ctypes.c_int32
@@ -179,24 +182,39 @@ def softmax_rows(logits, temperature: float) -> np.ndarray:
     return p
 
 
-def python_verify(tprobs, dprobs, tokens, u_acc, u_fin, top_p: float):
-    """speculative.py:152-195 with fed uniforms. Returns (n, tokens [B,K+1])."""
+def python_verify(tprobs, dprobs, tokens, uniforms, top_p: float):
+    """speculative.py:152-195 with fed uniforms [B, K+2] (columns 0..K-1 the
+    acceptance draws, K the resample / bonus draw, K+1 the bonus after a
+    rejection at the last position).  Returns (n, num_emitted, tokens [B,K+1]):
+    n accepted drafts (batch-wide), num_emitted tokens per row (the
+    reference's num_accepted), -1 padded tokens."""
     t, d = _f32(tprobs), _f32(dprobs)
     tok = _i32(tokens)
-    ua, uf = _f32(u_acc), _f32(u_fin)
+    U = _f32(uniforms)
     B, K1, V = t.shape
     K = K1 - 1
+    assert U.shape == (B, K + 2), "python-mode uniforms are [B, K+2]"
     n = ctypes.c_int32(0)
+    ne = ctypes.c_int32(0)
     out = np.zeros((B, K + 1), np.int32)
     if K == 0:
         d = np.zeros((B, 1, V), np.float32)
     rc = lib().orc_verify_python(B, K, V, V, (K + 1) * V, max(K, 1) * V, _p(t, c_f32p),
-                                 _p(d, c_f32p), _p(tok, c_i32p), _p(ua, c_f32p),
-                                 _p(uf, c_f32p), np.float32(top_p), ctypes.byref(n),
+                                 _p(d, c_f32p), _p(tok, c_i32p), _p(U, c_f32p),
+                                 np.float32(top_p), ctypes.byref(n), ctypes.byref(ne),
                                  _p(out, c_i32p))
     if rc != 0:
         raise ValueError("python_verify: token id out of range")
-    return int(n.value), out
+    return int(n.value), int(ne.value), out
+
+
+def py_sample_adjusted(target_p, draft_q, u: float) -> tuple[int, bool]:
+    """The python-mode residual draw (speculative.py:171-182)."""
+    t, d = _f32(target_p), _f32(draft_q)
+    fb = ctypes.c_int(0)
+    tok = lib().orc_py_sample_adjusted(_p(t, c_f32p), _p(d, c_f32p), t.size, np.float32(u),
+                                       ctypes.byref(fb))
+    return int(tok), bool(fb.value)
 
 
 def topp_keep(p, top_p: float) -> np.ndarray:
@@ -219,7 +237,7 @@ def topk_keep(p, top_k: int) -> np.ndarray:
 
 def sample_filtered(p, r: float, top_p: float, top_k: int) -> int:
     """Keep rule (top-p of speculative.py:67-81 and top-k), renormalise by
-    the sequential fp32 kept mass, sequential fp32 inverse CDF."""
+    the sequential fp32 kept mass, python-mode inverse CDF (sample_weights)."""
     a = _f32(p).ravel()
     keep = topp_keep(a, top_p) & topk_keep(a, top_k)
     return sample_weights(np.where(keep, a, np.float32(0)).astype(np.float32), r)
@@ -237,6 +255,9 @@ def topk_greedy(rows, k: int) -> np.ndarray:
 
 
 def sample_weights(w, r: float) -> int:
+    """Python-mode draw from non-negative weights: normalise by the sequential
+    fp32 sum, then the first index whose prefix sum exceeds r (never a
+    zero-weight index; past the end of the sums, the last positive one)."""
     a = _f32(w)
     return int(lib().orc_sample_weights(_p(a, c_f32p), a.size, np.float32(r)))
 

@@ -230,26 +230,79 @@ void orc_topp_keep(const float *p, int64_t V, float top_p, uint8_t *keep) {
   free(s);
 }
 
-int32_t orc_sample_weights(const float *w, int64_t V, float r) {
+/* Python-mode inverse CDF: the first i whose sequential fp32 prefix sum
+ * exceeds u (and is at least FLT_MIN), so that u = 0 never selects a
+ * zero-weight entry; when the prefix sums fall short of u (they end a few
+ * ulps below 1), the last entry of positive weight.  torch.multinomial, which
+ * the python engine calls (speculative.py:84, :182), never returns a
+ * zero-weight index either; its draws are equal in distribution to these. */
+static int32_t py_inverse_cdf(const float *x, int64_t V, float u) {
+  float cumulative = 0.0f;
+  for (int64_t i = 0; i < V; ++i) {
+    cumulative += x[i];
+    if (cumulative > u && cumulative >= FLT_MIN) return (int32_t)i;
+  }
+  for (int64_t i = V - 1; i >= 0; --i)
+    if (x[i] > 0.0f) return (int32_t)i;
+  return (int32_t)(V - 1);
+}
+
+int32_t orc_sample_weights(const float *w, int64_t V, float u) {
   float sum = orc_seq_sum(w, V);
-  if (!(sum > 0.0f)) return orc_sample_from_distribution(w, V, r);
+  if (!(sum > 0.0f)) return py_inverse_cdf(w, V, u);
   float *x = (float *)malloc((size_t)V * sizeof(float));
   for (int64_t i = 0; i < V; ++i) x[i] = w[i] / sum;
-  int32_t t = orc_sample_from_distribution(x, V, r);
+  int32_t t = py_inverse_cdf(x, V, u);
   free(x);
   return t;
+}
+
+/* speculative.py:171-182: residual clamp(t - d, 0), target row when its sum
+ * is <= 1e-6 (the sum formed sequentially in fp32, as speculative.cpp:30-37
+ * does), then a python-mode draw from the normalised weights. */
+int32_t orc_py_sample_adjusted(const float *target_p, const float *draft_q,
+                               int64_t V, float u, int *fallback) {
+  float *adjusted = (float *)malloc((size_t)V * sizeof(float));
+  float sum = 0.0f;
+  for (int64_t i = 0; i < V; ++i) {
+    adjusted[i] = relu_std_max(target_p[i] - draft_q[i]);
+    sum += adjusted[i];
+  }
+  int32_t tok;
+  if (sum <= 1e-6f) {
+    if (fallback) *fallback = 1;
+    tok = py_inverse_cdf(target_p, V, u);
+  } else {
+    if (fallback) *fallback = 0;
+    for (int64_t i = 0; i < V; ++i) adjusted[i] /= sum;
+    tok = py_inverse_cdf(adjusted, V, u);
+  }
+  free(adjusted);
+  return tok;
+}
+
+/* speculative.py:188-195: the top-p filtered bonus draw from target row K. */
+static int32_t py_bonus(const float *pk, int64_t V, float top_p, float u,
+                        uint8_t *keep, float *w) {
+  orc_topp_keep(pk, V, top_p, keep);
+  for (int64_t i = 0; i < V; ++i) w[i] = keep[i] ? pk[i] : 0.0f;
+  return orc_sample_weights(w, V, u);
 }
 
 /* speculative.py:155-195.  The acceptance test of :161-166 is restated with
  * the fed uniform in place of rand_like: ratio = min(1, q / (p + 1e-8)) in
  * fp32 and accept iff every row has u < ratio.  The resample (:171-182) and
- * the bonus (:188-195) draw with an inverse CDF on Ufin in place of
- * torch.multinomial (equal in distribution, not bit-for-bit). */
+ * the bonus (:188-195) draw with the python-mode inverse CDF on fed uniforms
+ * in place of torch.multinomial (equal in distribution, not bit-for-bit).
+ * A rejection at the last position (n = K - 1) brings num_accepted to K, so
+ * the reference's `num_accepted == self.k` branch (:188) appends the bonus
+ * after the resampled token as well. */
 int orc_verify_python(int B, int K, int64_t V, int64_t ld, int64_t tsb,
                       int64_t dsb, const float *tprobs, const float *dprobs,
-                      const int32_t *tokens, const float *Uacc,
-                      const float *Ufin, float top_p, int32_t *out_n,
+                      const int32_t *tokens, const float *U, float top_p,
+                      int32_t *out_n, int32_t *out_num_emitted,
                       int32_t *out_tokens) {
+  const int us = K + 2;
   int n = K;
   for (int b = 0; b < B; ++b) {
     int nb = K;
@@ -261,31 +314,30 @@ int orc_verify_python(int B, int K, int64_t V, int64_t ld, int64_t tsb,
       float den = pd + 1e-8f;
       float ratio = qt / den;
       if (ratio > 1.0f) ratio = 1.0f;
-      if (!(Uacc[(int64_t)b * K + i] < ratio)) {
+      if (!(U[(int64_t)b * us + i] < ratio)) {
         nb = i;
         break;
       }
     }
     if (nb < n) n = nb;
   }
+  const int extra = (K > 0 && n == K - 1) ? 1 : 0;
   *out_n = n;
+  *out_num_emitted = n + 1 + extra;
   uint8_t *keep = (uint8_t *)malloc((size_t)V);
   float *w = (float *)malloc((size_t)V * sizeof(float));
   for (int b = 0; b < B; ++b) {
     int32_t *row = out_tokens + (int64_t)b * (K + 1);
+    const float *Ub = U + (int64_t)b * us;
+    const float *pk = tprobs + b * tsb + (int64_t)K * ld;
     for (int j = 0; j <= K; ++j) row[j] = -1;
     for (int j = 0; j < n; ++j) row[j] = tokens[(int64_t)b * K + j];
-    int32_t fin;
-    if (n < K) {
-      fin = orc_sample_adjusted(tprobs + b * tsb + n * ld,
-                                dprobs + b * dsb + n * ld, V, Ufin[b], NULL);
-    } else {
-      const float *pk = tprobs + b * tsb + (int64_t)K * ld;
-      orc_topp_keep(pk, V, top_p, keep);
-      for (int64_t i = 0; i < V; ++i) w[i] = keep[i] ? pk[i] : 0.0f;
-      fin = orc_sample_weights(w, V, Ufin[b]);
-    }
-    row[n] = fin;
+    if (n < K)
+      row[n] = orc_py_sample_adjusted(tprobs + b * tsb + n * ld,
+                                      dprobs + b * dsb + n * ld, V, Ub[K], NULL);
+    else
+      row[n] = py_bonus(pk, V, top_p, Ub[K], keep, w);
+    if (extra) row[n + 1] = py_bonus(pk, V, top_p, Ub[K + 1], keep, w);
   }
   free(keep);
   free(w);

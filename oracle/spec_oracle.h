@@ -77,17 +77,25 @@ void orc_softmax_rows(const float *x, float *p, int64_t rows, int64_t V,
                       int64_t ld, float temperature);
 
 /* python-mode semantics of speculative.py:152-195 over a batch with fed
- * uniforms.  Uacc is [B,K] (rand_like at :161), Ufin is [B] (the draw used
- * by the resample at :182 or the bonus at :189).  bonus_probs is the
- * temperature softmax of target_candidate_logits[:, -1] (row K); top-p
- * filtering (:67-81) is applied to it before the bonus draw.
- * out_tokens is [B, K+1]; *out_n receives the batch accept count n
- * (accepted drafts; num_accepted of the reference is n + 1). */
+ * uniforms U [B, K+2]: columns 0..K-1 replace rand_like at :161, column K
+ * drives the resample (:182) or the bonus draw (:189), column K+1 the bonus
+ * that follows a rejection at the last position (n = K - 1 makes the
+ * reference's num_accepted equal K, so :188 appends a bonus too).  The bonus
+ * is drawn from row K after the top-p filter of :67-81.  out_tokens is
+ * [B, K+1], -1 padded; *out_n receives the batch accept count n (accepted
+ * drafts) and *out_num_emitted the tokens per row (the reference's
+ * num_accepted: n + 1, or K + 1 after a rejection at K - 1). */
 int orc_verify_python(int B, int K, int64_t V, int64_t ld, int64_t tsb,
                       int64_t dsb, const float *tprobs, const float *dprobs,
-                      const int32_t *tokens, const float *Uacc,
-                      const float *Ufin, float top_p, int32_t *out_n,
+                      const int32_t *tokens, const float *U, float top_p,
+                      int32_t *out_n, int32_t *out_num_emitted,
                       int32_t *out_tokens);
+
+/* The python-mode residual draw (speculative.py:171-182): max(0, t - d),
+ * sequential fp32 sum, the target row when the sum is <= 1e-6, otherwise the
+ * normalised residual; drawn with the python-mode inverse CDF below. */
+int32_t orc_py_sample_adjusted(const float *target_p, const float *draft_q,
+                               int64_t V, float u, int *fallback);
 
 /* Top-p keep set (speculative.py:67-81) restated without a sort: token j is
  * kept iff the probability mass strictly above p_j is <= top_p (fp64 sums).
@@ -95,9 +103,12 @@ int orc_verify_python(int B, int K, int64_t V, int64_t ld, int64_t tsb,
  * tied probabilities are kept or dropped together. */
 void orc_topp_keep(const float *p, int64_t V, float top_p, uint8_t *keep);
 
-/* Draw from unnormalised non-negative weights: sequential fp32 sum,
- * per-element division, sequential inverse CDF (the python-mode bonus). */
-int32_t orc_sample_weights(const float *w, int64_t V, float r);
+/* Python-mode draw from unnormalised non-negative weights (the bonus and the
+ * filtered sampler): sequential fp32 sum, per-element division, then the
+ * first i whose sequential fp32 prefix sum exceeds u (and is >= FLT_MIN);
+ * past the end of the sums, the last index of positive weight.  A
+ * zero-weight index is never returned (as torch.multinomial). */
+int32_t orc_sample_weights(const float *w, int64_t V, float u);
 
 /* Tree verification (multi-candidate rejection sampling), cpp semantics.
  * parent[0] = -1, parent[i] < i.  Row n of tprobs/dprobs is node n's target

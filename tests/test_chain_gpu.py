@@ -91,11 +91,21 @@ def _to_dev(device, *arrays):
     return [torch.from_numpy(np.ascontiguousarray(a)).to(device) for a in arrays]
 
 
+def _py_uniforms(U, seed=0):
+    """[B, K+1] uniforms widened to python mode's [B, K+2] (one more column
+    for the bonus that follows a rejection at the last position)."""
+    extra = np.random.default_rng(seed).random((U.shape[0], 1)).astype(np.float32)
+    return np.ascontiguousarray(np.concatenate([U, extra], axis=1))
+
+
 def _check_vs_oracle(out, tp, dp, tok, U, eos, mode, top_p=1.0):
     if mode == "python":
-        n, toks = O.python_verify(tp, dp, tok, U[:, :-1], U[:, -1], top_p)
+        n, ne, toks = O.python_verify(tp, dp, tok, U, top_p)
         assert (out.accept_len.cpu().numpy() == n).all()
+        assert (out.num_emitted.cpu().numpy() == ne).all()
         np.testing.assert_array_equal(out.tokens.cpu().numpy(), toks)
+        last = toks[np.arange(toks.shape[0]), ne - 1]
+        np.testing.assert_array_equal(out.final.cpu().numpy(), last)
         return
     want = O.chain_verify(tp, dp, tok, U, eos=eos, greedy=(mode == "greedy"))
     np.testing.assert_array_equal(out.accept_len.cpu().numpy(), want["accept_len"])
@@ -116,6 +126,8 @@ def _softmax64(x, T):
 def test_logits_path_matches_oracle(device, mode, B, K, V):
     T = 0.7
     tl, dl, tok, U = c2_inputs(seed=B * 1000 + K * 10 + V % 97, B=B, K=K, V=V, temperature=T)
+    if mode == "python":
+        U = _py_uniforms(U, seed=B + K)
     t_d, d_d, tok_d, U_d = _to_dev(device, tl, dl, tok, U)
     out = chain_verify(t_d, d_d, tok_d, U_d, input_kind="logits", temperature=T, mode=mode,
                        top_p=0.9, return_probs=True)
@@ -136,7 +148,7 @@ def test_logits_path_matches_oracle(device, mode, B, K, V):
 def test_probs_path_matches_oracle(device, mode):
     tok, d, t, eos = chain_case(21, 48, 6, 3000, sigma=3.0, eos_bias=True)
     rng = np.random.default_rng(4)
-    U = rng.random((48, 7)).astype(np.float32)
+    U = rng.random((48, 8 if mode == "python" else 7)).astype(np.float32)
     t_d, d_d, tok_d, U_d = _to_dev(device, t, d, tok, U)
     e = eos if mode != "python" else -1
     out = chain_verify(t_d, d_d, tok_d, U_d, input_kind="probs", mode=mode, eos_token_id=e,

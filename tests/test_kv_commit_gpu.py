@@ -28,8 +28,10 @@ def _random_paths(rng, parents, B, maxlen):
     return paths, lens
 
 
-@pytest.mark.parametrize("layers,bs", [(4, 16), (2, 32)])
+@pytest.mark.parametrize("layers,bs", [(32, 16), (4, 16), (2, 32)])
 def test_commit_matches_oracle(device, layers, bs):
+    """(32, 16) is the full tree-commit shape: B = 32, 63-node tree, 32 layers
+    x 8 KV heads x 128, pages of 16."""
     rng = np.random.default_rng(layers * 10 + bs)
     B, N, Hkv, D = 32, 63, 8, 128
     parents = T.binary_tree_parents(N)

@@ -234,8 +234,8 @@ def test_python_mode_lockstep_invariant():
     B, K, V = 6, 5, 50
     tok, d, t, _ = chain_case(77, B, K, V)
     ua = rng.random((B, K)).astype(np.float32) * 0.6
-    uf = rng.random(B).astype(np.float32)
-    n, toks = O.python_verify(t, d, tok, ua, uf, 0.9)
+    U = np.concatenate([ua, rng.random((B, 2)).astype(np.float32)], axis=1)
+    n, ne, toks = O.python_verify(t, d, tok, U, 0.9)
     # n = min over rows of each row's first failure of u < min(1, q/(p+1e-8))
     per_row = []
     for b in range(B):
@@ -250,4 +250,6 @@ def test_python_mode_lockstep_invariant():
         per_row.append(nb)
     assert n == min(per_row)
     np.testing.assert_array_equal(toks[:, :n], tok[:, :n])
-    assert (toks[:, n] >= 0).all() and (toks[:, n + 1:] == -1).all()
+    extra = 1 if n == K - 1 else 0
+    assert ne == n + 1 + extra
+    assert (toks[:, n:ne] >= 0).all() and (toks[:, ne:] == -1).all()

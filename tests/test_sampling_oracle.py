@@ -20,9 +20,13 @@ def test_sample_filtered_known_answers():
     # top-k 1 keeps token 1 only: every u > 0 selects it
     for u in (1e-7, 0.3, 0.999):
         assert O.sample_filtered(p, u, 1.0, 1) == 1
-    # u = 0 meets `u <= cumulative` at index 0 whatever its mass (the rule of
-    # speculative.cpp:17-22 and sampling.h:170-182)
-    assert O.sample_filtered(p, 0.0, 1.0, 1) == 0
+    # the python-mode draw takes the first prefix sum that EXCEEDS u: u = 0
+    # selects the first kept token, never a filtered one (torch.multinomial
+    # never returns a zero-weight index)
+    assert O.sample_filtered(p, 0.0, 1.0, 1) == 1
+    # past the end of the prefix sums: the last kept token
+    assert O.sample_filtered(p, 1.0, 1.0, 1) == 1
+    assert O.sample_filtered(p, 1.0, 1.0, 2) == 3
     # top-k 2 keeps {1, 2, 3} with mass 0.8: normalised 0.5, 0.25, 0.25
     assert O.sample_filtered(p, 0.49, 1.0, 2) == 1
     assert O.sample_filtered(p, 0.51, 1.0, 2) == 2
@@ -41,9 +45,10 @@ def test_sample_filtered_top_p_matches_python_verify_bonus():
     for top_p in (0.3, 0.9):
         p = rng.dirichlet(np.ones(64)).astype(np.float32)[None, None, :]
         for u in rng.random(10).astype(np.float32):
-            _, toks = O.python_verify(p, np.zeros((1, 0, 64), np.float32),
-                                      np.zeros((1, 0), np.int32), np.zeros((1, 0), np.float32),
-                                      np.array([u], np.float32), top_p)
+            _, ne, toks = O.python_verify(p, np.zeros((1, 0, 64), np.float32),
+                                          np.zeros((1, 0), np.int32),
+                                          np.array([[u, 0.5]], np.float32), top_p)
+            assert ne == 1
             assert O.sample_filtered(p[0, 0], u, top_p, 0) == toks[0, 0]
 
 

@@ -180,6 +180,75 @@ def test_target_tree_forward_vs_fp32(device):
     assert err <= 3e-2 * max(1.0, scale), (err, scale)
 
 
+def test_target_tree_forward_8b_width_vs_fp32(device):
+    """The target's tree forward at the 8B layer width (d 4096, GQA 32/8,
+    head_dim 128, FFN 14336, V 128256) with 2 of its 32 layers, over the full
+    63-node tree, against the fp32 forward."""
+    shape = LlamaShape(2, 4096, 32, 8, 128, 14336, 128256)
+    B, ctx0, N = 2, 130, 63
+    tm = TargetModel(shape, device, seed=13)
+    dm = DraftModel(LlamaShape(1, 128, 4, 2, 64, 256, 128256), device, B,
+                    max_slots=ctx0 + 64 + 64)
+    sp = TreeSpeculator(tm, dm, B, ctx0, depth=5, temperature=1.0, max_steps=8, seed=14)
+    sp.ctx = [130, 77]
+    for b in range(B):
+        sp.kv.truncate_sequence(b, sp.ctx[b])
+    base = torch.tensor(sp.ctx, dtype=torch.int32, device=device)
+    tokens = torch.randint(0, shape.vocab, (B, N), device=device, dtype=torch.int32)
+    for b in range(B):
+        sp.kv.append_tokens(b, N)
+    desc = sp.kv.prepare_batch_metadata(list(range(B)))
+    pos = base[:, None] + sp.depths[None, :]
+    got = tm.forward_tree(tokens, pos, sp.kv, desc.block_tables, base, sp.masks, max(sp.ctx) + N)
+    torch.cuda.synchronize()
+    got = got.float()
+    want = _ref_forward(tm, tokens, pos, sp.kv, desc.block_tables, base, N)
+    torch.cuda.synchronize()
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    assert err <= 3e-2 * max(1.0, scale), (err, scale)
+
+
+def _slots(pool, table, n):
+    """Slots [0, n) of one sequence of a paged pool [blocks, L, Hkv, bs, D]
+    as [L, Hkv, n, D]."""
+    pages = pool[table.long()]
+    P, L, H, bs, D = pages.shape
+    return pages.permute(1, 2, 0, 3, 4).reshape(L, H, P * bs, D)[:, :, :n]
+
+
+def test_full_8b_step_bookkeeping(device):
+    """Two verify steps of the full workload (32-layer 8B-shape W4A16 target,
+    1B-shape draft, B = 8, context 2048, 63-node tree): paths, context growth,
+    page tables, emitted ids and the draft cache's commit."""
+    from cudaforge_amd.spec_step import DRAFT_1B, TARGET_8B
+
+    B, ctx0 = 8, 2048
+    tm = TargetModel(TARGET_8B, device, seed=0)
+    dm = DraftModel(DRAFT_1B, device, B, max_slots=ctx0 + 64 + 8 * 4)
+    sp = TreeSpeculator(tm, dm, B, ctx0, depth=5, temperature=1.0, mode="cpp", max_steps=4,
+                        use_graphs=True)
+    for _ in range(2):
+        ctx_before = list(sp.ctx)
+        dk_before = dm.k_pool.clone()
+        r = sp.step()
+        torch.cuda.synchronize()
+        for b in range(B):
+            L = r.path_len[b]
+            assert 1 <= L <= sp.depth + 1
+            assert sp.ctx[b] == ctx_before[b] + L
+            assert sp.kv.context_length(b) == sp.ctx[b]
+            assert len(sp.kv.get_block_table(b)) == -(-sp.ctx[b] // 16)
+            assert len(r.emitted[b]) == L and r.emitted[b][-1] == r.final[b]
+            assert all(0 <= t < TARGET_8B.vocab for t in r.emitted[b])
+            # the draft cache below the old context is untouched by the step
+            assert torch.equal(_slots(dk_before, dm.block_tables[b], ctx_before[b]),
+                               _slots(dm.k_pool, dm.block_tables[b], ctx_before[b]))
+        assert sp.root.tolist() == r.final
+    del sp, tm, dm
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("mode", ["cpp", "greedy"])
 def test_steps_bookkeeping(device, mode):
     B, ctx0 = 4, 40

@@ -112,6 +112,39 @@ def test_tree_logits_c4_shape(device):
     _check(c, parents, tp, dp, tok, U, -1, False)
 
 
+def test_tree_logits_c4_full_batch(device):
+    """The whole tree-acceptance workload: B = 32 sequences, 63-node binary
+    tree, V = 128256, T = 0.7, logits ~ 2 N(0,1) with N(0, 0.5) draft noise,
+    node tokens drawn from the parent's draft softmax (inputs generated on the
+    device).  Every sequence's path, tokens and final draw vs the oracle fed
+    the kernel's probabilities; visited rows' softmax within 1e-6."""
+    parents = T.binary_tree_parents(63)
+    B, N, V, Tm = 32, 63, 128256, 0.7
+    g = torch.Generator(device=device).manual_seed(2024)
+    tl = 2.0 * torch.randn(B, N, V, device=device, generator=g)
+    dl = tl + 0.5 * torch.randn(B, N, V, device=device, generator=g)
+    par = torch.from_numpy(parents).to(device).long()
+    rows = torch.softmax(dl[:, par[1:]] / Tm, dim=-1).reshape(-1, V)
+    tok = torch.zeros(B, N, dtype=torch.int32, device=device)
+    tok[:, 1:] = torch.multinomial(rows, 1, generator=g).view(B, N - 1).int()
+    del rows
+    U = torch.rand(B, N + 1, device=device, generator=g)
+    p_d = torch.from_numpy(parents).to(device)
+    out = tree_verify(tl, dl, p_d, tok, U, input_kind="logits", temperature=Tm, mode="cpp",
+                      return_probs=True)
+    torch.cuda.synchronize()
+    c = _cpu(out)
+    assert c.status.tolist() == [0] * B
+    tp, dp = out.target_probs.cpu().numpy(), out.draft_probs.cpu().numpy()
+    tl_c = tl.cpu().numpy()
+    del out, tl, dl
+    for b in range(B):
+        for n in c.path[b][: int(c.path_len[b])].tolist():
+            ref = _softmax64(tl_c[b, n].astype(np.float64) / Tm)
+            assert np.abs(tp[b, n] - ref).max() <= 1e-6
+    _check(c, parents, tp, dp, tok.cpu().numpy(), U.cpu().numpy(), -1, False)
+
+
 def test_one_child_chain_equals_chain_verify(device):
     """A chain tree (parent = i - 1) is exactly verify_candidates."""
     B, K, V = 16, 6, 5000
