@@ -107,6 +107,11 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _i64, _p, _i64, _i64, _i, _p, _p, _i, _i, _i, _f, _f, _i, _i32,
          _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p],
     ),
+    "cfa_chain_verify_noalloc": (
+        _i,
+        [_p, _i64, _i64, _p, _i64, _i64, _i, _p, _p, _i, _i, _i, _f, _f, _i, _i32,
+         _p, _p, _p, _p, _p, _p, _p, _p],
+    ),
     "cfa_sample_workspace_size": (_sz, [_i, _i, _i, _i]),
     "cfa_sample": (
         _i, [_p, _i64, _i, _i, _i, _i, _f, _i, _f, _i, _p, _p, _p, _p, _sz, _p]),

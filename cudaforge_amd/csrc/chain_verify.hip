@@ -20,6 +20,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "abi_internal.hpp"
 #include "dist.hpp"
@@ -1531,13 +1532,77 @@ extern "C" int cfa_sample(const float *rows, int64_t row_stride, int input_kind,
   a.top_p = (mode == CFA_SAMPLE_FILTERED) ? top_p : 1.0f;
   a.top_k = (mode == CFA_SAMPLE_FILTERED) ? top_k : 0;
   const WsLayout L = ws_layout(B, 0, V, chain_mode);
-  int32_t *scratch = (int32_t *)((char *)workspace + L.total);
+  char *tail = (char *)workspace + L.total;
   const size_t ib = align_up((size_t)B * sizeof(int32_t));
   a.out_tokens = out_tokens;
-  a.out_final = (int32_t *)((char *)scratch);
-  a.out_accept_len = (int32_t *)((char *)scratch + ib);
-  a.out_num_emitted = (int32_t *)((char *)scratch + 2 * ib);
+  a.out_final = (int32_t *)tail;
+  a.out_accept_len = (int32_t *)(tail + ib);
+  a.out_num_emitted = (int32_t *)(tail + 2 * ib);
   a.out_eos = a.out_accept_len;  // written after out_accept_len, never read
   const bool vec = (V % 4 == 0) && (row_stride % 4 == 0) && (((uintptr_t)rows & 15) == 0);
   return run_pipeline(a, vec, workspace, st, out_probs, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free chain verification.  Its workspace is a file-scope device
+// array, so a caller that cannot allocate (HIP graph capture, a serving loop
+// that forbids allocation) passes only inputs and outputs.  Every GPU the
+// library runs on holds its own copy of the array until the process ends;
+// calls on one GPU share it, so calls that overlap on one GPU (different
+// streams, or host threads) race.  Nothing in it has to start at zero: every
+// region the pipeline reads is written earlier in the same call.
+// ---------------------------------------------------------------------------
+
+constexpr size_t kScratchBytes = size_t(32) << 20;  // 32 MiB: B = 64, K = 8, V = 128256 needs 18.7
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+}  // namespace
+
+// The current device's address of `scratch`, looked up once per device (the
+// host-side name of the array is not a device address).
+static int scratch_ptr(void **out) {
+  using namespace cfa::abi;
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail_hip(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail_arg("device ordinal out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail_code(CFA_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return CFA_OK;
+}
+
+extern "C" int cfa_chain_verify_noalloc(const float *target, int64_t t_stride_b,
+                                        int64_t t_stride_k, const float *draft,
+                                        int64_t d_stride_b, int64_t d_stride_k, int input_kind,
+                                        const int32_t *draft_tokens, const float *uniforms, int B,
+                                        int K, int V, float temperature, float top_p, int mode,
+                                        int32_t eos_token_id, int32_t *out_accept_len,
+                                        int32_t *out_tokens, int32_t *out_num_emitted,
+                                        int32_t *out_final, int32_t *out_eos,
+                                        float *out_target_probs, float *out_draft_probs,
+                                        void *stream) {
+  using namespace cfa::abi;
+  clear_error();
+  const size_t need = cfa_chain_verify_workspace_size(B, K, V, input_kind, mode);
+  if (need > kScratchBytes)
+    return fail_arg("cfa_chain_verify_noalloc: this shape needs more than the 32 MiB static "
+                    "scratch (see cfa_chain_verify_workspace_size); use cfa_chain_verify with "
+                    "a workspace");
+  void *ws = nullptr;
+  if (const int rc = scratch_ptr(&ws)) return rc;
+  return cfa_chain_verify(target, t_stride_b, t_stride_k, draft, d_stride_b, d_stride_k,
+                          input_kind, draft_tokens, uniforms, B, K, V, temperature, top_p, mode,
+                          eos_token_id, out_accept_len, out_tokens, out_num_emitted, out_final,
+                          out_eos, out_target_probs, out_draft_probs, ws, kScratchBytes, stream);
 }

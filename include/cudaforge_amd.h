@@ -6,7 +6,8 @@
  * buffers are HIP device addresses (e.g. torch.Tensor.data_ptr()); `stream` is
  * a hipStream_t (NULL = default stream) and all device work is enqueued on it
  * in order, without host synchronisation.  The library allocates no device
- * memory: scratch space is the caller's `workspace`.
+ * memory: scratch space is the caller's `workspace` (cfa_chain_verify_noalloc
+ * uses a static device array of the library instead).
  *
  * Errors: every function returns CFA_OK (0) or a negative code; the message
  * of the calling thread's last failure is available from cfa_last_error().
@@ -110,6 +111,23 @@ int cfa_chain_verify(const float *target, int64_t t_stride_b, int64_t t_stride_k
                      int32_t *out_num_emitted, int32_t *out_final, int32_t *out_eos,
                      float *out_target_probs, float *out_draft_probs, void *workspace,
                      size_t workspace_bytes, void *stream);
+
+/* cfa_chain_verify without a workspace argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, serving loops or harnesses that forbid hipMalloc).  Its scratch is
+ * a static 32 MiB device array inside the library (one per GPU, held until
+ * the process ends); shapes whose cfa_chain_verify_workspace_size exceeds
+ * 32 MiB are refused with CFA_ERR_ARG (B = 64, K = 8, V = 128256 needs
+ * 18.7 MiB).  It allocates nothing.  Every call on one GPU shares that array,
+ * so calls that overlap on one GPU (other streams, other host threads) race;
+ * serialise them.  Arguments and results are those of cfa_chain_verify. */
+int cfa_chain_verify_noalloc(const float *target, int64_t t_stride_b, int64_t t_stride_k,
+                             const float *draft, int64_t d_stride_b, int64_t d_stride_k,
+                             int input_kind, const int32_t *draft_tokens, const float *uniforms,
+                             int B, int K, int V, float temperature, float top_p, int mode,
+                             int32_t eos_token_id, int32_t *out_accept_len, int32_t *out_tokens,
+                             int32_t *out_num_emitted, int32_t *out_final, int32_t *out_eos,
+                             float *out_target_probs, float *out_draft_probs, void *stream);
 
 /* ---------------------------------------------------------------------------
  * Token sampler: plain decode and draft-tree expansion.
