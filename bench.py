@@ -34,10 +34,31 @@ SIGMA, NOISE = 2.0, 0.5
 NSETS = 4
 # algorithmic bytes of one step: target [B,K+1,V] + draft [B,K,V] logits, read once
 ALG_BYTES = B * (2 * K + 1) * V * 4
-# HBM bytes per chain_stats launch: reads from rocprofv3 --pmc TCC_EA0_RDREQ_{32B,64B,128B}
-# (request-size weighted, exact on a plain copy) plus WRITE_SIZE
-# (profiles/hbm_traffic_per_dispatch.md)
-STATS_TRAFFIC_BYTES = 576_649_216
+# per-dispatch HBM traffic measured with rocprofv3 --pmc for this build
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic_per_dispatch.md")
+
+
+def traffic_from_profile(kernel: str):
+    """HBM bytes (read + written) per dispatch of `kernel` from the counter
+    table in profiles/hbm_traffic_per_dispatch.md (columns "HBM bytes read"
+    and "HBM bytes written"); None when the table has no such row."""
+    try:
+        with open(TRAFFIC_TABLE) as f:
+            lines = [ln.strip() for ln in f if ln.strip().startswith("|")]
+    except OSError:
+        return None
+    if not lines:
+        return None
+    head = [c.strip() for c in lines[0].strip("|").split("|")]
+    try:
+        ir, iw = head.index("HBM bytes read"), head.index("HBM bytes written")
+    except ValueError:
+        return None
+    for ln in lines[2:]:
+        cells = [c.strip() for c in ln.strip("|").split("|")]
+        if cells and cells[0].strip("`") == kernel:
+            return int(cells[ir].replace(",", "")) + int(cells[iw].replace(",", ""))
+    return None
 
 
 def make_inputs(dev, seed):
@@ -53,30 +74,150 @@ def make_inputs(dev, seed):
     return tl.contiguous(), dl.contiguous(), tok, U
 
 
-def cpu_baseline(tl, dl, tok, U, budget_s=12.0):
-    """The oracle (plain C restatement of speculative.cpp, OpenMP over rows)
-    on the host cores: softmax of both logit tensors, then per-row
-    verification; repeated on the same batch until ~budget_s elapse."""
-    import numpy as np
-    from oracle import oracle as O
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or len(os.sched_getaffinity(0))
-    os.environ["OMP_NUM_THREADS"] = str(threads)
-    t, d = tl.cpu().numpy(), dl.cpu().numpy()
-    tk, u = tok.cpu().numpy(), U.cpu().numpy()
+
+def _timed(fn, budget_s):
+    """Call fn() (returns tokens emitted) until budget_s elapse; (passes,
+    tokens, seconds)."""
     passes, emitted, t0 = 0, 0, time.perf_counter()
     while True:
-        tp = O.softmax_rows(t, T)
-        dp = O.softmax_rows(d, T)
-        out = O.chain_verify(tp, dp, tk, u)
-        emitted += int(out["num_emitted"].sum())
+        emitted += fn()
         passes += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
-            break
-    return {"value": emitted / el, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{passes} full passes over one B=64,K=8,V=128256 batch "
-                      f"(oracle softmax + per-row verify, {el:.1f} s)"}
+            return passes, emitted, el
+
+
+def cpu_baseline(tl, dl, tok, budget_s=6.0):
+    """The chain-acceptance workload on the host cores, from the same logits:
+    torch-CPU softmax of the target and draft windows (what the reference's
+    python engine runs, speculative.py:118, :145), then the reference's own
+    SpeculativeEngine::verify_candidates (csrc/src/scheduler/speculative.cpp,
+    compiled from source into oracle/_ref) once per sequence on one engine,
+    as its pybind binding serves it.  Timed with every host thread and with
+    one; the build's C port of the same rules (OpenMP over rows) beside it.
+    Without oracle/_ref the port is the reported figure."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+
+    threads = len(os.sched_getaffinity(0))
+    t_c, d_c = tl.cpu(), dl.cpu()
+    tk = tok.cpu().numpy()
+    ref = O.ref_lib()
+
+    def softmax():
+        return (torch.softmax(t_c / T, dim=-1).numpy(), torch.softmax(d_c / T, dim=-1).numpy())
+
+    def ref_pass():
+        tp, dp = softmax()
+        out = O.ref_verify(1234, tk, dp, tp, -1)
+        return int(out["num_accepted"].sum()) + B  # accepted drafts + one final token each
+
+    def port_pass():
+        tp = O.softmax_rows(t_c.numpy(), T)
+        dp = O.softmax_rows(d_c.numpy(), T)
+        u = np.random.default_rng(0).random((B, K + 1)).astype(np.float32)
+        return int(O.chain_verify(tp, dp, tk, u)["num_emitted"].sum())
+
+    sample = "passes over one B=64,K=8,V=128256 logit batch (softmax of both windows + verify)"
+    res = {"cpu_model": _cpu_model(), "threads_available": threads}
+    old = torch.get_num_threads()
+    try:
+        for label, fn in (("reference", ref_pass), ("port", port_pass)):
+            if label == "reference" and ref is None:
+                continue
+            for nt in (threads, 1):
+                torch.set_num_threads(nt)
+                O.set_threads(nt)
+                passes, emitted, el = _timed(fn, budget_s if nt > 1 else budget_s / 2)
+                res[f"{label}_{nt}t"] = {"value": round(emitted / el, 1), "unit": "tok/s",
+                                         "cores": nt, "sample": f"{passes} {sample}, {el:.1f} s"}
+    finally:
+        torch.set_num_threads(old)
+        O.set_threads(threads)
+    head = res.get(f"reference_{threads}t") or res[f"port_{threads}t"]
+    out = dict(head)
+    out["kind"] = "reference" if f"reference_{threads}t" in res else "port"
+    out.update({k: v for k, v in res.items() if k not in (f"{out['kind']}_{threads}t",)})
+    if out["kind"] == "reference":
+        out["sample"] += ("; reference verify_candidates single-threaded per call, softmax on "
+                          f"{threads} threads")
+    return out
+
+
+def chain_step_c1_leg(dev, steps=20, warmup=3, cpu_budget_s=6.0):
+    """the drop-in SpeculativeEngine.step() (python
+    mode, the reference's default) with random-init fp32 runners -- target
+    4 layers / d 512 / 8 heads of 64, draft 1 layer / d 256 / 4 heads,
+    V = 32000 -- at B = 1, K = 4, a 128-token seeded prompt, T = 1.0; every
+    step verifies from the same prompt.  Beside it the same step on the host
+    (oracle/speculative_cpu.py: torch-CPU runners with the same weights and
+    the C oracle's rejection sampling)."""
+    import torch
+    from cudaforge_amd.runners import draft_runner, target_runner
+    from cudaforge_amd.speculative import SpeculativeEngine
+    from oracle.speculative_cpu import chain_step
+
+    Kc, Vc, P = 4, 32000, 128
+    tgt_c, drf_c = target_runner(seed=1), draft_runner(seed=2)
+    tgt, drf = tgt_c.to(dev), drf_c.to(dev)
+    g = torch.Generator().manual_seed(42)
+    prompt = torch.randint(0, Vc, (1, P), generator=g)
+    eng = SpeculativeEngine(drf, tgt, num_speculative_tokens=Kc, temperature=1.0,
+                            generator=torch.Generator(device=dev).manual_seed(43))
+    ids = prompt.to(dev)
+    for _ in range(warmup):
+        eng.step(ids)
+    torch.cuda.synchronize()
+    eng.total_draft_tokens = eng.total_accepted_tokens = 0
+    t0 = time.perf_counter()
+    dlat = tlat = 0.0
+    for _ in range(steps):
+        r = eng.step(ids)
+        dlat += r.draft_latency_ms
+        tlat += r.target_latency_ms
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    out = {"config": "chain step B=1,K=4,V=32000,prompt 128,T=1.0; random-init fp32 target "
+                     "4L/d512/8x64, draft 1L/d256/4x64 (BASELINE configs[0]); drop-in "
+                     "SpeculativeEngine.step(), python mode",
+           "gpu": {"ms_per_step": round(dt / steps * 1e3, 3),
+                   "steps_s": round(steps / dt, 1),
+                   "accepted_tok_s": round(eng.total_accepted_tokens / dt, 1),
+                   "acceptance_rate": round(eng.get_aggregate_acceptance_rate(), 3),
+                   "draft_ms": round(dlat / steps, 3), "target_ms": round(tlat / steps, 3)}}
+    threads = len(os.sched_getaffinity(0))
+    old = torch.get_num_threads()
+    try:
+        for nt in (threads, 1):
+            torch.set_num_threads(nt)
+            gc = torch.Generator().manual_seed(44)
+            chain_step(drf_c, tgt_c, prompt, Kc, generator=gc)  # warm-up
+            emitted, n, t0 = 0, 0, time.perf_counter()
+            while True:
+                emitted += chain_step(drf_c, tgt_c, prompt, Kc, generator=gc)[1]
+                n += 1
+                el = time.perf_counter() - t0
+                if el >= (cpu_budget_s if nt > 1 else cpu_budget_s / 2):
+                    break
+            out[f"cpu_{nt}t"] = {"ms_per_step": round(el / n * 1e3, 2),
+                                 "steps_s": round(n / el, 2),
+                                 "accepted_tok_s": round(emitted / el, 1), "cores": nt,
+                                 "kind": "port", "sample": f"{n} steps, {el:.1f} s"}
+    finally:
+        torch.set_num_threads(old)
+    out["cpu_model"] = _cpu_model()
+    return out
 
 
 def _time_launches(fn, reps, names):
@@ -246,7 +387,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-tree", action="store_true",
                     help="skip the extra legs (tree attention, tree accept/commit, 8B verify step)")
-    ap.add_argument("--legs", default="tree_attention,tree_accept_commit,verify_step_8b",
+    ap.add_argument("--legs",
+                    default="chain_step_c1,tree_attention,tree_accept_commit,verify_step_8b",
                     help="comma-separated extra legs to run")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (reference for HBM byte counters)")
@@ -321,6 +463,7 @@ def main() -> int:
     _lib.profile_reset()
     stats_ms = kern["chain_stats"]  # one launch per step
     achieved = ALG_BYTES / (stats_ms * 1e-3) / 1e9
+    step_gbs = ALG_BYTES / (ms_per_step * 1e-3) / 1e9
 
     line = {
         "metric": METRIC,
@@ -342,14 +485,16 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "chain_stats",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": STATS_TRAFFIC_BYTES},
+                     "traffic": traffic_from_profile("cfa::chain::stats_kernel<256, 4>"),
+                     "step_achieved": round(step_gbs, 1),
+                     "step_frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "kernels_ms_per_step": {k: round(v, 5) for k, v in kern.items()},
-        "step_hbm_gbs": round(ALG_BYTES / (ms_per_step * 1e-3) / 1e9, 1),
+        "step_hbm_gbs": round(step_gbs, 1),
         "wall_s": round(wall, 4),
     }
     legs = [] if args.no_tree else [x for x in args.legs.split(",") if x]
-    known = {"tree_attention": tree_attention_leg, "tree_accept_commit": tree_accept_commit_leg,
-             "verify_step_8b": verify_step_8b_leg}
+    known = {"chain_step_c1": chain_step_c1_leg, "tree_attention": tree_attention_leg,
+             "tree_accept_commit": tree_accept_commit_leg, "verify_step_8b": verify_step_8b_leg}
     if legs:
         del sets
         torch.cuda.empty_cache()
@@ -361,7 +506,7 @@ def main() -> int:
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         tl, dl, tok, U = make_inputs(dev, 1000)
-        line["cpu_baseline"] = cpu_baseline(tl, dl, tok, U)
+        line["cpu_baseline"] = cpu_baseline(tl, dl, tok)
     print(json.dumps(line), flush=True)
     return 0
 

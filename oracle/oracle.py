@@ -80,6 +80,8 @@ def lib() -> ctypes.CDLL:
         L.orc_topp_keep.argtypes = [c_f32p, ctypes.c_int64, ctypes.c_float, c_u8p]
         L.orc_sample_weights.restype = ctypes.c_int32
         L.orc_sample_weights.argtypes = [c_f32p, ctypes.c_int64, ctypes.c_float]
+        L.orc_set_threads.restype = None
+        L.orc_set_threads.argtypes = [ctypes.c_int]
         L.orc_tree_verify.restype = ctypes.c_int
         L.orc_tree_verify.argtypes = [
             ctypes.c_int, ctypes.c_int64, ctypes.c_int64, c_i32p, c_i32p, c_f32p, c_f32p,
@@ -105,6 +107,11 @@ def ref_lib() -> Optional[ctypes.CDLL]:
                                  c_i32p, c_i32p, c_i32p, c_i32p]
         _REF = L
     return _REF
+
+
+def set_threads(n: int) -> None:
+    """OpenMP threads of the batched oracle functions."""
+    lib().orc_set_threads(int(n))
 
 
 def _f32(a) -> np.ndarray:

@@ -9,8 +9,14 @@
 
 #include <float.h>
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
+
+/* Threads of the OpenMP loops below (the CPU baseline times 1 and all). */
+void orc_set_threads(int n) {
+  if (n > 0) omp_set_num_threads(n);
+}
 
 /* speculative.cpp:11-24: cumulative += probs[i]; if (r <= cumulative) return i;
  * falls through to the last index. */

@@ -26,6 +26,9 @@
 extern "C" {
 #endif
 
+/* Threads used by the OpenMP loops of the batched functions. */
+void orc_set_threads(int n);
+
 /* speculative.cpp:11-24 -- sequential fp32 inverse CDF. */
 int32_t orc_sample_from_distribution(const float *probs, int64_t V, float r);
 

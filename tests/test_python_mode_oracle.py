@@ -154,3 +154,52 @@ def test_draws_never_return_zero_weight_tokens():
         assert not fb and tok in (3, 5)
     assert O.py_sample_adjusted(t, d, 0.0)[0] == 3
     assert O.py_sample_adjusted(t, d, np.nextafter(np.float32(1), np.float32(0)))[0] == 5
+
+
+class _Peak:
+    """CPU stub runner: logits 50 on token fn(t) at position t, 0 elsewhere."""
+
+    def __init__(self, fn, V):
+        self.fn, self.V = fn, V
+
+    def forward(self, ids, kv=None):
+        B, T = ids.shape
+        out = torch.zeros(B, T, self.V)
+        for t in range(T):
+            out[:, t, self.fn(t)] = 50.0
+        return out
+
+
+def test_cpu_chain_step_quirks():
+    """oracle.speculative_cpu.chain_step (the CPU path of the chain step): the
+    reference's emitted tokens for forced outcomes."""
+    from oracle.speculative_cpu import chain_step
+
+    V, K, T0 = 64, 4, 6
+    ids = torch.zeros(2, T0, dtype=torch.long)
+    draft = _Peak(lambda t: 7, V)
+    g = torch.Generator().manual_seed(0)
+    last = _Peak(lambda t: 7 if t < T0 + K - 2 else (3 if t == T0 + K - 2 else 9), V)
+    toks, n = chain_step(draft, last, ids, K, generator=g)
+    assert n == K + 1 and toks.tolist() == [[7, 7, 7, 3, 9]] * 2
+    full = _Peak(lambda t: 7 if t < T0 + K - 1 else 9, V)
+    toks, n = chain_step(draft, full, ids, K, generator=g)
+    assert n == K + 1 and toks.tolist() == [[7, 7, 7, 7, 9]] * 2
+    early = _Peak(lambda t: 3 if t == T0 else 7, V)
+    toks, n = chain_step(draft, early, ids, K, generator=g)
+    assert n == 2 and toks.tolist() == [[7, 3]] * 2
+
+
+def test_cpu_chain_step_random_runners():
+    """Small random-init runners: the emitted prefix is the drafted prefix."""
+    from cudaforge_amd.runners import DecoderRunner
+    from oracle.speculative_cpu import chain_step
+
+    V, K = 500, 4
+    tgt = DecoderRunner(V, 64, 2, 2, 32, seed=1)
+    drf = DecoderRunner(V, 32, 1, 1, 32, seed=2)
+    g = torch.Generator().manual_seed(3)
+    ids = torch.randint(0, V, (3, 20), generator=g)
+    toks, n = chain_step(drf, tgt, ids, K, generator=g)
+    assert 1 <= n <= K + 1 and toks.shape == (3, n)
+    assert bool(((toks >= 0) & (toks < V)).all())
