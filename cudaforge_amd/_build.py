@@ -6,6 +6,14 @@ gfx950 into an object under ``csrc/_build/`` (in parallel), then linked into
 runs on any host with ROCm installed.
 
 Run ``python -m cudaforge_amd._build`` (or ``__graft_entry__.build()``).
+
+``--sanitize address`` / ``--sanitize thread`` builds a variant whose HOST
+code (entry points, argument checks, page tables, the host RNG) is
+instrumented with AddressSanitizer + UndefinedBehaviorSanitizer or
+ThreadSanitizer, into ``cudaforge_amd/_san/libcfa_<kind>.so``; device code is
+compiled as usual.  These variants are for CPU-only test runs (the sanitizer
+runtime is preloaded into the test process, and ``CFA_LIB_PATH`` points the
+package at the variant); they are never run on a GPU.
 """
 from __future__ import annotations
 
@@ -48,9 +56,21 @@ def sources() -> list[str]:
     )
 
 
-def _compile(src: str, hipcc: str, verbose: bool) -> str:
-    obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [hipcc, *HIPCC_FLAGS, "-c", src, "-o", obj]
+# host-only instrumentation: each -fsanitize= applies to the host pass only
+SANITIZE_FLAGS = {
+    "address": ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host",
+                "-fno-omit-frame-pointer", "-g"],
+    "thread": ["-Xarch_host", "-fsanitize=thread", "-Xarch_host", "-fno-omit-frame-pointer",
+               "-g"],
+}
+SAN_DIR = os.path.join(PKG, "_san")
+
+
+def _compile(src: str, hipcc: str, verbose: bool, objdir: str = OBJ,
+             extra: tuple = ()) -> str:
+    obj = os.path.join(objdir, os.path.basename(src) + ".o")
+    cmd = [hipcc, *HIPCC_FLAGS, *extra, "-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -63,22 +83,33 @@ def _compile(src: str, hipcc: str, verbose: bool) -> str:
     return obj
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compile every kernel source and link libcfa.so; returns its path."""
+def build(verbose: bool = False, jobs: int | None = None, sanitize: str | None = None) -> str:
+    """Compile every kernel source and link libcfa.so (or, with `sanitize`,
+    the host-instrumented variant under _san/); returns its path."""
     hipcc = _hipcc()
-    os.makedirs(OBJ, exist_ok=True)
+    objdir, lib, extra = OBJ, LIB, ()
+    if sanitize is not None:
+        if sanitize not in SANITIZE_FLAGS:
+            raise ValueError(f"sanitize must be one of {sorted(SANITIZE_FLAGS)}")
+        objdir = os.path.join(SAN_DIR, "obj_" + sanitize)
+        lib = os.path.join(SAN_DIR, f"libcfa_{sanitize}.so")
+        extra = tuple(SANITIZE_FLAGS[sanitize])
+    os.makedirs(objdir, exist_ok=True)
     srcs = sources()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, hipcc, verbose), srcs))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda s: _compile(s, hipcc, verbose, objdir, extra), srcs))
+    tmp = lib + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError("link of libcfa.so failed:\n" + res.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+        raise RuntimeError(f"link of {os.path.basename(lib)} failed:\n" + res.stderr)
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    san = None
+    if "--sanitize" in sys.argv:
+        san = sys.argv[sys.argv.index("--sanitize") + 1]
+    print(build(verbose=True, sanitize=san))

@@ -1,8 +1,10 @@
 """ctypes binding of ``libcfa.so`` (the C ABI declared in include/cudaforge_amd.h).
 
-The library is loaded from the package directory only (it is built in-tree by
-``cudaforge_amd._build``).  There is no fallback: if the library is missing,
-every entry point raises ``RuntimeError`` naming the build command.
+The library is loaded from the package directory (it is built in-tree by
+``cudaforge_amd._build``); ``CFA_LIB_PATH`` selects another build of the same
+library, such as a host-sanitizer variant for CPU test runs.  There is no
+fallback: if the library is missing, every entry point raises
+``RuntimeError`` naming the build command.
 
 Error mapping follows the reference's pybind layer: a C-ABI ``CFA_ERR_ARG`` is
 the ``std::invalid_argument`` of ``csrc/src/scheduler/speculative.cpp:58-62``
@@ -17,7 +19,8 @@ import ctypes
 import os
 import threading
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcfa.so")
+LIB_PATH = os.environ.get("CFA_LIB_PATH") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libcfa.so")
 
 CFA_OK = 0
 CFA_ERR_ARG = -1

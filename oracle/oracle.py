@@ -47,7 +47,8 @@ def build() -> None:
 def lib() -> ctypes.CDLL:
     global _LIB
     if _LIB is None:
-        path = os.path.join(HERE, "liboracle.so")
+        # ORACLE_LIB_PATH: another build of spec_oracle.c (the sanitizer runs)
+        path = os.environ.get("ORACLE_LIB_PATH") or os.path.join(HERE, "liboracle.so")
         if not os.path.exists(path):
             build()
         L = ctypes.CDLL(path)

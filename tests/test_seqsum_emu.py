@@ -14,14 +14,20 @@ SRC = os.path.join(HERE, "native", "seqsum_emu.cpp")
 LIB = os.path.join(HERE, "native", "libseqsum_emu.so")
 
 
-@pytest.fixture(scope="module")
-def emu():
+def build_emu(lib: str = LIB, extra: tuple = ()) -> str:
+    """Compile the host emulation (extra: e.g. sanitizer flags) unless current."""
     hdr = os.path.join(os.path.dirname(HERE), "cudaforge_amd", "csrc", "seqsum.hpp")
-    if not os.path.exists(LIB) or os.path.getmtime(LIB) < max(os.path.getmtime(SRC),
+    if not os.path.exists(lib) or os.path.getmtime(lib) < max(os.path.getmtime(SRC),
                                                                os.path.getmtime(hdr)):
         subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-fPIC", "-shared",
-                        SRC, "-o", LIB], check=True)
-    L = ctypes.CDLL(LIB)
+                        *extra, SRC, "-o", lib], check=True)
+    return lib
+
+
+@pytest.fixture(scope="module")
+def emu():
+    # SEQSUM_EMU_LIB: another build of the emulation (the sanitizer runs)
+    L = ctypes.CDLL(os.environ.get("SEQSUM_EMU_LIB") or build_emu())
     L.emu_seq.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_longlong, ctypes.c_int,
                           ctypes.c_float, ctypes.c_int, ctypes.c_float,
                           ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_longlong),
