@@ -124,10 +124,11 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _p, _i64, _i, _i, _i, _i, _i, _i, _f, _i, _i,
          _p, _p, _sz, _p],
     ),
+    "cfa_tree_verify_workspace_size": (_sz, [_i]),
     "cfa_tree_verify": (
         _i,
         [_p, _i64, _i64, _p, _i64, _i64, _i, _p, _i64, _p, _p, _i, _i, _i, _i, _f, _i, _i32,
-         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p],
     ),
     "cfa_kv_commit": (
         _i,

@@ -21,18 +21,22 @@
 // verify_candidates.  Greedy: a child is accepted iff its token is the first
 // argmax of p_node; none accepted -> final = that argmax (:105-150).
 //
-// One 1024-thread work-group per sequence walks its tree.  A visited row's
-// softmax statistics (logits input) are computed when the walk first needs
-// them, so only visited rows are read; every residual sum and inverse CDF is
-// the exact sequential fp32 replay of seqsum.hpp, with the residual chain
-// r^(k) = max(0, r^(k-1) - q) / S_k evaluated element-wise on the fly.
+// A team of G <= 8 work-groups per sequence (one cooperative launch; team.hpp)
+// walks its tree: each visited row's softmax statistics (logits input) are
+// reduced over the team, each member reading its slice of the row, so only
+// visited rows are read; every residual sum and inverse CDF is the exact
+// sequential fp32 replay of seqsum.hpp split over the team (team_seq), with
+// the residual chain r^(k) = max(0, r^(k-1) - q) / S_k evaluated element-wise
+// on the fly.  With more sequences than teams, each team walks several.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "abi_internal.hpp"
 #include "dist.hpp"
 #include "seqsum.hpp"
+#include "team.hpp"
 
 #pragma clang fp contract(off)
 
@@ -55,6 +59,9 @@ struct Args {
   const float *U;      // [B, n_u]
   int n_u;
   int B, N, V, greedy, eos, vec;
+  int T, G;              // teams, work-groups per team
+  team::State *teams;    // [T] (zero before the launch)
+  int *err;              // team wait timed out somewhere
   int32_t *out_path, *out_path_len, *out_tokens, *out_num_emitted, *out_final, *out_eos,
       *out_status;
   float *probs_t, *probs_d;  // optional [B, N, V]: the probabilities of visited rows
@@ -94,14 +101,57 @@ struct ResidX {
   }
 };
 
+// fp32 bounds on a double: the largest float <= v and the smallest >= v.
+__device__ __forceinline__ float f32_down(double v) {
+  float f = (float)v;
+  if ((double)f > v) f = __uint_as_float(__float_as_uint(f) - 1u);  // v > 0 here
+  return f;
+}
+__device__ __forceinline__ float f32_up(double v) {
+  float f = (float)v;
+  if ((double)f < v) f = __uint_as_float(__float_as_uint(f) + 1u);
+  return f;
+}
+
+// Early exit of the residual sum S = sum max(0, r^(k) - q) that a rejected
+// child needs only for its next sibling's test: given the blocked fp32 total
+// Sb of the same terms (at most `depth` additions deep), the sequential sum
+// lies in [Sb (1 - g_n) / (1 + g_depth), Sb (1 + g_n) / (1 - g_depth)] with
+// g_k = k u / (1 - k u), u = 2^-24 (the standard bound for sums of
+// non-negative terms).  The sibling's ratio min(1, r^(k+1)(x) / q(x)),
+// r^(k+1)(x) = max(0, r^(k)(x) - q(x)) / S, does not increase with S, so if
+// its uniform passes at the largest S (and the <= 1e-6 fallback is excluded)
+// it is accepted whatever the exact S is: the exact walk is skipped.
+struct SiblingAccepts {
+  Resid r;  // r^(k)
+  int x;    // the sibling's token (valid)
+  float u;  // its uniform
+  long long n;
+  __device__ bool operator()(float Sb, int depth) const {
+    const double u24 = 5.9604644775390625e-08;
+    const double gn = (double)n * u24 / (1.0 - (double)n * u24);
+    const double gd = (double)depth * u24 / (1.0 - (double)depth * u24);
+    if (!(gn < 0.5) || !(gd < 0.5)) return false;
+    const float lo = f32_down((double)Sb * (1.0 - gn) / (1.0 + gd));
+    const float hi = f32_up((double)Sb * (1.0 + gn) / (1.0 - gd));
+    if (!(lo > 1e-6f) || !(hi < INFINITY)) return false;
+    const float p = r.eval(r.load(x));
+    const float q = r.d(x);
+    const float ratio = ratio_cpp(relu_ref(p - q) / hi, q);
+    return u <= ratio;
+  }
+};
+
 struct __align__(16) Smem {
   seq::Shared<kNT> seq;
-  float red_m[kNT / 64], red_s[kNT / 64];
+  team::Lds tl;
+  float red[4][kNT / 64];
   float Slist[kMaxN];
   int par[kMaxN];
   int tk[kMaxN];
   int path[kMaxN];
-  float2 amv[kNT / 64];
+  float4 stat;  // (max, 1/sum) of the target and the draft row
+  int amax;
   unsigned long long kids;
 };
 
@@ -112,14 +162,32 @@ __device__ __forceinline__ const float *drow(const Args &a, int b, int n) {
   return a.drf + (long long)b * a.d_sb + (long long)n * a.d_sn;
 }
 
-// Softmax statistics (max, 1/sum exp2) of one logits row, block-wide, in a
-// fixed reduction order.
-__device__ float2 row_stats(const Args &a, const float *row, Smem &sm) {
+// This member's slice [lo, hi) of a row (a multiple of 4 elements long).
+__device__ __forceinline__ void slice(const Args &a, const team::Team &tm, long long &lo,
+                                      long long &hi) {
+  const long long L = ((a.V + tm.G - 1) / tm.G + 3) / 4 * 4;
+  lo = min((long long)a.V, (long long)tm.m * L);
+  hi = min((long long)a.V, lo + L);
+}
+
+__device__ __forceinline__ void ms_merge(float &m1, float &s1, float m2, float s2, float c) {
+  const float M = fmaxf(m1, m2);
+  if (M == -INFINITY) return;
+  const float f1 = (m1 == M) ? 1.0f : __builtin_amdgcn_exp2f((m1 - M) * c);
+  const float f2 = (m2 == M) ? 1.0f : __builtin_amdgcn_exp2f((m2 - M) * c);
+  s1 = s1 * f1 + s2 * f2;
+  m1 = M;
+}
+
+// (max, sum exp2((x - max) c)) of t[lo, hi) and of d[lo, hi) (d may be
+// NULL), block-wide, in a fixed order: (m_t, s_t, m_d, s_d).  Both rows'
+// loads are issued together.
+__device__ float4 slice_ms2(const Args &a, const float *t, const float *d, long long lo,
+                            long long hi, Smem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float c = a.c;
-  float m = -INFINITY, s = 0.0f;
-  // one online update per group of four values: rescale once per new maximum
-  auto update = [&](float v0, float v1, float v2, float v3) {
+  float mt = -INFINITY, st = 0.0f, md = -INFINITY, sd = 0.0f;
+  auto update = [c](float &m, float &s, float v0, float v1, float v2, float v3) {
     const float mx = fmaxf(fmaxf(v0, v1), fmaxf(v2, v3));
     if (mx > m) {
       s *= __builtin_amdgcn_exp2f((m - mx) * c);
@@ -130,87 +198,122 @@ __device__ float2 row_stats(const Args &a, const float *row, Smem &sm) {
          __builtin_amdgcn_exp2f((v2 - ms) * c) + __builtin_amdgcn_exp2f((v3 - ms) * c);
   };
   if (a.vec) {
-    // 16-byte loads, four in flight per thread
-    const float4 *p4 = reinterpret_cast<const float4 *>(row);
-    const int n4 = a.V / 4;
+    // 16-byte loads; lo and hi are multiples of 4 (a.vec implies V % 4 == 0)
+    const float4 *t4 = reinterpret_cast<const float4 *>(t + lo);
+    const float4 *d4 = d ? reinterpret_cast<const float4 *>(d + lo) : t4;
+    const int n4 = (int)((hi - lo) / 4);
     constexpr int U = 4;
     int i = tid;
     for (; i + (U - 1) * kNT < n4; i += U * kNT) {
-      float4 v[U];
+      float4 vt[U], vd[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = p4[i + u * kNT];
+      for (int u = 0; u < U; ++u) vt[u] = t4[i + u * kNT];
+      if (d) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) update(v[u].x, v[u].y, v[u].z, v[u].w);
+        for (int u = 0; u < U; ++u) vd[u] = d4[i + u * kNT];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) update(mt, st, vt[u].x, vt[u].y, vt[u].z, vt[u].w);
+      if (d) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) update(md, sd, vd[u].x, vd[u].y, vd[u].z, vd[u].w);
+      }
     }
     for (; i < n4; i += kNT) {
-      const float4 v = p4[i];
-      update(v.x, v.y, v.z, v.w);
+      const float4 vt = t4[i];
+      const float4 vd = d4[i];
+      update(mt, st, vt.x, vt.y, vt.z, vt.w);
+      if (d) update(md, sd, vd.x, vd.y, vd.z, vd.w);
     }
   } else {
-    for (int i = tid; i < a.V; i += kNT) {
-      const float v = row[i];
+    auto upd1 = [c](float &m, float &s, float v) {
       if (v > m) {
         s *= __builtin_amdgcn_exp2f((m - v) * c);
         m = v;
       }
       const float ms = (m == -INFINITY) ? 0.0f : m;
       s += __builtin_amdgcn_exp2f((v - ms) * c);
+    };
+    for (long long i = lo + tid; i < hi; i += kNT) {
+      upd1(mt, st, t[i]);
+      if (d) upd1(md, sd, d[i]);
     }
   }
-  auto merge = [c](float &m1, float &s1, float m2, float s2) {
-    const float M = fmaxf(m1, m2);
-    if (M == -INFINITY) return;
-    const float f1 = (m1 == M) ? 1.0f : __builtin_amdgcn_exp2f((m1 - M) * c);
-    const float f2 = (m2 == M) ? 1.0f : __builtin_amdgcn_exp2f((m2 - M) * c);
-    s1 = s1 * f1 + s2 * f2;
-    m1 = M;
-  };
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const float m2 = __shfl_xor(m, d, 64), s2 = __shfl_xor(s, d, 64);
-    merge(m, s, m2, s2);
+  for (int k = 32; k >= 1; k >>= 1) {
+    const float m2 = __shfl_xor(mt, k, 64), s2 = __shfl_xor(st, k, 64);
+    const float m3 = __shfl_xor(md, k, 64), s3 = __shfl_xor(sd, k, 64);
+    ms_merge(mt, st, m2, s2, c);
+    ms_merge(md, sd, m3, s3, c);
   }
   if (lane == 0) {
-    sm.red_m[wave] = m;
-    sm.red_s[wave] = s;
+    sm.red[0][wave] = mt;
+    sm.red[1][wave] = st;
+    sm.red[2][wave] = md;
+    sm.red[3][wave] = sd;
   }
   __syncthreads();
-  float M = sm.red_m[0], S = sm.red_s[0];
-  for (int w = 1; w < kNT / 64; ++w) merge(M, S, sm.red_m[w], sm.red_s[w]);
+  float4 r = make_float4(sm.red[0][0], sm.red[1][0], sm.red[2][0], sm.red[3][0]);
+  for (int w = 1; w < kNT / 64; ++w) {
+    ms_merge(r.x, r.y, sm.red[0][w], sm.red[1][w], c);
+    ms_merge(r.z, r.w, sm.red[2][w], sm.red[3][w], c);
+  }
   __syncthreads();
-  return make_float2(M, 1.0f / S);
+  return r;
 }
 
-__device__ Dist make_row(const Args &a, const float *row, Smem &sm) {
+// Softmax statistics of the target row (and the draft row when `d` is set),
+// reduced over the team in member order: sm.stat = (M_t, 1/S_t, M_d, 1/S_d).
+__device__ void team_stats(const Args &a, team::Team &tm, Smem &sm, const float *t,
+                           const float *d) {
+  long long lo, hi;
+  slice(a, tm, lo, hi);
+  const float4 p = slice_ms2(a, t, d, lo, hi, sm);
+  team::publish(tm, 2, team::f4u(p));
+  team::sync(tm, sm.tl);
+  team::fetch(tm, sm.tl, 2, 2);
+  if (threadIdx.x == 0) {
+    float4 acc = team::u4f(sm.tl.got[0][0]);
+    for (int j = 1; j < tm.G; ++j) {
+      const float4 v = team::u4f(sm.tl.got[j][0]);
+      ms_merge(acc.x, acc.y, v.x, v.y, a.c);
+      ms_merge(acc.z, acc.w, v.z, v.w, a.c);
+    }
+    sm.stat = make_float4(acc.x, 1.0f / acc.y, acc.z, 1.0f / acc.w);
+  }
+  __syncthreads();
+}
+
+__device__ Dist row_dist(const Args &a, const float *row, float M, float invS) {
   Dist d;
   d.p = row;
   d.c = a.c;
   d.logits = a.logits;
-  d.M = 0.0f;
-  d.invS = 1.0f;
-  if (a.logits) {
-    const float2 st = row_stats(a, row, sm);
-    d.M = st.x;
-    d.invS = st.y;
-  }
+  d.M = a.logits ? M : 0.0f;
+  d.invS = a.logits ? invS : 1.0f;
   return d;
 }
 
-__device__ void write_probs(const Dist &d, float *dst, int V) {
+// This member's slice of the probabilities the walk used.
+__device__ void write_probs(const Args &a, const team::Team &tm, const Dist &d, float *dst) {
   if (!dst) return;
-  for (int i = threadIdx.x; i < V; i += kNT) dst[i] = d(i);
+  long long lo, hi;
+  slice(a, tm, lo, hi);
+  for (long long i = lo + threadIdx.x; i < hi; i += kNT) dst[i] = d(i);
 }
 
-// First index of the largest probability (std::max_element), block-wide.
-__device__ int row_argmax(const Dist &d, int V, Smem &sm) {
+// First index of the largest probability (std::max_element) over the team.
+__device__ int team_argmax(const Args &a, team::Team &tm, Smem &sm, const Dist &d) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  long long lo, hi;
+  slice(a, tm, lo, hi);
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = tid; i < V; i += kNT) {
+  for (long long i = lo + tid; i < hi; i += kNT) {
     const float v = d(i);
     if (v > bv) {  // strided: indices increase, so ">" keeps the first max
       bv = v;
-      bi = i;
+      bi = (int)i;
     }
   }
 #pragma unroll
@@ -222,34 +325,58 @@ __device__ int row_argmax(const Dist &d, int V, Smem &sm) {
       bi = i2;
     }
   }
-  if (lane == 0) sm.amv[wave] = make_float2(bv, __int_as_float(bi));
-  __syncthreads();
-  float v = sm.amv[0].x;
-  int ix = __float_as_int(sm.amv[0].y);
-  for (int w = 1; w < kNT / 64; ++w) {
-    const float v2 = sm.amv[w].x;
-    const int i2 = __float_as_int(sm.amv[w].y);
-    if (v2 > v || (v2 == v && i2 < ix)) {
-      v = v2;
-      ix = i2;
-    }
+  if (lane == 0) {
+    sm.red[0][wave] = bv;
+    sm.red[1][wave] = __int_as_float(bi);
   }
   __syncthreads();
-  return ix == 0x7fffffff ? 0 : ix;
+  if (tid == 0) {
+    float v = sm.red[0][0];
+    int ix = __float_as_int(sm.red[1][0]);
+    for (int w = 1; w < kNT / 64; ++w) {
+      const float v2 = sm.red[0][w];
+      const int i2 = __float_as_int(sm.red[1][w]);
+      if (v2 > v || (v2 == v && i2 < ix)) {
+        v = v2;
+        ix = i2;
+      }
+    }
+    sm.red[2][0] = v;
+    sm.red[3][0] = __int_as_float(ix);
+  }
+  __syncthreads();
+  team::publish(tm, 3, make_uint4(__float_as_uint(sm.red[2][0]), __float_as_uint(sm.red[3][0]), 0u, 0u));
+  team::sync(tm, sm.tl);
+  team::fetch(tm, sm.tl, 3, 3);
+  if (tid == 0) {
+    float v = __uint_as_float(sm.tl.got[0][0].x);
+    int ix = (int)sm.tl.got[0][0].y;
+    for (int j = 1; j < tm.G; ++j) {
+      const float v2 = __uint_as_float(sm.tl.got[j][0].x);
+      const int i2 = (int)sm.tl.got[j][0].y;
+      if (v2 > v || (v2 == v && i2 < ix)) {
+        v = v2;
+        ix = i2;
+      }
+    }
+    sm.amax = (ix == 0x7fffffff) ? 0 : ix;
+  }
+  __syncthreads();
+  return sm.amax;
 }
 
-__global__ __launch_bounds__(kNT) void tree_verify_kernel(Args a) {
-  __shared__ Smem sm;
-  const int b = blockIdx.x, tid = threadIdx.x;
+// One sequence's walk; every member of the team runs it with the same data.
+__device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
+  const int tid = threadIdx.x;
   const int N = a.N, V = a.V;
   if (tid < N) {
     sm.par[tid] = a.parent[(long long)b * a.parent_sb + tid];
     sm.tk[tid] = a.tok[(long long)b * N + tid];
   }
+  if (tid == 0) sm.path[0] = 0;
   __syncthreads();
   const float *U = a.U ? a.U + (long long)b * a.n_u : nullptr;
   int node = 0, len = 1, draws = 0, fin = -1, eos_acc = 0, status = 0;
-  if (tid == 0) sm.path[0] = 0;
   for (;;) {
     // children of `node`, in increasing index order
     unsigned long long kids = 0;
@@ -261,25 +388,31 @@ __global__ __launch_bounds__(kNT) void tree_verify_kernel(Args a) {
       kids = sm.kids;
       __syncthreads();
     }
-    const Dist t = make_row(a, trow(a, b, node), sm);
-    if (a.probs_t) write_probs(t, a.probs_t + ((long long)b * N + node) * V, V);
-    if (!kids) {  // a leaf: the bonus token
+    const bool leaf = kids == 0;
+    const float *tr = trow(a, b, node);
+    const float *dr = (leaf || a.greedy) ? nullptr : drow(a, b, node);
+    if (a.logits) team_stats(a, tm, sm, tr, dr);
+    const float4 st = sm.stat;
+    const Dist t = row_dist(a, tr, st.x, st.y);
+    if (a.probs_t) write_probs(a, tm, t, a.probs_t + ((long long)b * N + node) * V);
+    if (leaf) {  // the bonus token
       if (a.greedy) {
-        fin = row_argmax(t, V, sm);
+        fin = team_argmax(a, tm, sm, t);
       } else {
         if (draws >= a.n_u) {
           status = 1;
           break;
         }
         long long idx = -1;
-        seq::run<kNT>(Resid{t, t, sm.Slist, 0}, V, true, U[draws++], sm.seq, &idx);
+        team::team_seq<kNT>(tm, sm.tl, Resid{t, t, sm.Slist, 0}, V, true, U[draws++], sm.seq,
+                            &idx);
         fin = (idx < 0) ? V - 1 : (int)idx;
       }
       break;
     }
     int accepted = -1;
     if (a.greedy) {
-      const int am = row_argmax(t, V, sm);
+      const int am = team_argmax(a, tm, sm, t);
       for (unsigned long long m = kids; m; m &= m - 1) {
         const int c = __builtin_ctzll(m);
         if (sm.tk[c] == am) {
@@ -292,8 +425,8 @@ __global__ __launch_bounds__(kNT) void tree_verify_kernel(Args a) {
         break;
       }
     } else {
-      const Dist d = make_row(a, drow(a, b, node), sm);
-      if (a.probs_d) write_probs(d, a.probs_d + ((long long)b * N + node) * V, V);
+      const Dist d = row_dist(a, dr, st.z, st.w);
+      if (a.probs_d) write_probs(a, tm, d, a.probs_d + ((long long)b * N + node) * V);
       int k = 0;  // applied normalisations of the residual
       for (unsigned long long m = kids; m; m &= m - 1) {
         const int c = __builtin_ctzll(m);
@@ -313,7 +446,21 @@ __global__ __launch_bounds__(kNT) void tree_verify_kernel(Args a) {
           accepted = c;
           break;
         }
-        const float S = seq::run<kNT>(ResidX{r}, V, false, 0.0f, sm.seq, nullptr);
+        // the next sibling, when its test can be settled from bounds on S
+        const unsigned long long rest = m & (m - 1);
+        float S;
+        if (rest && draws < a.n_u && sm.tk[__builtin_ctzll(rest)] >= 0 &&
+            sm.tk[__builtin_ctzll(rest)] < V) {
+          const SiblingAccepts early{r, sm.tk[__builtin_ctzll(rest)], U[draws], (long long)V};
+          S = team::team_seq<kNT>(tm, sm.tl, ResidX{r}, V, false, 0.0f, sm.seq, nullptr, early);
+          if (S < 0.0f) {  // the sibling is accepted for every S in the bounds
+            accepted = __builtin_ctzll(rest);
+            ++draws;
+            break;
+          }
+        } else {
+          S = team::team_seq<kNT>(tm, sm.tl, ResidX{r}, V, false, 0.0f, sm.seq, nullptr);
+        }
         if (S > 1e-6f) {  // else the residual stays (speculative.cpp:37-40)
           if (tid == 0) sm.Slist[k] = S;
           __syncthreads();
@@ -327,7 +474,8 @@ __global__ __launch_bounds__(kNT) void tree_verify_kernel(Args a) {
           break;
         }
         long long idx = -1;
-        seq::run<kNT>(Resid{t, d, sm.Slist, k}, V, true, U[draws++], sm.seq, &idx);
+        team::team_seq<kNT>(tm, sm.tl, Resid{t, d, sm.Slist, k}, V, true, U[draws++], sm.seq,
+                            &idx);
         fin = (idx < 0) ? V - 1 : (int)idx;
         break;
       }
@@ -342,6 +490,8 @@ __global__ __launch_bounds__(kNT) void tree_verify_kernel(Args a) {
     }
   }
   __syncthreads();
+  if (sm.tl.failed || team::error_set(a.err)) status = 2;  // a team wait timed out
+  if (tm.m != 0) return;
   // outputs: path (root first), emitted tokens (accepted drafts then final)
   const long long ob = (long long)b * N;
   for (int j = tid; j < N; j += kNT) a.out_path[ob + j] = (j < len) ? sm.path[j] : -1;
@@ -360,10 +510,64 @@ __global__ __launch_bounds__(kNT) void tree_verify_kernel(Args a) {
   }
 }
 
+__global__ __launch_bounds__(kNT) void tree_verify_kernel(Args a) {
+  __shared__ Smem sm;
+  const int team_id = (int)blockIdx.x / a.G;
+  if (threadIdx.x == 0) sm.tl.failed = 0;
+  __syncthreads();
+  if (team_id >= a.T) return;
+  team::Team tm{a.teams + team_id, a.err, (int)blockIdx.x % a.G, a.G, 0u, 0u};
+  for (int b = team_id; b < a.B; b += a.T) {
+    walk_sequence(a, tm, sm, b);
+    __syncthreads();
+  }
+}
+
+// Zero the teams' state before the cooperative launch.
+__global__ __launch_bounds__(256) void clear_kernel(uint4 *p, long long n) {
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Teams and members for B sequences on `cus` CUs holding `per_cu` work-groups.
+struct Plan {
+  int G, T;
+};
+inline Plan plan(int B, int cus, int per_cu) {
+  const int slots = max(1, cus * max(1, per_cu));
+  int G = team::kMaxG;
+  while (G > 1 && (long long)B * G > slots) G >>= 1;
+  const int T = max(1, min(B, slots / G));
+  return Plan{G, T};
+}
+
 }  // namespace treev
 }  // namespace cfa
 
 using namespace cfa;
+
+namespace {
+// Work-groups of the tree kernel one CU holds, per device (queried once).
+int kernel_per_cu() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)treev::tree_verify_kernel,
+                                                     treev::kNT, 0) != hipSuccess || n < 1)
+      n = 1;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+constexpr size_t kErrBytes = 256;
+}  // namespace
+
+extern "C" size_t cfa_tree_verify_workspace_size(int B) {
+  if (B <= 0) return 0;
+  return kErrBytes + (size_t)B * sizeof(team::State);
+}
 
 extern "C" int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t t_stride_n,
                                const float *draft, int64_t d_stride_b, int64_t d_stride_n,
@@ -373,11 +577,13 @@ extern "C" int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t 
                                int32_t eos_token_id, int32_t *out_path, int32_t *out_path_len,
                                int32_t *out_tokens, int32_t *out_num_emitted, int32_t *out_final,
                                int32_t *out_eos, int32_t *out_status, float *out_target_probs,
-                               float *out_draft_probs, void *stream) {
+                               float *out_draft_probs, void *workspace, size_t workspace_bytes,
+                               void *stream) {
   using namespace cfa::abi;
   clear_error();
   if (B <= 0 || N <= 0 || N > treev::kMaxN || V <= 0)
     return fail_arg("need B > 0, 0 < N <= 64 and V > 0");
+  if (V >= (1 << 24) - 1) return fail_arg("V must be below 16777215");
   if (mode != CFA_MODE_CPP && mode != CFA_MODE_GREEDY)
     return fail_arg("tree verification supports CFA_MODE_CPP and CFA_MODE_GREEDY");
   if (input_kind != CFA_INPUT_PROBS && input_kind != CFA_INPUT_LOGITS)
@@ -392,6 +598,12 @@ extern "C" int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t 
   if (!greedy && (d_stride_n < V || d_stride_b < (int64_t)N * d_stride_n))
     return fail_arg("draft strides overlap rows");
   if (B > 2147483647 / 2) return fail_arg("B too large");
+  const int cus = device_cu_count();
+  const treev::Plan pl = treev::plan(B, cus, kernel_per_cu());
+  const size_t need = kErrBytes + (size_t)pl.T * sizeof(team::State);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255))
+    return fail_arg("workspace missing, too small or not 256-byte aligned "
+                    "(see cfa_tree_verify_workspace_size)");
   treev::Args a{};
   a.tgt = target;
   a.t_sb = t_stride_b;
@@ -411,6 +623,10 @@ extern "C" int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t 
   a.V = V;
   a.greedy = greedy ? 1 : 0;
   a.eos = eos_token_id;
+  a.T = pl.T;
+  a.G = pl.G;
+  a.err = (int *)workspace;
+  a.teams = (team::State *)((char *)workspace + kErrBytes);
   a.out_path = out_path;
   a.out_path_len = out_path_len;
   a.out_tokens = out_tokens;
@@ -424,7 +640,17 @@ extern "C" int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t 
   a.vec = (V % 4 == 0) && (t_stride_b % 4 == 0) && (t_stride_n % 4 == 0) &&
           (((uintptr_t)target & 15) == 0) &&
           (greedy || ((d_stride_b % 4 == 0) && (d_stride_n % 4 == 0) && (((uintptr_t)draft & 15) == 0)));
-  CFA_LAUNCH("tree_verify", treev::tree_verify_kernel, dim3(B), dim3(treev::kNT), 0,
-             (hipStream_t)stream, a);
+  hipStream_t st = (hipStream_t)stream;
+  const long long words = (long long)(need / sizeof(uint4));
+  CFA_LAUNCH("tree_verify_clear", treev::clear_kernel,
+             dim3((unsigned)std::min<long long>((words + 255) / 256, 1024)), dim3(256), 0, st,
+             (uint4 *)workspace, words);
+  // every team's members must be resident together: a cooperative launch
+  void *tok = prof::enabled() ? prof::begin("tree_verify", st) : nullptr;
+  void *args[] = {&a};
+  const hipError_t e = hipLaunchCooperativeKernel((const void *)treev::tree_verify_kernel,
+                                                  dim3(pl.T * pl.G), dim3(treev::kNT), args, 0, st);
+  if (tok) prof::end(tok, st);
+  if (e != hipSuccess) return fail_hip(e, "tree_verify (cooperative launch)");
   return CFA_OK;
 }

@@ -300,12 +300,17 @@ class TreeVerifyOutput:
 def tree_verify(target: torch.Tensor, draft: Optional[torch.Tensor], parents: torch.Tensor,
                 node_tokens: torch.Tensor, uniforms: Optional[torch.Tensor], *,
                 input_kind: str = "logits", temperature: float = 1.0, mode: str = "cpp",
-                eos_token_id: int = -1, return_probs: bool = False) -> TreeVerifyOutput:
+                eos_token_id: int = -1, return_probs: bool = False,
+                workspace: Optional[torch.Tensor] = None) -> TreeVerifyOutput:
     """Accept the longest root-to-leaf path of a draft tree.
 
     target / draft [B, N, V] fp32 (rows may be strided; the vocabulary
     dimension contiguous); parents [N] or [B, N] int32 with parents[c] < c and
     parents[0] = -1; node_tokens [B, N] int32; uniforms [B, n_u] fp32 (cpp mode).
+    workspace: optional uint8 device tensor of tree_verify_workspace_bytes(B).
+    status: 0 ok, 1 the uniform stream ran out, 2 a wait between the
+    work-groups of a sequence timed out (raised as RuntimeError by
+    check_status).
     """
     if mode not in ("cpp", "greedy"):
         raise ValueError("mode must be 'cpp' or 'greedy'")
@@ -350,8 +355,12 @@ def tree_verify(target: torch.Tensor, draft: Optional[torch.Tensor], parents: to
         out.target_probs = torch.zeros(B, N, V, dtype=torch.float32, device=dev)
         if not greedy:
             out.draft_probs = torch.zeros(B, N, V, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    need = int(lib.cfa_tree_verify_workspace_size(B))
+    if workspace is None or workspace.numel() < need or workspace.data_ptr() % 256:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        rc = _lib.load().cfa_tree_verify(
+        rc = lib.cfa_tree_verify(
             target.data_ptr(), target.stride(0), target.stride(1),
             None if greedy else draft.data_ptr(), 0 if greedy else draft.stride(0),
             0 if greedy else draft.stride(1), _KINDS[input_kind], parents.data_ptr(), pstride,
@@ -360,6 +369,10 @@ def tree_verify(target: torch.Tensor, draft: Optional[torch.Tensor], parents: to
             _MODES[mode], int(eos_token_id), out.path.data_ptr(), out.path_len.data_ptr(),
             out.tokens.data_ptr(), out.num_emitted.data_ptr(), out.final.data_ptr(),
             out.eos.data_ptr(), out.status.data_ptr(), _ptr(out.target_probs),
-            _ptr(out.draft_probs), _stream_ptr(dev))
+            _ptr(out.draft_probs), workspace.data_ptr(), workspace.numel(), _stream_ptr(dev))
     _lib.check(rc, "cfa_tree_verify")
     return out
+
+
+def tree_verify_workspace_bytes(B: int) -> int:
+    return int(_lib.load().cfa_tree_verify_workspace_size(B))

@@ -99,18 +99,23 @@ def w4a16_gemm(a: torch.Tensor, b_quant: torch.Tensor, scales: torch.Tensor, *,
 
 
 class W4A16Linear:
-    """y = x @ W with W [K, N] held as packed INT4 + fp16 group scales.
-    Random initialisation: uniform nibbles, scales chosen so that the output
-    of a unit-RMS input has RMS about 1 (nibbles are unsigned, as in the
-    reference format, so W has a positive mean)."""
+    """y = x @ W with W [K, N] held as packed INT4 + fp16 group scales and
+    zero points, w = (nibble - z) * s (dequantize.cuh:12-25).
+    Random initialisation: uniform nibbles, zero point 7.5 (symmetric
+    weights), scales chosen so that the output of a unit-RMS input has RMS
+    about 1.  With unsigned nibbles and no zero point every weight would be
+    positive, and the residual stream of a random model grows to thousands
+    and cancels on some rows, where no bf16 computation tracks an fp32 one."""
 
     def __init__(self, K: int, N: int, device, gen: torch.Generator, group: int = 128):
         self.K, self.N, self.group = K, N, group
         self.qweight = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), dtype=torch.int32,
                                      device=device, generator=gen)
-        base = 1.0 / (9.0 * math.sqrt(K))
+        # E[(nibble - 7.5)^2] = 21.25 for uniform nibbles 0..15
+        base = 1.0 / (math.sqrt(21.25) * math.sqrt(K))
         self.scales = (base * (0.5 + torch.rand(K // group, N, device=device, generator=gen))
                        ).to(torch.float16)
+        self.zeros = torch.full_like(self.scales, 7.5)
 
     # class-wide switch: the fused GEMM (cfa_w4a16_gemm) where the shape
     # allows; off by default because dequantise + hipBLASLt is faster at the
@@ -118,13 +123,13 @@ class W4A16Linear:
     fused = False
 
     def __call__(self, x: torch.Tensor, scratch: torch.Tensor) -> torch.Tensor:
-        if self.fused and fused_gemm_ok(x, self.qweight, None, self.group):
+        if self.fused and fused_gemm_ok(x, self.qweight, self.zeros, self.group):
             return w4a16_gemm(x, self.qweight, self.scales, group_size=self.group)
         # [N, K] (K contiguous): x @ w^T runs about 20% faster on hipBLASLt
         # than x @ w at M = 504 (1.27 against 1.06 PFLOP/s for gate/up)
         wt = scratch[: self.K * self.N].view(self.N, self.K)
-        w4a16_dequant(self.qweight, self.scales, group_size=self.group, dtype=x.dtype, out=wt,
-                      transposed=True)
+        w4a16_dequant(self.qweight, self.scales, self.zeros, group_size=self.group,
+                      dtype=x.dtype, out=wt, transposed=True)
         return x @ wt.t()
 
 

@@ -227,10 +227,18 @@ int cfa_tree_attention(const void *q, const void *k_pool, const void *v_pool,
  * Outputs (int32): path [B, N] accepted node ids from the root, -1 padded;
  * path_len [B] (1 + accepted drafts); tokens [B, N+1] accepted draft tokens
  * then the final token; num_emitted [B]; final [B]; eos [B]; status [B]
- * (optional; 1 when the uniform stream ran out).  out_target_probs /
- * out_draft_probs (optional, [B, N, V]) receive the probabilities of the rows
- * the walk visited.
+ * (optional; 1 when the uniform stream ran out, 2 when a wait between the
+ * work-groups of a sequence timed out -- the outputs are then invalid).
+ * out_target_probs / out_draft_probs (optional, [B, N, V]) receive the
+ * probabilities of the rows the walk visited.
+ *
+ * Up to 8 work-groups share each sequence (one cooperative launch: they
+ * exchange row statistics and split every exact pass); workspace is
+ * cfa_tree_verify_workspace_size(B) bytes, 256-byte aligned, holding their
+ * barrier and exchange state (cleared by the call itself).  Calls sharing a
+ * workspace must not overlap.
  */
+size_t cfa_tree_verify_workspace_size(int B);
 int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t t_stride_n,
                     const float *draft, int64_t d_stride_b, int64_t d_stride_n, int input_kind,
                     const int32_t *parents, int64_t parents_stride_b, const int32_t *node_tokens,
@@ -238,7 +246,8 @@ int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t t_stride_n,
                     float temperature, int mode, int32_t eos_token_id, int32_t *out_path,
                     int32_t *out_path_len, int32_t *out_tokens, int32_t *out_num_emitted,
                     int32_t *out_final, int32_t *out_eos, int32_t *out_status,
-                    float *out_target_probs, float *out_draft_probs, void *stream);
+                    float *out_target_probs, float *out_draft_probs, void *workspace,
+                    size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
  * KV commit / compaction of an accepted draft-tree path.

@@ -34,7 +34,7 @@ def _ref_forward(tm: TargetModel, tokens, positions, kv, tables, base, N):
     bs = kv.get_config().block_size
 
     def W(lin):
-        return w4a16_dequant(lin.qweight, lin.scales, group_size=lin.group,
+        return w4a16_dequant(lin.qweight, lin.scales, lin.zeros, group_size=lin.group,
                              dtype=torch.bfloat16).float()
 
     def rms(x, w):
@@ -167,7 +167,8 @@ def test_target_tree_forward_vs_fp32(device):
     for b in range(B):
         sp.kv.truncate_sequence(b, sp.ctx[b])
     base = torch.tensor(sp.ctx, dtype=torch.int32, device=device)
-    tokens = torch.randint(0, SMALL_T.vocab, (B, N), device=device, dtype=torch.int32)
+    tokens = torch.randint(0, SMALL_T.vocab, (B, N), device=device, dtype=torch.int32,
+                           generator=torch.Generator(device=device).manual_seed(21))
     for b in range(B):
         sp.kv.append_tokens(b, N)
     desc = sp.kv.prepare_batch_metadata(list(range(B)))
@@ -194,7 +195,8 @@ def test_target_tree_forward_8b_width_vs_fp32(device):
     for b in range(B):
         sp.kv.truncate_sequence(b, sp.ctx[b])
     base = torch.tensor(sp.ctx, dtype=torch.int32, device=device)
-    tokens = torch.randint(0, shape.vocab, (B, N), device=device, dtype=torch.int32)
+    tokens = torch.randint(0, shape.vocab, (B, N), device=device, dtype=torch.int32,
+                           generator=torch.Generator(device=device).manual_seed(22))
     for b in range(B):
         sp.kv.append_tokens(b, N)
     desc = sp.kv.prepare_batch_metadata(list(range(B)))
