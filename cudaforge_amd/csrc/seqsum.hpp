@@ -49,6 +49,10 @@ constexpr int kAnyRegion = 0x7fff;        // an all-zero tile fits every region
 // every applied increment against the exact running value); the slack only
 // trades guesses near a power of two for serial replays.
 constexpr float kDelta = 1.0f / 65536.0f;
+// Tiles straddling a region boundary from which a wave is replayed as one
+// serial run instead of tile by tile: a crossing costs the tile-level walk
+// about 2K cycles, a serial replay of the wave's 1024 elements about 5K.
+constexpr int kSerialCrossings = 3;
 
 // Region index of s >= 0 (see above).  Zero and subnormals fall in -126.
 CFA_HD int region_of(float s) {
@@ -176,6 +180,7 @@ struct Shared {
   int16_t treg[NT];             // tile region guess
   Inc wI[kWaves];               // wave function or kBad
   int16_t wreg[kWaves];         // wave region
+  uint8_t wserial[kWaves];      // the wave crosses several regions: replay it serially
   float wscan[kWaves];          // block scan scratch
   float s;                      // exact running value at the current block entry
   long long found;              // first index with r <= s_i, or -1
@@ -336,6 +341,49 @@ __device__ long long walk(int count, float &s, bool cdf, float r, const Item &it
   return -1;
 }
 
+// Serial replay of wave w's 64 tiles (all lanes redundantly; the 16-byte
+// LDS reads are broadcasts, eight of them in flight ahead of the adds).
+template <int NT>
+__device__ long long serial_wave(const Shared<NT> &sh, int w, float &s, bool cdf, float r,
+                                 long long blk0) {
+  constexpr int kElems = 64 * Shared<NT>::kTile;
+  const float4 *x4 = reinterpret_cast<const float4 *>(sh.x + w * kElems);
+  const long long i0 = blk0 + (long long)w * kElems;
+  float acc = s;
+  for (int c = 0; c < kElems / 4; c += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = x4[c + j];
+    float ps[32];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc = acc + v[j].x;
+      ps[4 * j] = acc;
+      acc = acc + v[j].y;
+      ps[4 * j + 1] = acc;
+      acc = acc + v[j].z;
+      ps[4 * j + 2] = acc;
+      acc = acc + v[j].w;
+      ps[4 * j + 3] = acc;
+    }
+    if (cdf && r <= acc) {
+      // the first hit of this batch (static indices: no scratch array)
+      int k = 31;
+      float sk = ps[31];
+#pragma unroll
+      for (int q = 30; q >= 0; --q) {
+        const bool h = r <= ps[q];
+        k = h ? q : k;
+        sk = h ? ps[q] : sk;
+      }
+      s = sk;
+      return i0 + 4 * c + k;
+    }
+  }
+  s = acc;
+  return -1;
+}
+
 // Walk one staged block (wave 0 executes); updates sh.s / sh.found.
 template <int NT>
 __device__ void sweep_block(Shared<NT> &sh, long long blk0, bool cdf, float r) {
@@ -351,6 +399,7 @@ __device__ void sweep_block(Shared<NT> &sh, long long blk0, bool cdf, float r) {
     return sh.wI[i];
   };
   auto wave_desc = [&](int w, float &ss) -> long long {
+    if (sh.wserial[w]) return serial_wave(sh, w, ss, cdf, r, blk0);
     auto tile_item = [&sh, w](int i, int &reg) -> Inc {
       reg = sh.treg[w * 64 + i];
       return sh.tI[w * 64 + i];
@@ -441,6 +490,7 @@ __device__ float run(const XF &xf, long long n, bool cdf, float r, Shared<NT> &s
     sh.tI[tid] = f;
     sh.treg[tid] = (int16_t)r_lo;
     const unsigned long long okm = __ballot(ok);
+    const int crossings = __popcll(__ballot(!ok && A != 0.0f));
     // the wave's region: that of its first tile with a region (all-zero waves: any)
     const unsigned long long real = __ballot(r_lo != kAnyRegion);
     const int r0 = real ? (int)seq::lane_bcast((uint32_t)r_lo, (int)__builtin_ctzll(real)) : kAnyRegion;
@@ -450,6 +500,7 @@ __device__ float run(const XF &xf, long long n, bool cdf, float r, Shared<NT> &s
       const bool uni = (okm == ~0ull) && (same == ~0ull);
       sh.wI[wave] = uni ? wtot : Inc{kBad, kBad};
       sh.wreg[wave] = (int16_t)r0;
+      sh.wserial[wave] = crossings >= kSerialCrossings ? 1 : 0;
     }
     __syncthreads();
     if (wave == 0) sweep_block(sh, blk0, cdf, r);

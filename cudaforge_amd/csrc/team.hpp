@@ -219,6 +219,7 @@ __device__ void block_functions(seq::Shared<NT> &sh, float E) {
   sh.tI[tid] = f;
   sh.treg[tid] = (int16_t)r_lo;
   const unsigned long long okm = __ballot(ok);
+  const int crossings = __popcll(__ballot(!ok && A != 0.0f));
   const unsigned long long real = __ballot(r_lo != kAnyRegion);
   const int r0 = real ? (int)lane_bcast((uint32_t)r_lo, (int)__builtin_ctzll(real)) : kAnyRegion;
   const unsigned long long same = __ballot(r_lo == r0 || r_lo == kAnyRegion);
@@ -227,6 +228,7 @@ __device__ void block_functions(seq::Shared<NT> &sh, float E) {
     const bool uni = (okm == ~0ull) && (same == ~0ull);
     sh.wI[wave] = uni ? wtot : Inc{kBad, kBad};
     sh.wreg[wave] = (int16_t)r0;
+    sh.wserial[wave] = crossings >= kSerialCrossings ? 1 : 0;
   }
   __syncthreads();
 }
@@ -288,7 +290,7 @@ struct NoEarlyExit {
 // only needs a decision valid for every sum within the rounding bounds of
 // both summation orders can skip the exact walk.
 template <int NT, class XF, class Early = NoEarlyExit>
-__device__ float team_seq(Team &tm, Lds &tl, const XF &xf, long long n, bool cdf, float r,
+__device__ __attribute__((noinline)) float team_seq(Team &tm, Lds &tl, const XF &xf, long long n, bool cdf, float r,
                           seq::Shared<NT> &sh, long long *idx, const Early &early = Early()) {
   using namespace seq;
   constexpr int TILE = Shared<NT>::kTile;

@@ -45,6 +45,7 @@ namespace treev {
 
 constexpr int kNT = 1024;
 constexpr int kMaxN = 64;
+constexpr int kMaxU = 256;  // uniforms staged in LDS per sequence
 
 struct Args {
   const float *tgt;
@@ -124,7 +125,7 @@ __device__ __forceinline__ float f32_up(double v) {
 // it is accepted whatever the exact S is: the exact walk is skipped.
 struct SiblingAccepts {
   Resid r;  // r^(k)
-  int x;    // the sibling's token (valid)
+  float2 raw;  // the sibling token's raw (target, draft) values
   float u;  // its uniform
   long long n;
   __device__ bool operator()(float Sb, int depth) const {
@@ -135,8 +136,8 @@ struct SiblingAccepts {
     const float lo = f32_down((double)Sb * (1.0 - gn) / (1.0 + gd));
     const float hi = f32_up((double)Sb * (1.0 + gn) / (1.0 - gd));
     if (!(lo > 1e-6f) || !(hi < INFINITY)) return false;
-    const float p = r.eval(r.load(x));
-    const float q = r.d(x);
+    const float p = r.eval(raw);
+    const float q = r.d.eval(raw.y);
     const float ratio = ratio_cpp(relu_ref(p - q) / hi, q);
     return u <= ratio;
   }
@@ -153,6 +154,8 @@ struct __align__(16) Smem {
   float4 stat;  // (max, 1/sum) of the target and the draft row
   int amax;
   unsigned long long kids;
+  float2 raw[kMaxN];  // (target, draft) raw values of the current node's rows at each child's token
+  float uni[kMaxU];   // the sequence's uniforms (the first kMaxU)
 };
 
 __device__ __forceinline__ const float *trow(const Args &a, int b, int n) {
@@ -182,7 +185,7 @@ __device__ __forceinline__ void ms_merge(float &m1, float &s1, float m2, float s
 // (max, sum exp2((x - max) c)) of t[lo, hi) and of d[lo, hi) (d may be
 // NULL), block-wide, in a fixed order: (m_t, s_t, m_d, s_d).  Both rows'
 // loads are issued together.
-__device__ float4 slice_ms2(const Args &a, const float *t, const float *d, long long lo,
+__device__ __attribute__((noinline)) float4 slice_ms2(const Args &a, const float *t, const float *d, long long lo,
                             long long hi, Smem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float c = a.c;
@@ -374,8 +377,12 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
     sm.tk[tid] = a.tok[(long long)b * N + tid];
   }
   if (tid == 0) sm.path[0] = 0;
+  const float *Ug = a.U ? a.U + (long long)b * a.n_u : nullptr;
+  if (Ug)
+    for (int i = tid; i < min(a.n_u, kMaxU); i += kNT) sm.uni[i] = Ug[i];
   __syncthreads();
-  const float *U = a.U ? a.U + (long long)b * a.n_u : nullptr;
+  // draw i: from LDS when staged
+  auto U_at = [&](int i) -> float { return i < kMaxU ? sm.uni[i] : Ug[i]; };
   int node = 0, len = 1, draws = 0, fin = -1, eos_acc = 0, status = 0;
   for (;;) {
     // children of `node`, in increasing index order
@@ -391,7 +398,15 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
     const bool leaf = kids == 0;
     const float *tr = trow(a, b, node);
     const float *dr = (leaf || a.greedy) ? nullptr : drow(a, b, node);
+    // the rows' raw values at the children's tokens, loaded ahead of the
+    // statistics pass (thread c: child c; an invalid token reads index 0)
+    if (dr && tid < N && ((kids >> tid) & 1ull)) {
+      const int x = sm.tk[tid];
+      const int xs = (x >= 0 && x < V) ? x : 0;
+      sm.raw[tid] = make_float2(tr[xs], dr[xs]);
+    }
     if (a.logits) team_stats(a, tm, sm, tr, dr);
+    else __syncthreads();
     const float4 st = sm.stat;
     const Dist t = row_dist(a, tr, st.x, st.y);
     if (a.probs_t) write_probs(a, tm, t, a.probs_t + ((long long)b * N + node) * V);
@@ -404,7 +419,7 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
           break;
         }
         long long idx = -1;
-        team::team_seq<kNT>(tm, sm.tl, Resid{t, t, sm.Slist, 0}, V, true, U[draws++], sm.seq,
+        team::team_seq<kNT>(tm, sm.tl, Resid{t, t, sm.Slist, 0}, V, true, U_at(draws++), sm.seq,
                             &idx);
         fin = (idx < 0) ? V - 1 : (int)idx;
       }
@@ -433,15 +448,17 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
         const int x = sm.tk[c];
         const bool valid = x >= 0 && x < V;
         const int xs = valid ? x : 0;
+        (void)xs;
         const Resid r{t, d, sm.Slist, k};
-        const float p = r.eval(r.load(xs));  // r^(k)(x)
-        const float q = d(xs);
+        const float2 raw = sm.raw[c];
+        const float p = r.eval(raw);  // r^(k)(x)
+        const float q = d.eval(raw.y);
         const float ratio = valid ? ratio_cpp(p, q) : -1.0f;  // an out-of-range id never passes
         if (draws >= a.n_u) {
           status = 1;
           break;
         }
-        const float u = U[draws++];
+        const float u = U_at(draws++);
         if (u <= ratio) {
           accepted = c;
           break;
@@ -451,7 +468,7 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
         float S;
         if (rest && draws < a.n_u && sm.tk[__builtin_ctzll(rest)] >= 0 &&
             sm.tk[__builtin_ctzll(rest)] < V) {
-          const SiblingAccepts early{r, sm.tk[__builtin_ctzll(rest)], U[draws], (long long)V};
+          const SiblingAccepts early{r, sm.raw[__builtin_ctzll(rest)], U_at(draws), (long long)V};
           S = team::team_seq<kNT>(tm, sm.tl, ResidX{r}, V, false, 0.0f, sm.seq, nullptr, early);
           if (S < 0.0f) {  // the sibling is accepted for every S in the bounds
             accepted = __builtin_ctzll(rest);
@@ -474,7 +491,7 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
           break;
         }
         long long idx = -1;
-        team::team_seq<kNT>(tm, sm.tl, Resid{t, d, sm.Slist, k}, V, true, U[draws++], sm.seq,
+        team::team_seq<kNT>(tm, sm.tl, Resid{t, d, sm.Slist, k}, V, true, U_at(draws++), sm.seq,
                             &idx);
         fin = (idx < 0) ? V - 1 : (int)idx;
         break;

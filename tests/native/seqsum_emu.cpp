@@ -18,6 +18,7 @@ struct Emu {
   std::vector<int> treg;
   std::vector<Inc> wI;
   std::vector<int> wreg;
+  std::vector<int> wserial;
   long long serial_tiles = 0;
 
   long long serial_tile(int t, float &s, bool cdf, float r, long long blk0) {
@@ -72,10 +73,21 @@ struct Emu {
         [&](int L, float &ss) { return serial_tile(w * 64 + L, ss, cdf, r, blk0); });
   }
 
+  // a wave with several straddling tiles is replayed element by element
+  long long serial_wave(int w, float &s, bool cdf, float r, long long blk0) {
+    for (int k = 0; k < 64 * tile; ++k) {
+      s = s + x[(size_t)w * 64 * tile + k];
+      if (cdf && r <= s) return blk0 + (long long)w * 64 * tile + k;
+    }
+    return -1;
+  }
+
   long long sweep_block(float &s, bool cdf, float r, long long blk0) {
     return walk(
         nw, s, cdf, r, [&](int L) { return wI[L]; }, [&](int L) { return wreg[L]; },
-        [&](int L, float &ss) { return tile_sweep(L, ss, cdf, r, blk0); });
+        [&](int L, float &ss) {
+          return wserial[L] ? serial_wave(L, ss, cdf, r, blk0) : tile_sweep(L, ss, cdf, r, blk0);
+        });
   }
 };
 
@@ -94,6 +106,8 @@ extern "C" int emu_seq(const float *xin, long long n, int cdf, float r, int nt, 
   e.treg.resize(nt);
   e.wI.resize(e.nw);
   e.wreg.resize(e.nw);
+  e.wserial.resize(e.nw);
+  std::vector<int> straddle(nt);
   float s = 0.0f;
   long long found = -1;
   for (long long blk0 = 0; blk0 < n && found < 0; blk0 += blk) {
@@ -135,6 +149,7 @@ extern "C" int emu_seq(const float *xin, long long n, int cdf, float r, int nt, 
       }
       e.tI[t] = f;
       e.treg[t] = rlo;
+      straddle[t] = (!ok && A[t] != 0.0f) ? 1 : 0;
     }
     for (int w = 0; w < e.nw; ++w) {
       bool uni = true;
@@ -150,6 +165,9 @@ extern "C" int emu_seq(const float *xin, long long n, int cdf, float r, int nt, 
       }
       e.wI[w] = uni ? tot : Inc{kBad, kBad};
       e.wreg[w] = r0;
+      int crossings = 0;
+      for (int l = 0; l < 64; ++l) crossings += straddle[w * 64 + l];
+      e.wserial[w] = crossings >= kSerialCrossings ? 1 : 0;
     }
     found = e.sweep_block(s, cdf != 0, r, blk0);
   }
