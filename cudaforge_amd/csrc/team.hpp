@@ -1,7 +1,8 @@
-// team.hpp -- teams of work-groups inside one cooperative launch.
+// team.hpp -- teams of work-groups that work on one sequence together.
 //
-// A team is G <= 8 work-groups (all co-resident: the kernel is launched with
-// hipLaunchCooperativeKernel) that work on one sequence together.  Members
+// A team is G <= 8 work-groups of one launch, all resident at once (the
+// launch never holds more work-groups than the device runs together), that
+// work on one sequence together.  Members
 // take identical control-flow decisions from identical data, and meet at
 // team barriers.  Values crossing work-groups (which may sit on different
 // XCDs, whose L2s are not coherent with each other) are written with

@@ -21,8 +21,7 @@
 // verify_candidates.  Greedy: a child is accepted iff its token is the first
 // argmax of p_node; none accepted -> final = that argmax (:105-150).
 //
-// A team of G <= 8 work-groups per sequence (one cooperative launch; team.hpp)
-// walks its tree: each visited row's softmax statistics (logits input) are
+// A team of G <= 8 work-groups per sequence (team.hpp) walks its tree: each visited row's softmax statistics (logits input) are
 // reduced over the team, each member reading its slice of the row, so only
 // visited rows are read; every residual sum and inverse CDF is the exact
 // sequential fp32 replay of seqsum.hpp split over the team (team_seq), with
@@ -32,6 +31,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 #include "abi_internal.hpp"
 #include "dist.hpp"
@@ -540,7 +540,7 @@ __global__ __launch_bounds__(kNT) void tree_verify_kernel(Args a) {
   }
 }
 
-// Zero the teams' state before the cooperative launch.
+// Zero the teams' state before the launch.
 __global__ __launch_bounds__(256) void clear_kernel(uint4 *p, long long n) {
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256)
     p[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -579,6 +579,14 @@ int kernel_per_cu() {
   return cache[dev];
 }
 constexpr size_t kErrBytes = 256;
+
+bool cooperative_launch() {
+  static const bool on = [] {
+    const char *v = std::getenv("CFA_COOPERATIVE_LAUNCH");
+    return v != nullptr && v[0] == '1';
+  }();
+  return on;
+}
 }  // namespace
 
 extern "C" size_t cfa_tree_verify_workspace_size(int B) {
@@ -662,12 +670,26 @@ extern "C" int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t 
   CFA_LAUNCH("tree_verify_clear", treev::clear_kernel,
              dim3((unsigned)std::min<long long>((words + 255) / 256, 1024)), dim3(256), 0, st,
              (uint4 *)workspace, words);
-  // every team's members must be resident together: a cooperative launch
-  void *tok = prof::enabled() ? prof::begin("tree_verify", st) : nullptr;
-  void *args[] = {&a};
-  const hipError_t e = hipLaunchCooperativeKernel((const void *)treev::tree_verify_kernel,
-                                                  dim3(pl.T * pl.G), dim3(treev::kNT), args, 0, st);
-  if (tok) prof::end(tok, st);
-  if (e != hipSuccess) return fail_hip(e, "tree_verify (cooperative launch)");
+  // A team's members must be resident together.  plan() never asks for more
+  // work-groups than the device holds at once for this kernel (occupancy
+  // query), so on a device running no other kernel every member is resident
+  // from the start; kernels of other streams can only delay a member, and one
+  // delayed past the bounded wait makes its team report status 2.
+  // hipLaunchCooperativeKernel guarantees residency, but measured on MI355X
+  // (ROCm 7) it leaves the process's later dispatches slower for a while
+  // (~15 us added to each; the 8B-shape target forward that follows it:
+  // 15.3 -> 24.5 ms), and the kernel itself runs slower (B = 8: 0.34 against
+  // 0.21 ms), so it is taken only when CFA_COOPERATIVE_LAUNCH=1.
+  const dim3 grid((unsigned)(pl.T * pl.G));
+  if (cooperative_launch()) {
+    void *tok = prof::enabled() ? prof::begin("tree_verify", st) : nullptr;
+    void *args[] = {&a};
+    const hipError_t e = hipLaunchCooperativeKernel((const void *)treev::tree_verify_kernel, grid,
+                                                    dim3(treev::kNT), args, 0, st);
+    if (tok) prof::end(tok, st);
+    if (e != hipSuccess) return fail_hip(e, "tree_verify (cooperative launch)");
+  } else {
+    CFA_LAUNCH("tree_verify", treev::tree_verify_kernel, grid, dim3(treev::kNT), 0, st, a);
+  }
   return CFA_OK;
 }

@@ -309,7 +309,8 @@ def tree_verify(target: torch.Tensor, draft: Optional[torch.Tensor], parents: to
     parents[0] = -1; node_tokens [B, N] int32; uniforms [B, n_u] fp32 (cpp mode).
     workspace: optional uint8 device tensor of tree_verify_workspace_bytes(B).
     status: 0 ok, 1 the uniform stream ran out, 2 a wait between the
-    work-groups of a sequence timed out (raised as RuntimeError by
+    work-groups of a sequence timed out -- kernels of other streams held one
+    of them back; run the call again (raised as RuntimeError by
     check_status).
     """
     if mode not in ("cpp", "greedy"):

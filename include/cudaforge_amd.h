@@ -232,8 +232,13 @@ int cfa_tree_attention(const void *q, const void *k_pool, const void *v_pool,
  * out_target_probs / out_draft_probs (optional, [B, N, V]) receive the
  * probabilities of the rows the walk visited.
  *
- * Up to 8 work-groups share each sequence (one cooperative launch: they
- * exchange row statistics and split every exact pass); workspace is
+ * Up to 8 work-groups share each sequence (they exchange row statistics and
+ * split every exact pass, so they must run together: the launch never holds
+ * more work-groups than the device runs at once, and kernels of other streams
+ * can only delay a member -- past the bounded wait, status 2; environment
+ * CFA_COOPERATIVE_LAUNCH=1 launches with hipLaunchCooperativeKernel, which
+ * guarantees residency but slows this call and the process's next
+ * dispatches); workspace is
  * cfa_tree_verify_workspace_size(B) bytes, 256-byte aligned, holding their
  * barrier and exchange state (cleared by the call itself).  Calls sharing a
  * workspace must not overlap.
