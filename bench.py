@@ -75,14 +75,21 @@ def make_inputs(dev, seed):
 
 
 def _cpu_model() -> str:
+    """/proc/cpuinfo's model name with its family / model / stepping numbers
+    (virtual machines often report only "AMD EPYC" as the name)."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    return ln.split(":", 1)[1].strip()
+                if not ln.strip():
+                    break                      # first processor only
+                k, _, v = ln.partition(":")
+                info[k.strip()] = v.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    ids = [f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def _timed(fn, budget_s):

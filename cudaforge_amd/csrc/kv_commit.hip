@@ -17,7 +17,8 @@
 // it; a batch of rows is read before the batch is written.  One work-group
 // per (sequence, layer) checks the path once, one thread per entry.  Rows
 // with path[j] == j (the root, and any prefix of a chain) are already in
-// place and are neither read nor written.
+// place and are neither read nor written; the others are compacted in path
+// order, so the batches hold only rows that move.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -53,25 +54,39 @@ __device__ __forceinline__ long long slot_base(const Args &a, int b, int pos) {
 }
 
 constexpr int kBatch = 8;  // rows held in registers per thread at a time
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(kNT) void commit_kernel(Args a) {
-  __shared__ long long src[kMaxPath], dst[kMaxPath];
+  __shared__ long long src[kMaxPath], dst[kMaxPath];  // the rows that move, in path order
+  __shared__ int n_moves;
   const int layer = blockIdx.x, b = blockIdx.y;
   const int ctx = a.ctx[b];
   const int L = a.plen[b];
   const int32_t *p = a.paths + (long long)b * a.path_stride;
-  // path check, one thread per entry: 1 <= L <= kMaxPath, path[0] == 0,
-  // strictly increasing, every source and destination slot mapped
+  // path check, one thread per entry of wave 0 (L <= 64): 1 <= L <= kMaxPath,
+  // path[0] == 0, strictly increasing, every source and destination slot
+  // mapped; the entries with path[j] != j are then compacted in order
   bool good = true;
   const bool shape_ok = L >= 1 && L <= kMaxPath && L <= a.path_stride && ctx >= 0;
-  if (shape_ok && threadIdx.x < L) {
+  if (threadIdx.x < 64) {
     const int j = threadIdx.x;
-    const int pj = p[j];
-    good = (j == 0) ? (pj == 0) : (pj > p[j - 1]);
-    const long long so = slot_base(a, b, ctx + pj), d = slot_base(a, b, ctx + j);
-    good = good && so >= 0 && d >= 0;
-    src[j] = (pj == j) ? -1 : so;  // -1: already in place
-    dst[j] = d;
+    bool moves = false;
+    long long so = -1, d = -1;
+    if (shape_ok && j < L) {
+      const int pj = p[j];
+      good = (j == 0) ? (pj == 0) : (pj > p[j - 1]);
+      so = slot_base(a, b, ctx + pj);
+      d = slot_base(a, b, ctx + j);
+      good = good && so >= 0 && d >= 0;
+      moves = pj != j;
+    }
+    const unsigned long long m = __ballot(moves);
+    if (moves) {
+      const int at = __popcll(m & ((1ull << j) - 1ull));
+      src[at] = so;
+      dst[at] = d;
+    }
+    if (j == 0) n_moves = __popcll(m);
   }
   const bool ok = __syncthreads_and(good ? 1 : 0) && shape_ok;
   if (layer == 0 && threadIdx.x == 0) {
@@ -79,6 +94,7 @@ __global__ __launch_bounds__(kNT) void commit_kernel(Args a) {
     if (a.new_ctx) a.new_ctx[b] = ok ? ctx + L : ctx;
   }
   if (!ok) return;
+  const int M = n_moves;
   const int cpr = a.row_bytes / 16;  // 16-byte chunks per row
   const long long head_stride = (long long)a.bs * a.row_bytes;
   const long long layer_off = (long long)layer * a.Hkv * head_stride;
@@ -86,16 +102,19 @@ __global__ __launch_bounds__(kNT) void commit_kernel(Args a) {
     const int kv = col / (a.Hkv * cpr), h = (col / cpr) % a.Hkv, c = col % cpr;
     uint8_t *pool = kv ? a.vpool : a.kpool;
     const long long off = layer_off + h * head_stride + 16LL * c;
-    for (int j0 = 0; j0 < L; j0 += kBatch) {
-      uint4 v[kBatch];
+    for (int j0 = 0; j0 < M; j0 += kBatch) {
+      // every load of a batch before any store of it; past the last move a
+      // batch repeats that move (the same bytes to the same place), so that
+      // loads and stores are unconditional and the batch stays in registers
+      // (a clang vector type: an array of HIP's uint4 struct is kept in
+      // scratch memory by the compiler)
+      u32x4 v[kBatch];
 #pragma unroll
       for (int q = 0; q < kBatch; ++q)
-        if (j0 + q < L && src[j0 + q] >= 0)
-          v[q] = *reinterpret_cast<const uint4 *>(pool + src[j0 + q] + off);
+        v[q] = *reinterpret_cast<const u32x4 *>(pool + src[min(j0 + q, M - 1)] + off);
 #pragma unroll
       for (int q = 0; q < kBatch; ++q)
-        if (j0 + q < L && src[j0 + q] >= 0)
-          *reinterpret_cast<uint4 *>(pool + dst[j0 + q] + off) = v[q];
+        *reinterpret_cast<u32x4 *>(pool + dst[min(j0 + q, M - 1)] + off) = v[q];
     }
   }
 }
