@@ -40,24 +40,31 @@ TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic_per_dispatch.md")
 
 def traffic_from_profile(kernel: str):
     """HBM bytes (read + written) per dispatch of `kernel` from the counter
-    table in profiles/hbm_traffic_per_dispatch.md (columns "HBM bytes read"
-    and "HBM bytes written"); None when the table has no such row."""
+    table in profiles/hbm_traffic_per_dispatch.md (the table whose header has
+    columns "HBM bytes read" and "HBM bytes written"); None when there is no
+    such row."""
     try:
         with open(TRAFFIC_TABLE) as f:
-            lines = [ln.strip() for ln in f if ln.strip().startswith("|")]
+            lines = [ln.strip() for ln in f]
     except OSError:
         return None
-    if not lines:
-        return None
-    head = [c.strip() for c in lines[0].strip("|").split("|")]
-    try:
+
+    def cells(ln):
+        return [c.strip() for c in ln.strip("|").split("|")]
+
+    for i, ln in enumerate(lines):
+        if not ln.startswith("|"):
+            continue
+        head = cells(ln)
+        if "HBM bytes read" not in head or "HBM bytes written" not in head:
+            continue
         ir, iw = head.index("HBM bytes read"), head.index("HBM bytes written")
-    except ValueError:
-        return None
-    for ln in lines[2:]:
-        cells = [c.strip() for c in ln.strip("|").split("|")]
-        if cells and cells[0].strip("`") == kernel:
-            return int(cells[ir].replace(",", "")) + int(cells[iw].replace(",", ""))
+        for row in lines[i + 2:]:
+            if not row.startswith("|"):
+                break
+            c = cells(row)
+            if c[0].strip("`") == kernel:
+                return int(c[ir].replace(",", "")) + int(c[iw].replace(",", ""))
     return None
 
 
