@@ -320,96 +320,133 @@ __device__ int row_argmax(const Args &a, int r) {
 
 constexpr int kMaxK = 64;
 
-__device__ void write_job(const Args &a, int b, int n, int kind, int row, int eos_acc, float u,
-                          int extra = 0, float u2 = 0.0f);
+struct DecideLds;
+__device__ MwJob make_job(const Args &a, int b, int n, int kind, int row, int eos_acc, float u,
+                         int extra = 0, float u2 = 0.0f, const DecideLds *L = nullptr);
+__device__ void write_job(const Args &a, int b, const MwJob &j);
 
-__global__ __launch_bounds__(64) void decide_kernel(Args a) {
-  const int b = blockIdx.x, lane = threadIdx.x;
-  __shared__ float pt[kMaxK], qd[kMaxK];
-  __shared__ int tk[kMaxK], am[kMaxK + 1], ok[kMaxK];
+// The decision's inputs, gathered by a work-group of nt threads: the draft
+// tokens and p(tok), q(tok) at every position with the statistics of every
+// row of the sequence (or, greedy, the first argmax of every target row),
+// and the sequence's uniforms.  One thread per row, so a row's partials and
+// its value at the token are two rounds of loads for the whole gather.
+struct DecideLds {
+  float pt[kMaxK], qd[kMaxK];
+  int tk[kMaxK], am[kMaxK + 1], ok[kMaxK];
+  float2 st[2 * kMaxK + 1];  // (max, 1/S) of rows 0 .. 2K (logits input)
+  float u[kMaxK + 2];
+};
+
+__device__ void decide_gather(const Args &a, int b, int tid, int nt, DecideLds &L) {
   const int K = a.K;
-  for (int i = lane; i < K; i += 64) {
-    int t = a.tokens[(long long)b * K + i];
-    tk[i] = t;
-    t = min(max(t, 0), a.V - 1);  // never read outside the row
-    if (a.mode != CFA_MODE_GREEDY) {
-      const bool valid = (a.tokens[(long long)b * K + i] == t);
-      const Dist dt = make_dist(a, b, i);
-      const Dist dd = make_dist(a, b, K + 1 + i);
-      pt[i] = valid ? dt(t) : 0.0f;
-      qd[i] = valid ? dd(t) : 0.0f;
-      ok[i] = valid ? 1 : 0;  // an id outside [0, V) is never accepted
-    }
+  if (a.mode == CFA_MODE_GREEDY) {
+    for (int i = tid; i < K; i += nt) L.tk[i] = a.tokens[(long long)b * K + i];
+    for (int i = tid; i <= K; i += nt) L.am[i] = row_argmax(a, (b / a.draws) * a.rpb + i);
+    return;
   }
-  if (a.mode == CFA_MODE_GREEDY)
-    for (int i = lane; i <= K; i += 64) am[i] = row_argmax(a, (b / a.draws) * a.rpb + i);
-  __syncthreads();
-  if (lane != 0) return;
-  const float *U = a.U + (long long)b * a.ustride;
-  int n = 0, kind = kNone, row = -1, eos_acc = 0;
-  float uf = 0.0f;
-  if (a.mode == CFA_MODE_CPP) {
-    int draws = 0;
-    for (int i = 0; i < K; ++i) {
-      const float ratio = ratio_cpp(pt[i], qd[i]);
-      const float r = U[draws++];
-      if (ok[i] && r <= ratio) {
-        ++n;
-        if (tk[i] == a.eos) {
-          eos_acc = 1;
-          break;
-        }
+  // rows 0 .. K-1 target at a draft position, K the target's last row,
+  // K+1 .. 2K draft
+  for (int r = tid; r < 2 * K + 1; r += nt) {
+    const int i = r <= K ? r : r - K - 1;
+    const int traw = (r != K) ? a.tokens[(long long)b * K + i] : 0;
+    const Dist d = make_dist(a, b, r);
+    L.st[r] = make_float2(d.M, d.invS);
+    if (r != K) {
+      const int t = min(max(traw, 0), a.V - 1);  // never read outside the row
+      const bool valid = traw == t;                // an id outside [0, V) is never accepted
+      const float v = valid ? d(t) : 0.0f;
+      if (r < K) {
+        L.pt[i] = v;
+        L.tk[i] = traw;
+        L.ok[i] = valid ? 1 : 0;
       } else {
-        kind = kResid;
-        row = i;
-        uf = U[draws++];
-        break;
+        L.qd[i] = v;
       }
     }
-    if (!eos_acc && kind == kNone) {
-      kind = kPlain;
-      row = K;
-      uf = U[draws++];
+  }
+  const int nu = min(a.ustride, kMaxK + 2);
+  for (int i = tid; i < nu; i += nt) L.u[i] = a.U[(long long)b * a.ustride + i];
+}
+
+// cpp rules (speculative.cpp:66-97), one thread: the acceptance walk on the
+// sequence's uniforms and the draw it still needs.
+__device__ MwJob decide_cpp(const Args &a, int b, const DecideLds &L) {
+  const int K = a.K;
+  int n = 0, kind = kNone, row = -1, eos_acc = 0, draws = 0;
+  float uf = 0.0f;
+  for (int i = 0; i < K; ++i) {
+    const float ratio = ratio_cpp(L.pt[i], L.qd[i]);
+    const float r = L.u[draws++];
+    if (L.ok[i] && r <= ratio) {
+      ++n;
+      if (L.tk[i] == a.eos) {
+        eos_acc = 1;
+        break;
+      }
+    } else {
+      kind = kResid;
+      row = i;
+      uf = L.u[draws++];
+      break;
     }
-  } else if (a.mode == CFA_MODE_PYTHON) {
+  }
+  if (!eos_acc && kind == kNone) {
+    kind = kPlain;
+    row = K;
+    uf = L.u[draws++];
+  }
+  return make_job(a, b, n, kind, row, eos_acc, uf, 0, 0.0f, &L);
+}
+
+// One work-group per sequence.  cpp mode runs this only where the exact
+// draw is not needed (the mw sums kernel decides otherwise); python mode
+// records n_b for plan_kernel; greedy writes the final outputs.
+__global__ __launch_bounds__(64) void decide_kernel(Args a) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  __shared__ DecideLds L;
+  const int K = a.K;
+  decide_gather(a, b, lane, 64, L);
+  __syncthreads();
+  if (lane != 0) return;
+  if (a.mode == CFA_MODE_CPP) {
+    write_job(a, b, decide_cpp(a, b, L));
+    return;
+  }
+  int n = 0, eos_acc = 0;
+  if (a.mode == CFA_MODE_PYTHON) {
     n = K;
     for (int i = 0; i < K; ++i)
-      if (!(U[i] < ratio_py(pt[i], qd[i]))) {
+      if (!(L.u[i] < ratio_py(L.pt[i], L.qd[i]))) {
         n = i;
         break;
       }
-    uf = U[K];
-  } else {  // greedy: outputs are final here
-    int fin = -1;
-    for (int i = 0; i < K; ++i) {
-      if (tk[i] == am[i]) {
-        ++n;
-        if (tk[i] == a.eos) {
-          eos_acc = 1;
-          fin = a.eos;
-          break;
-        }
-      } else {
-        fin = am[i];
-        break;
-      }
-    }
-    if (!eos_acc && n == K) fin = am[K];
-    int32_t *ot = a.out_tokens + (long long)b * (K + 1);
-    for (int j = 0; j <= K; ++j) ot[j] = (j < n) ? tk[j] : -1;
-    if (!eos_acc) ot[n] = fin;
-    a.out_accept_len[b] = n;
-    a.out_final[b] = fin;
-    a.out_eos[b] = (eos_acc || fin == a.eos) ? 1 : 0;
-    a.out_num_emitted[b] = eos_acc ? n : n + 1;
+    a.dec[b] = make_int4(n, kNone, -1, 0);
+    a.ufin[b] = L.u[K];
     return;
   }
-  if (a.mode == CFA_MODE_CPP) {
-    write_job(a, b, n, kind, row, eos_acc, uf);
-  } else {
-    a.dec[b] = make_int4(n, kind, row, eos_acc);
-    a.ufin[b] = uf;
+  // greedy: outputs are final here
+  int fin = -1;
+  for (int i = 0; i < K; ++i) {
+    if (L.tk[i] == L.am[i]) {
+      ++n;
+      if (L.tk[i] == a.eos) {
+        eos_acc = 1;
+        fin = a.eos;
+        break;
+      }
+    } else {
+      fin = L.am[i];
+      break;
+    }
   }
+  if (!eos_acc && n == K) fin = L.am[K];
+  int32_t *ot = a.out_tokens + (long long)b * (K + 1);
+  for (int j = 0; j <= K; ++j) ot[j] = (j < n) ? L.tk[j] : -1;
+  if (!eos_acc) ot[n] = fin;
+  a.out_accept_len[b] = n;
+  a.out_final[b] = fin;
+  a.out_eos[b] = (eos_acc || fin == a.eos) ? 1 : 0;
+  a.out_num_emitted[b] = eos_acc ? n : n + 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -523,10 +560,9 @@ __device__ __forceinline__ float py_threshold(float u) {
 
 // The job of sequence b: its draw (n, kind, row, eos_acc, threshold u; a
 // python-mode bonus after the resample when extra) and the statistics of the
-// draw's rows, once for every kernel that reads them; also resets the walk
-// state of b.
-__device__ void write_job(const Args &a, int b, int n, int kind, int row, int eos_acc, float u,
-                          int extra, float u2) {
+// draw's rows, once for every kernel that reads them.
+__device__ MwJob make_job(const Args &a, int b, int n, int kind, int row, int eos_acc, float u,
+                         int extra, float u2, const DecideLds *L) {
   const int K = a.K;
   MwJob j;
   j.n = n;
@@ -540,22 +576,28 @@ __device__ void write_job(const Args &a, int b, int n, int kind, int row, int eo
   j.tM = j.dM = 0.0f;
   j.tInvS = j.dInvS = 1.0f;
   if (a.logits && (j.kind == kResid || j.kind == kPlain)) {
-    const float2 ts = row_stat(a, (b / a.draws) * a.rpb + j.row);
+    // the rows' statistics, from the gather when it has them
+    const float2 ts = L ? L->st[j.row] : row_stat(a, (b / a.draws) * a.rpb + j.row);
     j.tM = ts.x;
     j.tInvS = ts.y;
     if (j.kind == kResid) {
-      const float2 ds = row_stat(a, (b / a.draws) * a.rpb + K + 1 + j.row);
+      const float2 ds = L ? L->st[K + 1 + j.row] : row_stat(a, (b / a.draws) * a.rpb + K + 1 + j.row);
       j.dM = ds.x;
       j.dInvS = ds.y;
     }
   }
+  return j;
+}
+
+// Store the job and reset the walk state of b.
+__device__ void write_job(const Args &a, int b, const MwJob &j) {
   a.jobs[b] = j;
   a.res[b] = MwRes{0.0f, 0, -1, -1};
   a.badcnt[b] = 0;
   a.badcnt[a.B + b] = 0;
 }
 
-// Python mode only (cpp mode writes its jobs in decide).
+// Python mode only (cpp mode decides each sequence's draw by itself).
 __global__ __launch_bounds__(256) void plan_kernel(Args a) {
   __shared__ int nmin;
   const int K = a.K;
@@ -571,8 +613,8 @@ __global__ __launch_bounds__(256) void plan_kernel(Args a) {
   const int extra = (K > 0 && nmin == K - 1) ? 1 : 0;
   for (int b = threadIdx.x; b < a.B; b += blockDim.x) {
     const float u2 = extra ? py_threshold(a.U[(long long)b * a.ustride + K + 1]) : 0.0f;
-    write_job(a, b, nmin, (nmin < K) ? kResid : kPyBonus, (nmin < K) ? nmin : K, 0,
-              py_threshold(a.ufin[b]), extra, u2);
+    write_job(a, b, make_job(a, b, nmin, (nmin < K) ? kResid : kPyBonus, (nmin < K) ? nmin : K, 0,
+                             py_threshold(a.ufin[b]), extra, u2));
   }
 }
 
@@ -684,10 +726,27 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
 }
 
 // One wave per chunk: chunk c = 4 * blockIdx.x + wave, lane = tile in chunk.
-__global__ __launch_bounds__(kMwNT) void mw_sums_kernel(Args a) {
+// With `decide` (cpp rules) every work-group first takes sequence b's
+// decision itself (decide_cpp: the same inputs, so the same job everywhere)
+// and the first one stores it, which saves the separate decide launch.
+__global__ __launch_bounds__(kMwNT) void mw_sums_kernel(Args a, int decide) {
   const int b = blockIdx.y, lane = threadIdx.x & 63;
   const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
-  const MwJob j = a.jobs[b];
+  MwJob j;
+  if (decide) {
+    __shared__ DecideLds L;
+    __shared__ MwJob sj;
+    decide_gather(a, b, threadIdx.x, kMwNT, L);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      sj = decide_cpp(a, b, L);
+      if (blockIdx.x == 0) write_job(a, b, sj);
+    }
+    __syncthreads();
+    j = sj;
+  } else {
+    j = a.jobs[b];
+  }
   if (j.kind != kResid && j.kind != kPlain) return;
   if (c >= a.NC) return;
   const MwElem e = mw_elem(a, b, j, kPassSum);
@@ -1425,11 +1484,13 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   }
   if (mode == CFA_MODE_GREEDY)
     CFA_LAUNCH("chain_argmax", (argmax_kernel<256>), dim3(a.G), dim3(256), 0, st, a);
-  CFA_LAUNCH("chain_decide", decide_kernel, dim3(B), dim3(64), 0, st, a);
+  // cpp rules: the mw sums kernel takes each sequence's decision itself
+  const int fused_decide = mode == CFA_MODE_CPP ? 1 : 0;
+  if (!fused_decide) CFA_LAUNCH("chain_decide", decide_kernel, dim3(B), dim3(64), 0, st, a);
   if (mode != CFA_MODE_GREEDY) {
     const dim3 cg((a.NC + kMwNT / 64 - 1) / (kMwNT / 64), B);
     if (mode == CFA_MODE_PYTHON) CFA_LAUNCH("chain_plan", plan_kernel, dim3(1), dim3(256), 0, st, a);
-    CFA_LAUNCH("chain_mw_sums", mw_sums_kernel, cg, dim3(kMwNT), 0, st, a);
+    CFA_LAUNCH("chain_mw_sums", mw_sums_kernel, cg, dim3(kMwNT), 0, st, a, fused_decide);
     CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassSum);
     CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassSum);
     CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassCdf);

@@ -201,32 +201,32 @@ __device__ __attribute__((noinline)) float4 slice_ms2(const Args &a, const float
          __builtin_amdgcn_exp2f((v2 - ms) * c) + __builtin_amdgcn_exp2f((v3 - ms) * c);
   };
   if (a.vec) {
-    // 16-byte loads; lo and hi are multiples of 4 (a.vec implies V % 4 == 0)
-    const float4 *t4 = reinterpret_cast<const float4 *>(t + lo);
-    const float4 *d4 = d ? reinterpret_cast<const float4 *>(d + lo) : t4;
+    // 16-byte loads; lo and hi are multiples of 4 (a.vec implies V % 4 == 0).
+    // Every round issues all U loads of each row before the first use (a
+    // lane past the slice end reloads the last vector and skips it), so a
+    // slice of up to U * kNT vectors costs one load latency, not one per
+    // vector a lane owns.
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 *t4 = reinterpret_cast<const f32x4 *>(t + lo);
+    const f32x4 *d4 = d ? reinterpret_cast<const f32x4 *>(d + lo) : t4;
     const int n4 = (int)((hi - lo) / 4);
     constexpr int U = 4;
-    int i = tid;
-    for (; i + (U - 1) * kNT < n4; i += U * kNT) {
-      float4 vt[U], vd[U];
+    for (int i0 = 0; i0 < n4; i0 += U * kNT) {
+      f32x4 vt[U], vd[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) vt[u] = t4[i + u * kNT];
+      for (int u = 0; u < U; ++u) vt[u] = t4[min(i0 + u * kNT + tid, n4 - 1)];
       if (d) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) vd[u] = d4[i + u * kNT];
+        for (int u = 0; u < U; ++u) vd[u] = d4[min(i0 + u * kNT + tid, n4 - 1)];
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u) update(mt, st, vt[u].x, vt[u].y, vt[u].z, vt[u].w);
+      for (int u = 0; u < U; ++u)
+        if (i0 + u * kNT + tid < n4) update(mt, st, vt[u][0], vt[u][1], vt[u][2], vt[u][3]);
       if (d) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) update(md, sd, vd[u].x, vd[u].y, vd[u].z, vd[u].w);
+        for (int u = 0; u < U; ++u)
+          if (i0 + u * kNT + tid < n4) update(md, sd, vd[u][0], vd[u][1], vd[u][2], vd[u][3]);
       }
-    }
-    for (; i < n4; i += kNT) {
-      const float4 vt = t4[i];
-      const float4 vd = d4[i];
-      update(mt, st, vt.x, vt.y, vt.z, vt.w);
-      if (d) update(md, sd, vd.x, vd.y, vd.z, vd.w);
     }
   } else {
     auto upd1 = [c](float &m, float &s, float v) {
