@@ -33,7 +33,19 @@ B, K, V, T = 64, 8, 128256, 0.7
 SIGMA, NOISE = 2.0, 0.5
 NSETS = 4
 # algorithmic bytes of one step: target [B,K+1,V] + draft [B,K,V] logits, read once
-ALG_BYTES = B * (2 * K + 1) * V * 4
+ALG_BYTES = B * (2 * K + 1) * V * 4   # every logit of both windows
+# Under the per-sequence rules with logits, the library reads the rows of
+# positions 0 .. HEAD-1 of every sequence first, and the other rows (the
+# remaining positions and the target's row K) only for sequences that
+# accepted all HEAD of them (kHeadPositions in csrc/chain_verify.hip).
+HEAD_POSITIONS = 3
+
+
+def stats_rows(accept_len) -> int:
+    """Rows the two statistics passes read in one step, given the step's
+    accepted-draft counts: each of them read once."""
+    pending = int((accept_len >= HEAD_POSITIONS).sum())
+    return B * 2 * HEAD_POSITIONS + pending * (2 * (K - HEAD_POSITIONS) + 1)
 # per-dispatch HBM traffic measured with rocprofv3 --pmc for this build
 TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic_per_dispatch.md")
 
@@ -437,9 +449,11 @@ def main() -> int:
         return chain_verify(tl, dl, tok, U, input_kind="logits", temperature=T, mode="cpp",
                             workspace=ws)
 
-    emitted = []
+    emitted, rows = [], []
     for s in range(NSETS):
-        emitted.append(int(step(s).num_emitted.sum().item()))
+        o = step(s)
+        emitted.append(int(o.num_emitted.sum().item()))
+        rows.append(stats_rows(o.accept_len.cpu().numpy()))
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -470,14 +484,19 @@ def main() -> int:
     _lib.profile_enable(False)
 
     kern = {}
-    for name in ("chain_stats", "chain_decide", "chain_plan", "chain_mw_sums", "chain_mw_records",
-                 "chain_mw_walk", "chain_finish"):
+    for name in ("chain_stats_head", "chain_stats_tail", "chain_decide", "chain_plan",
+                 "chain_mw_sums", "chain_mw_records", "chain_mw_walk", "chain_finish"):
         n, ms = _lib.profile_query(name)
         kern[name] = ms / args.steps  # per step (records and walk run twice)
     _lib.profile_reset()
-    stats_ms = kern["chain_stats"]  # one launch per step
-    achieved = ALG_BYTES / (stats_ms * 1e-3) / 1e9
+    # the statistics passes: the logits of their rows, each read once
+    stats_bytes = sum(rows[i % NSETS] for i in range(args.steps)) / args.steps * V * 4
+    stats_ms = kern["chain_stats_head"] + kern["chain_stats_tail"]
+    achieved = stats_bytes / (stats_ms * 1e-3) / 1e9
+    # the whole step on the workload's algorithmic bytes (every logit once)
     step_gbs = ALG_BYTES / (ms_per_step * 1e-3) / 1e9
+    head_t = traffic_from_profile("cfa::chain::stats_kernel<256, 4> (head)")
+    tail_t = traffic_from_profile("cfa::chain::stats_kernel<256, 4> (tail)")
 
     line = {
         "metric": METRIC,
@@ -496,10 +515,12 @@ def main() -> int:
                                "(BASELINE configs[1]); per-sequence rules",
                    "B": B, "K": K, "V": V, "temperature": T, "input": "fp32 logits",
                    "mean_accept_len": round(sum(emitted) / (NSETS * B) - 1, 3)},
-        "roofline": {"bound": "hbm", "kernel": "chain_stats",
+        "roofline": {"bound": "hbm", "kernel": "chain_stats (head + tail passes)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profile("cfa::chain::stats_kernel<256, 4>"),
+                     "traffic": (head_t + tail_t) if head_t and tail_t else None,
+                     "algorithmic_bytes": int(stats_bytes),
+                     "logits_read_frac": round(stats_bytes / ALG_BYTES, 4),
                      "step_achieved": round(step_gbs, 1),
                      "step_frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "kernels_ms_per_step": {k: round(v, 5) for k, v in kern.items()},

@@ -90,12 +90,12 @@ struct Args {
   int eos;
   float top_p;
   int top_k;              // > 0: keep only probabilities >= the top_k-th largest
-  // partition of the stats / argmax passes
+  // partition of the stats / argmax passes: every row in S fixed slices
   long long Vw;  // row length in vector units
-  long long C;   // units per work-group
-  int G;         // work-groups
-  float2 *part;  // [G*2] (max logit, sum exp) per (wg, row slot)
-  float2 *apart; // [G*2] (max prob, index as bits) per (wg, row slot)
+  int S;         // slices per row (a function of the shape only)
+  int P;         // cpp rules, logits: positions whose rows the first stats pass reads
+  float2 *part;  // [R, S] (max logit, sum exp) per (row, slice)
+  float2 *apart; // [R, S] (max prob, index as bits) per (row, slice)
   int4 *dec;     // [B] {n_b, kind, row, eos_accepted}
   float *ufin;   // [B]
   // exact multi-work-group sampler (see "mw" below)
@@ -109,6 +109,7 @@ struct Args {
   int *badcnt;            // [2, B]
   MwBad *bad;             // [2, B, kMwMaxBad]
   float *x0;              // [2, B, kMwChunk] chunk 0's element values per pass
+  float *rawtok;          // [R] head pass: a row's raw logit at its position's draft token
   int32_t *out_accept_len, *out_tokens, *out_num_emitted, *out_final, *out_eos;
 };
 
@@ -122,19 +123,15 @@ __device__ __forceinline__ const float *row_ptr(const Args &a, int b, int j) {
   return row_ptr_u(a, b / a.draws, j);
 }
 
-// (max, 1/S) of row r from the stats partials, combined in a fixed order.
+// (max, 1/S) of row r from its slices' partials, combined in slice order
+// (the same for whichever pass computed the row).
 __device__ float2 row_stat(const Args &a, int r) {
-  const long long lo = (long long)r * a.Vw, hi = lo + a.Vw - 1;
-  const long long w0 = lo / a.C, w1 = hi / a.C;
+  const float2 *p = a.part + (long long)r * a.S;
   float M = -INFINITY;
-  for (long long w = w0; w <= w1; ++w) {
-    const int slot = r - (int)((w * a.C) / a.Vw);
-    M = fmaxf(M, a.part[2 * w + slot].x);
-  }
+  for (int w = 0; w < a.S; ++w) M = fmaxf(M, p[w].x);
   float S = 0.0f;
-  for (long long w = w0; w <= w1; ++w) {
-    const int slot = r - (int)((w * a.C) / a.Vw);
-    const float2 ms = a.part[2 * w + slot];
+  for (int w = 0; w < a.S; ++w) {
+    const float2 ms = p[w];
     S += (ms.x == M) ? ms.y : ms.y * __builtin_amdgcn_exp2f((ms.x - M) * a.c);
   }
   return make_float2(M, 1.0f / S);
@@ -196,63 +193,114 @@ __device__ __forceinline__ float4 ld_stream4(const float4 *p) {
   return make_float4(q[0], q[1], q[2], q[3]);
 }
 
+// Row sets of a stats pass.  Under the cpp rules with logits input only the
+// rows of positions up to a sequence's first rejection are ever read, so
+// the first pass takes positions 0 .. P-1 of every sequence ("head"), and
+// the second the remaining rows (positions P .. K-1 and the target's row K,
+// "tail") of the sequences that accepted all P head positions.
+enum RowSet : int { kRowsAll = 0, kRowsHead = 1, kRowsTail = 2 };
+
+// Row id (ub * rpb + j) of entry y of a row set; -1 past its end.
+__device__ __forceinline__ int set_row(const Args &a, int set, int y) {
+  const int groups = a.R / a.rpb;
+  if (set == kRowsAll) return y < a.R ? y : -1;
+  const int P = a.P, K = a.K;
+  if (set == kRowsHead) {
+    const int ub = y / (2 * P), q = y % (2 * P);
+    return ub < groups ? ub * a.rpb + (q < P ? q : K + 1 + (q - P)) : -1;
+  }
+  const int per = 2 * (K - P) + 1, ub = y / per, q = y % per;
+  return ub < groups ? ub * a.rpb + (q <= K - P ? P + q : K + 1 + P + (q - (K - P + 1))) : -1;
+}
+
+// Whether row group ub accepted every head position under the cpp rules
+// (speculative.cpp:66-80: position i takes the i-th uniform when all before
+// it were accepted, and an accepted EOS ends the walk), i.e. needs its tail
+// rows; from the head pass's statistics and the raw logits at the draft
+// tokens it recorded, so that every load here is independent of the others.
+// Every thread of the work-group gets the answer.
+template <int NT>
+__device__ bool tail_needed(const Args &a, int ub) {
+  __shared__ int all_ok;
+  if (threadIdx.x == 0) all_ok = 1;
+  __syncthreads();
+  for (int i = threadIdx.x; i < a.P; i += NT) {
+    const int rt = ub * a.rpb + i, rd = ub * a.rpb + a.K + 1 + i;
+    const int traw = a.tokens[(long long)ub * a.K + i];
+    const float u = a.U[(long long)ub * a.ustride + i];
+    const float2 st = row_stat(a, rt), sd = row_stat(a, rd);
+    const float pt = __builtin_amdgcn_exp2f((a.rawtok[rt] - st.x) * a.c) * st.y;
+    const float qd = __builtin_amdgcn_exp2f((a.rawtok[rd] - sd.x) * a.c) * sd.y;
+    const bool valid = traw >= 0 && traw < a.V;
+    if (!(valid && u <= ratio_cpp(pt, qd)) || traw == a.eos) atomicAnd(&all_ok, 0);
+  }
+  __syncthreads();
+  return all_ok != 0;
+}
+
+// One work-group per (entry y of the row set, slice x): online
+// (max, sum exp2) over the slice.
 template <int NT, int W>
-__global__ __launch_bounds__(NT) void stats_kernel(Args a) {
-  const long long total = (long long)a.R * a.Vw;
-  const long long lo = (long long)blockIdx.x * a.C;
-  const long long hi = min(lo + a.C, total);
-  if (lo >= hi) return;
+__global__ __launch_bounds__(NT) void stats_kernel(Args a, int set) {
+  const int r = set_row(a, set, (int)blockIdx.x);
+  if (r < 0) return;
+  if (set == kRowsTail && !tail_needed<NT>(a, r / a.rpb)) return;
   const float c = a.c;
-  int slot = 0;
-  for (long long r = lo / a.Vw; r * a.Vw < hi; ++r, ++slot) {
-    const long long s0 = max(lo, r * a.Vw) - r * a.Vw;
-    const long long s1 = min(hi, (r + 1) * a.Vw) - r * a.Vw;
-    const float *row = row_ptr_u(a, (int)(r / a.rpb), (int)(r % a.rpb));
-    float m = -INFINITY, s = 0.0f;
-    if (W == 4) {
-      const float4 *p4 = reinterpret_cast<const float4 *>(row);
-      long long i = s0 + threadIdx.x;
-      constexpr int U = 8;
-      for (; i + (U - 1) * NT < s1; i += U * NT) {
-        float4 v[U];
+  const long long s0 = (long long)blockIdx.y * a.Vw / a.S;
+  const long long s1 = (long long)(blockIdx.y + 1) * a.Vw / a.S;
+  const float *row = row_ptr_u(a, r / a.rpb, r % a.rpb);
+  float m = -INFINITY, s = 0.0f;
+  if (W == 4) {
+    const float4 *p4 = reinterpret_cast<const float4 *>(row);
+    long long i = s0 + threadIdx.x;
+    constexpr int U = 8;
+    for (; i + (U - 1) * NT < s1; i += U * NT) {
+      float4 v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = ld_stream4(p4 + i + u * NT);
+      for (int u = 0; u < U; ++u) v[u] = ld_stream4(p4 + i + u * NT);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const float mx = fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w));
-          if (mx > m) {
-            s *= __builtin_amdgcn_exp2f((m - mx) * c);
-            m = mx;
-          }
-          const float ms = (m == -INFINITY) ? 0.0f : m;
-          s += __builtin_amdgcn_exp2f((v[u].x - ms) * c) + __builtin_amdgcn_exp2f((v[u].y - ms) * c) +
-               __builtin_amdgcn_exp2f((v[u].z - ms) * c) + __builtin_amdgcn_exp2f((v[u].w - ms) * c);
-        }
-      }
-      for (; i < s1; i += NT) {
-        const float4 v = ld_stream4(p4 + i);
-        const float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+      for (int u = 0; u < U; ++u) {
+        const float mx = fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w));
         if (mx > m) {
           s *= __builtin_amdgcn_exp2f((m - mx) * c);
           m = mx;
         }
         const float ms = (m == -INFINITY) ? 0.0f : m;
-        s += __builtin_amdgcn_exp2f((v.x - ms) * c) + __builtin_amdgcn_exp2f((v.y - ms) * c) +
-             __builtin_amdgcn_exp2f((v.z - ms) * c) + __builtin_amdgcn_exp2f((v.w - ms) * c);
-      }
-    } else {
-      for (long long i = s0 + threadIdx.x; i < s1; i += NT) {
-        const float v = __builtin_nontemporal_load(row + i);
-        if (v > m) {
-          s *= __builtin_amdgcn_exp2f((m - v) * c);
-          m = v;
-        }
-        const float ms = (m == -INFINITY) ? 0.0f : m;
-        s += __builtin_amdgcn_exp2f((v - ms) * c);
+        s += __builtin_amdgcn_exp2f((v[u].x - ms) * c) + __builtin_amdgcn_exp2f((v[u].y - ms) * c) +
+             __builtin_amdgcn_exp2f((v[u].z - ms) * c) + __builtin_amdgcn_exp2f((v[u].w - ms) * c);
       }
     }
-    const float2 out = block_ms<NT>(m, s, c);
-    if (threadIdx.x == 0) a.part[2 * blockIdx.x + slot] = out;
+    for (; i < s1; i += NT) {
+      const float4 v = ld_stream4(p4 + i);
+      const float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+      if (mx > m) {
+        s *= __builtin_amdgcn_exp2f((m - mx) * c);
+        m = mx;
+      }
+      const float ms = (m == -INFINITY) ? 0.0f : m;
+      s += __builtin_amdgcn_exp2f((v.x - ms) * c) + __builtin_amdgcn_exp2f((v.y - ms) * c) +
+           __builtin_amdgcn_exp2f((v.z - ms) * c) + __builtin_amdgcn_exp2f((v.w - ms) * c);
+    }
+  } else {
+    for (long long i = s0 + threadIdx.x; i < s1; i += NT) {
+      const float v = __builtin_nontemporal_load(row + i);
+      if (v > m) {
+        s *= __builtin_amdgcn_exp2f((m - v) * c);
+        m = v;
+      }
+      const float ms = (m == -INFINITY) ? 0.0f : m;
+      s += __builtin_amdgcn_exp2f((v - ms) * c);
+    }
+  }
+  const float2 out = block_ms<NT>(m, s, c);
+  if (threadIdx.x == 0) {
+    a.part[(long long)r * a.S + blockIdx.y] = out;
+    if (set == kRowsHead) {
+      // the raw logit at this position's draft token, by the slice holding it
+      const int j = r % a.rpb, i = j <= a.K ? j : j - a.K - 1;
+      const int t = min(max(a.tokens[(long long)(r / a.rpb) * a.K + i], 0), a.V - 1);
+      if ((long long)t >= s0 * W && (long long)t < s1 * W) a.rawtok[r] = row[t];
+    }
   }
 }
 
@@ -267,48 +315,41 @@ __device__ __forceinline__ void am_merge(float &v, int &i, float v2, int i2) {
   }
 }
 
+// One work-group per (row x, slice y).
 template <int NT>
 __global__ __launch_bounds__(NT) void argmax_kernel(Args a) {
-  const long long total = (long long)a.R * a.Vw;
-  const long long lo = (long long)blockIdx.x * a.C;
-  const long long hi = min(lo + a.C, total);
-  if (lo >= hi) return;
+  const int r = (int)blockIdx.x;
+  if (r >= a.R) return;
   __shared__ float2 red[NT / 64];
   const int W = (int)(a.V / a.Vw);
-  int slot = 0;
-  for (long long r = lo / a.Vw; r * a.Vw < hi; ++r, ++slot) {
-    const long long e0 = (max(lo, r * a.Vw) - r * a.Vw) * W;
-    const long long e1 = (min(hi, (r + 1) * a.Vw) - r * a.Vw) * W;
-    const Dist d = make_dist_u(a, (int)(r / a.rpb), (int)(r % a.rpb));
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (long long i = e0 + threadIdx.x; i < e1; i += NT) am_merge(bv, bi, d(i), (int)i);
+  const long long e0 = (long long)blockIdx.y * a.Vw / a.S * W;
+  const long long e1 = (long long)(blockIdx.y + 1) * a.Vw / a.S * W;
+  const Dist d = make_dist_u(a, r / a.rpb, r % a.rpb);
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (long long i = e0 + threadIdx.x; i < e1; i += NT) am_merge(bv, bi, d(i), (int)i);
 #pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) {
-      const float v2 = __shfl_xor(bv, s, 64);
-      const int i2 = __shfl_xor(bi, s, 64);
-      am_merge(bv, bi, v2, i2);
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) red[wave] = make_float2(bv, __int_as_float(bi));
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float v = red[0].x;
-      int ix = __float_as_int(red[0].y);
-      for (int w = 1; w < NT / 64; ++w) am_merge(v, ix, red[w].x, __float_as_int(red[w].y));
-      a.apart[2 * blockIdx.x + slot] = make_float2(v, __int_as_float(ix));
-    }
-    __syncthreads();
+  for (int s = 32; s >= 1; s >>= 1) {
+    const float v2 = __shfl_xor(bv, s, 64);
+    const int i2 = __shfl_xor(bi, s, 64);
+    am_merge(bv, bi, v2, i2);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = make_float2(bv, __int_as_float(bi));
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = red[0].x;
+    int ix = __float_as_int(red[0].y);
+    for (int w = 1; w < NT / 64; ++w) am_merge(v, ix, red[w].x, __float_as_int(red[w].y));
+    a.apart[(long long)r * a.S + blockIdx.y] = make_float2(v, __int_as_float(ix));
   }
 }
 
 __device__ int row_argmax(const Args &a, int r) {
-  const long long lo = (long long)r * a.Vw, hi = lo + a.Vw - 1;
   float v = -INFINITY;
   int ix = 0x7fffffff;
-  for (long long w = lo / a.C; w <= hi / a.C; ++w) {
-    const int slot = r - (int)((w * a.C) / a.Vw);
-    const float2 e = a.apart[2 * w + slot];
+  for (int w = 0; w < a.S; ++w) {
+    const float2 e = a.apart[(long long)r * a.S + w];
     am_merge(v, ix, e.x, __float_as_int(e.y));
   }
   return ix == 0x7fffffff ? 0 : ix;
@@ -1328,16 +1369,31 @@ using namespace cfa::chain;
 
 static size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
 
-static int max_groups(int R) { return std::max(R, 8192); }
+// Slices per row of the stats / argmax passes: slices of at most 16384
+// vector units (256 KiB of fp32 at 16-byte loads; 128 KiB slices measured
+// 1% slower at C2, 64 KiB 9%), and for few rows enough slices for about
+// 1024 work-groups (slices of at least 256 units).  A function of the shape
+// only, so every pass over a row combines the same partials in the same
+// order.
+static int stats_slices(long long R, long long Vw) {
+  const long long by_len = (Vw + 16383) / 16384;
+  const long long by_rows = std::min<long long>((1024 + R - 1) / R, std::max<long long>(1, Vw / 256));
+  return (int)std::min<long long>(256, std::max<long long>(1, std::max(by_len, by_rows)));
+}
+// Head positions of the two-pass statistics (cpp rules, logits): with the
+// ~0.7 per-position acceptance of typical draft models, 3 minimises the rows
+// the two passes read together.
+constexpr int kHeadPositions = 3;
 
 // Workspace layout (each region 256-byte aligned).
 struct WsLayout {
-  size_t part, apart, dec, ufin, jobs, res, csum_x, csum_t, crec, trec, badcnt, bad, x0, total;
+  size_t part, apart, rawtok, dec, ufin, jobs, res, csum_x, csum_t, crec, trec, badcnt, bad, x0, total;
 };
 
 static WsLayout ws_layout(int B, int K, int V, int mode) {
   const int rpb = (mode == CFA_MODE_GREEDY) ? K + 1 : 2 * K + 1;
-  const size_t G = (size_t)max_groups(B * rpb);
+  const size_t R = (size_t)B * rpb;
+  const size_t G = R * (size_t)stats_slices((long long)R, V);  // the largest slice count (scalar loads)
   const size_t NC = (size_t)((V + kMwChunk - 1) / kMwChunk);
   const bool mw = mode != CFA_MODE_GREEDY;
   WsLayout L{};
@@ -1347,8 +1403,9 @@ static WsLayout ws_layout(int B, int K, int V, int mode) {
     o += align_up(bytes);
     return at;
   };
-  L.part = take(G * 2 * sizeof(float2));
-  L.apart = take(G * 2 * sizeof(float2));
+  L.part = take(G * sizeof(float2));
+  L.apart = take(G * sizeof(float2));
+  L.rawtok = take(R * sizeof(float));
   L.dec = take((size_t)B * sizeof(int4));
   L.ufin = take((size_t)B * sizeof(float));
   L.jobs = take((size_t)B * sizeof(MwJob));
@@ -1450,13 +1507,13 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   a.Vw = V / W;
   const int R = (B / a.draws) * a.rpb;
   a.R = R;
-  const long long total = (long long)R * a.Vw;
-  const int cus = device_cu_count();
-  long long G = std::min<long long>((long long)cus * 4, (total + 1023) / 1024);
-  G = std::max<long long>(G, R);
-  G = std::min<long long>(G, max_groups(R));
-  a.C = (total + G - 1) / G;
-  a.G = (int)((total + a.C - 1) / a.C);
+  a.S = stats_slices(R, a.Vw);
+  // cpp rules with logits: statistics in two passes, the second only for the
+  // sequences that accepted every head position (not when the caller asks
+  // for every row's probabilities)
+  const bool two_pass = mode == CFA_MODE_CPP && a.logits && a.draws == 1 && K > kHeadPositions &&
+                        !out_target_probs && !out_draft_probs;
+  a.P = two_pass ? kHeadPositions : K;
 
   a.vec = vec ? 1 : 0;
   a.NC = (V + kMwChunk - 1) / kMwChunk;
@@ -1464,6 +1521,7 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   char *ws = (char *)workspace;
   a.part = (float2 *)(ws + L.part);
   a.apart = (float2 *)(ws + L.apart);
+  a.rawtok = (float *)(ws + L.rawtok);
   a.dec = (int4 *)(ws + L.dec);
   a.ufin = (float *)(ws + L.ufin);
   a.jobs = (MwJob *)(ws + L.jobs);
@@ -1477,13 +1535,28 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   a.x0 = (float *)(ws + L.x0);
 
   if (a.logits) {
-    if (vec)
-      CFA_LAUNCH("chain_stats", (stats_kernel<256, 4>), dim3(a.G), dim3(256), 0, st, a);
-    else
-      CFA_LAUNCH("chain_stats", (stats_kernel<256, 1>), dim3(a.G), dim3(256), 0, st, a);
+    const int groups = R / a.rpb;
+    auto stats = [&](int set, int entries) -> int {
+      const dim3 grid((unsigned)entries, (unsigned)a.S);
+      const char *name = set == kRowsHead ? "chain_stats_head"
+                         : set == kRowsTail ? "chain_stats_tail" : "chain_stats";
+      if (vec)
+        CFA_LAUNCH(name, (stats_kernel<256, 4>), grid, dim3(256), 0, st, a, set);
+      else
+        CFA_LAUNCH(name, (stats_kernel<256, 1>), grid, dim3(256), 0, st, a, set);
+      return CFA_OK;
+    };
+    int rc;
+    if (two_pass) {
+      if ((rc = stats(kRowsHead, groups * 2 * a.P)) != CFA_OK) return rc;
+      if ((rc = stats(kRowsTail, groups * (2 * (K - a.P) + 1))) != CFA_OK) return rc;
+    } else if ((rc = stats(kRowsAll, R)) != CFA_OK) {
+      return rc;
+    }
   }
   if (mode == CFA_MODE_GREEDY)
-    CFA_LAUNCH("chain_argmax", (argmax_kernel<256>), dim3(a.G), dim3(256), 0, st, a);
+    CFA_LAUNCH("chain_argmax", (argmax_kernel<256>), dim3((unsigned)R, (unsigned)a.S), dim3(256), 0,
+               st, a);
   // cpp rules: the mw sums kernel takes each sequence's decision itself
   const int fused_decide = mode == CFA_MODE_CPP ? 1 : 0;
   if (!fused_decide) CFA_LAUNCH("chain_decide", decide_kernel, dim3(B), dim3(64), 0, st, a);

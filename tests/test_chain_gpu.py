@@ -208,3 +208,42 @@ def test_out_of_range_token_is_rejected(device):
     t_d, d_d, tok_d, U_d = _to_dev(device, t, d, tok, U)
     out = chain_verify(t_d, d_d, tok_d, U_d, input_kind="probs", mode="cpp")
     assert out.accept_len.cpu().tolist() == [1, 0]
+
+
+def _chain_outputs(out):
+    return [x.cpu().numpy() for x in (out.accept_len, out.tokens, out.num_emitted, out.final,
+                                       out.eos)]
+
+
+@pytest.mark.parametrize("case", ["c2", "all_accept", "eos_in_head", "small_v"])
+def test_two_pass_statistics_match_one_pass(device, case):
+    """cpp rules with logits read the rows of positions 0..2 first, and the
+    rest only for sequences that accepted all three.  Every row is cut into
+    the same slices in both passes, so the outputs are bit-identical to the
+    one-pass run (return_probs=True reads every row), which the oracle checks
+    in test_logits_path_matches_oracle."""
+    T, eos = 0.7, -1
+    if case == "small_v":
+        tl, dl, tok, U = c2_inputs(seed=91, B=33, K=5, V=3001, temperature=T)
+    else:
+        tl, dl, tok, U = c2_inputs(seed=92, B=64, K=8, V=128256, temperature=T)
+    if case == "all_accept":   # draft = target: every ratio is 1, every sequence needs its tail
+        dl = tl[:, :-1].copy()
+    if case == "eos_in_head":  # an accepted EOS at position 1 ends the walk in the head
+        eos = int(tok[0, 1])
+        tok[::2, 1] = eos
+        U[::2, :2] = 0.0
+    t_d, d_d, tok_d, U_d = _to_dev(device, tl, dl, tok, U)
+    kw = dict(input_kind="logits", temperature=T, mode="cpp", eos_token_id=eos)
+    one = chain_verify(t_d, d_d, tok_d, U_d, return_probs=True, **kw)
+    two = chain_verify(t_d, d_d, tok_d, U_d, **kw)
+    torch.cuda.synchronize()
+    for a, b in zip(_chain_outputs(one), _chain_outputs(two)):
+        np.testing.assert_array_equal(a, b)
+    n = one.accept_len.cpu().numpy()
+    if case == "all_accept":
+        assert (n == tok.shape[1]).all()
+    if case == "eos_in_head":
+        assert (one.eos.cpu().numpy()[::2] == 1).all()
+    if case == "c2":  # both outcomes present: sequences stopped in the head and ones that went on
+        assert (n < 3).any() and (n >= 3).any()
