@@ -251,13 +251,20 @@ __global__ __launch_bounds__(NT) void stats_kernel(Args a, int set) {
   const float *row = row_ptr_u(a, r / a.rpb, r % a.rpb);
   float m = -INFINITY, s = 0.0f;
   if (W == 4) {
+    // rounds of U vectors per thread, every load of a round issued before
+    // the first use; in the last round a lane past the slice reloads its
+    // last vector and folds -inf instead (exp2(-inf) = 0 and the max is
+    // unchanged, so that is exactly nothing).  A thread folds its vectors
+    // in index order, so the partial does not depend on U.
     const float4 *p4 = reinterpret_cast<const float4 *>(row);
-    long long i = s0 + threadIdx.x;
-    constexpr int U = 8;
-    for (; i + (U - 1) * NT < s1; i += U * NT) {
+    constexpr int U = 4;
+    for (long long i0 = s0 + threadIdx.x; i0 < s1; i0 += U * NT) {
       float4 v[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = ld_stream4(p4 + i + u * NT);
+      for (int u = 0; u < U; ++u) v[u] = ld_stream4(p4 + min(i0 + u * NT, s1 - 1));
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (i0 + u * NT >= s1) v[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const float mx = fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w));
@@ -269,17 +276,6 @@ __global__ __launch_bounds__(NT) void stats_kernel(Args a, int set) {
         s += __builtin_amdgcn_exp2f((v[u].x - ms) * c) + __builtin_amdgcn_exp2f((v[u].y - ms) * c) +
              __builtin_amdgcn_exp2f((v[u].z - ms) * c) + __builtin_amdgcn_exp2f((v[u].w - ms) * c);
       }
-    }
-    for (; i < s1; i += NT) {
-      const float4 v = ld_stream4(p4 + i);
-      const float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
-      if (mx > m) {
-        s *= __builtin_amdgcn_exp2f((m - mx) * c);
-        m = mx;
-      }
-      const float ms = (m == -INFINITY) ? 0.0f : m;
-      s += __builtin_amdgcn_exp2f((v.x - ms) * c) + __builtin_amdgcn_exp2f((v.y - ms) * c) +
-           __builtin_amdgcn_exp2f((v.z - ms) * c) + __builtin_amdgcn_exp2f((v.w - ms) * c);
     }
   } else {
     for (long long i = s0 + threadIdx.x; i < s1; i += NT) {
