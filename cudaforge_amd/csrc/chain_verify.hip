@@ -24,6 +24,7 @@
 
 #include "abi_internal.hpp"
 #include "dist.hpp"
+#include "lds_dma.hpp"
 #include "seqsum.hpp"
 
 // Every fp32 expression below must round exactly as written (the oracle and
@@ -41,6 +42,12 @@ constexpr int kMwTile = 16;                 // elements per lane (one tile)
 constexpr int kMwChunkTiles = 64;           // tiles per chunk (one wave)
 constexpr int kMwChunk = kMwChunkTiles * kMwTile;  // 1024 elements per chunk
 constexpr int kMwMaxBad = 64;               // cached serial tiles per row and pass
+constexpr int kMwPf = 8;                    // chunks whose tile records the walk prefetches
+constexpr int kMwSerialTiles = 4;           // leading tiles of chunk 0 the walk replays serially
+// Relative slack within which a tile counts as near a binade boundary (its
+// values are cached for the walk).  The approximate prefix that places tiles
+// differs from the exact running value by about 2^-15 relatively at V = 128K.
+constexpr float kMwNear = 1.0f / 4096.0f;
 constexpr int kMwMaxNC = 4096;              // chunks per row (V <= 4M)
 struct MwJob {  // what sequence b still has to draw
   int kind, row, n, eos_acc;
@@ -62,11 +69,13 @@ struct MwRec {  // a tile's function of the entry parity, its region guess, pad 
 // A chunk as run 0 (tiles [0, brk)), break tile brk (replayed serially when
 // brk_serial, otherwise run 1 starts there in another region) and run 1
 // (the rest); brk = -1: one run.  Runs are functions of the entry parity.
+// near = 1: the walk will probably go down to this chunk's tiles (it holds a
+// tile cached for a serial replay), so the walk prefetches its tile records.
 struct MwChunk {
   uint32_t e0, o0, e1, o1;
   int reg0, reg1;
   int brk, brk_serial;
-  int status, pad[3];
+  int status, near, pad[2];
 };
 struct MwBad {  // a tile the walk will probably replay serially, with its values
   int tile, pad[3];
@@ -702,7 +711,9 @@ __device__ __forceinline__ bool mw_active(const MwJob &j, int pass) {
   return pass == kPassSum ? j.kind == kResid : (j.kind == kResid || j.kind == kPlain);
 }
 
-__device__ MwElem mw_elem(const Args &a, int b, const MwJob &j, int pass) {
+// The element function of (job b, pass); `r` holds the sum pass's result
+// (S, fallback) for the CDF pass.
+__device__ __forceinline__ MwElem mw_elem_r(const Args &a, int b, const MwJob &j, int pass, const MwRes &r) {
   MwElem e;
   e.t.p = row_ptr(a, b, j.row);
   e.t.c = a.c;
@@ -719,11 +730,14 @@ __device__ MwElem mw_elem(const Args &a, int b, const MwJob &j, int pass) {
   if (pass == kPassSum) {
     e.fn = 0;
   } else {
-    const MwRes r = a.res[b];
     e.fn = (j.kind == kResid && !r.fallback) ? 1 : 2;
     e.S = r.S;
   }
   return e;
+}
+
+__device__ __forceinline__ MwElem mw_elem(const Args &a, int b, const MwJob &j, int pass) {
+  return mw_elem_r(a, b, j, pass, pass == kPassSum ? MwRes{} : a.res[b]);
 }
 
 // Raw values of 16 consecutive elements starting at i0 (zero past V).
@@ -744,16 +758,29 @@ __device__ __forceinline__ void mw_load16(const Args &a, const float *p, long lo
   }
 }
 
+// Raw target and draft values of tile `tile` (the draft only when the
+// element function reads it).
+__device__ __forceinline__ void mw_tile_raw(const Args &a, const MwElem &e, long long tile,
+                                            float *tv, float *dv) {
+  const long long i0 = tile * kMwTile;
+  mw_load16(a, e.t.p, i0, tv);
+  if (e.fn != 2) mw_load16(a, e.d.p, i0, dv);
+}
+
+// Evaluated elements of tile `tile` from its raw values (zero past V).
+__device__ __forceinline__ void mw_tile_eval(const Args &a, const MwElem &e, long long tile,
+                                             const float *tv, const float *dv, float *x) {
+  const long long i0 = tile * kMwTile;
+#pragma unroll
+  for (int k = 0; k < kMwTile; ++k) x[k] = (i0 + k < a.V) ? e.eval(tv[k], e.fn != 2 ? dv[k] : 0.0f) : 0.0f;
+}
+
 // Evaluated elements of tile `tile` of a row (zero past V).
 __device__ __forceinline__ void mw_tile_values(const Args &a, const MwElem &e, long long tile,
                                                float *x) {
-  const long long i0 = tile * kMwTile;
   float tv[kMwTile], dv[kMwTile];
-  mw_load16(a, e.t.p, i0, tv);
-  if (e.fn != 2)
-    mw_load16(a, e.d.p, i0, dv);
-#pragma unroll
-  for (int k = 0; k < kMwTile; ++k) x[k] = (i0 + k < a.V) ? e.eval(tv[k], e.fn != 2 ? dv[k] : 0.0f) : 0.0f;
+  mw_tile_raw(a, e, tile, tv, dv);
+  mw_tile_eval(a, e, tile, tv, dv, x);
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
@@ -833,33 +860,31 @@ __device__ __forceinline__ seq::Inc wave_compose_where(bool in, seq::Inc f) {
   return Inc{lane_bcast(tot.e, 63), lane_bcast(tot.o, 63)};
 }
 
-__global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
+// A CDF search ends before any chunk whose approximate entry value E0 is
+// surely past u; such a chunk gets a "skipped" record and no loads.
+__device__ __forceinline__ bool mw_skip(int pass, const MwJob &j, float E0) {
+  return pass == kPassCdf && E0 * (1.0f - 1.0f / 64.0f) > j.u;
+}
+
+__device__ __forceinline__ void mw_write_skipped(const Args &a, long long rowrec, int c) {
+  if ((threadIdx.x & 63) == 0) {
+    MwChunk r{};
+    r.status = kChunkSkipped;
+    a.crec[rowrec * a.NC + c] = r;
+  }
+}
+
+// Records of chunk c of job b for one pass, by one wave (lane = tile in the
+// chunk), from the chunk's approximate entry value E0 (on the pass's scale)
+// and the lane's 16 evaluated elements.
+__device__ __forceinline__ void mw_records_chunk(const Args &a, int b, int c, int pass,
+                                                 const MwJob &j, float E0, const float *x) {
   using namespace seq;
-  const int b = blockIdx.y, lane = threadIdx.x & 63;
-  const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
-  const MwJob j = a.jobs[b];
-  if (!mw_active(j, pass)) return;
-  if (c >= a.NC) return;
-  const MwElem e = mw_elem(a, b, j, pass);
+  const int lane = threadIdx.x & 63;
   const long long rowrec = ((long long)pass * a.B + b);
   MwChunk *crec = a.crec + rowrec * a.NC;
   MwRec *trec = a.trec + rowrec * a.NC * kMwChunkTiles;
-  // approximate entry value of this chunk
-  const float *csum = (e.fn == 2 ? a.csum_t : a.csum_x) + (long long)b * a.NC;
-  float E0 = mw_entry_prefix(csum, c);
-  if (e.fn == 1) E0 = E0 / e.S;
-  // a CDF search ends before any chunk whose entry is surely past u
-  if (pass == kPassCdf && E0 * (1.0f - 1.0f / 64.0f) > j.u) {
-    if (lane == 0) {
-      MwChunk r{};
-      r.status = kChunkSkipped;
-      crec[c] = r;
-    }
-    return;
-  }
   const long long tile = (long long)c * kMwChunkTiles + lane;
-  float x[kMwTile];
-  mw_tile_values(a, e, tile, x);
   float A = 0.0f;
 #pragma unroll
   for (int k = 0; k < kMwTile; ++k) A += x[k];
@@ -889,9 +914,23 @@ __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
     for (int k = 0; k < kMwTile; k += 4) dst[k / 4] = make_float4(x[k], x[k + 1], x[k + 2], x[k + 3]);
     return;
   }
-  if (!ok) {  // cache the values for the walk's serial replay
-    const int slot = atomicAdd(&a.badcnt[rowrec], 1);
-    if (slot < kMwMaxBad) {
+  // Cache the values of the tiles the walk will probably replay serially: a
+  // straddling tile (!ok), a tile within kMwNear of a binade (the exact
+  // running value can sit on the other side of the boundary from the
+  // approximate one), and in the CDF pass a tile whose approximate range
+  // holds u (where the search ends).  One slot reservation per wave.
+  const bool nearb = A != 0.0f && region_of(E * (1.0f - kMwNear)) != region_of((E + A) * (1.0f + kMwNear));
+  const bool hitc = pass == kPassCdf && A != 0.0f && E * (1.0f - kMwNear) <= j.u &&
+                    j.u <= (E + A) * (1.0f + kMwNear);
+  const bool keep = !ok || nearb || hitc;
+  const unsigned long long keepm = __ballot(keep);
+  if (keepm) {
+    const int first = (int)__builtin_ctzll(keepm);
+    int base = 0;
+    if (lane == first) base = atomicAdd(&a.badcnt[rowrec], (int)__popcll(keepm));
+    base = (int)lane_bcast((uint32_t)base, first);
+    const int slot = base + (int)__popcll(keepm & ((1ull << lane) - 1ull));
+    if (keep && slot < kMwMaxBad) {
       MwBad *dst = a.bad + rowrec * kMwMaxBad + slot;
       dst->tile = (int)tile;
 #pragma unroll
@@ -905,6 +944,7 @@ __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
   const unsigned long long brkm = __ballot(!ok || (real && r_lo != r_first));
   MwChunk rec{};
   rec.status = kChunkOk;
+  rec.near = keepm != 0ull;
   if (brkm == 0ull) {
     const Inc F = wave_compose_where(true, f);
     rec.e0 = F.e;
@@ -932,12 +972,34 @@ __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
     rec.reg1 = r1;
     if (__ballot(bad1) != 0ull) rec.status = kChunkTiles;
   }
+  if (rec.status == kChunkTiles) rec.near = 1;
   if (lane == 0) crec[c] = rec;
+}
+
+// One wave per chunk: chunk c = 4 * blockIdx.x + wave of job blockIdx.y.
+__global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
+  const int b = blockIdx.y;
+  const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
+  const MwJob j = a.jobs[b];
+  if (!mw_active(j, pass)) return;
+  if (c >= a.NC) return;
+  const MwElem e = mw_elem(a, b, j, pass);
+  const float *csum = (e.fn == 2 ? a.csum_t : a.csum_x) + (long long)b * a.NC;
+  float E0 = mw_entry_prefix(csum, c);
+  if (e.fn == 1) E0 = E0 / e.S;
+  if (mw_skip(pass, j, E0)) {
+    mw_write_skipped(a, (long long)pass * a.B + b, c);
+    return;
+  }
+  float x[kMwTile];
+  mw_tile_values(a, e, (long long)c * kMwChunkTiles + (threadIdx.x & 63), x);
+  mw_records_chunk(a, b, c, pass, j, E0, x);
 }
 
 constexpr int kMwWin = 256;  // chunk records staged in LDS at a time
 
-__device__ void finish_one(const Args &a, int b, const MwJob &j, int idx, int idx2 = -1);
+__device__ __forceinline__ void finish_one(const Args &a, int b, const MwJob &j, int idx,
+                                           int idx2 = -1);
 
 // Last index of positive weight of a (job, pass) row, V - 1 if none; one
 // wave scans down from the end (python mode's rare fallback draw).
@@ -953,21 +1015,45 @@ __device__ long long mw_last_positive(const Args &a, const MwElem &e) {
   return a.V - 1;
 }
 
-__global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
+// LDS of one walk.
+struct MwWalkLds {
+  MwChunk cr[kMwWin];
+  MwRec tr[kMwChunkTiles];
+  MwRec pft[kMwPf][kMwChunkTiles];  // tile records of the prefetched chunks
+  MwBad bad[kMwMaxBad];
+  alignas(16) float xs[kMwChunk];
+};
+
+// Orders one wave's LDS accesses (a wave's LDS operations complete in issue
+// order, so this only keeps the compiler from moving accesses across it).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The exact walk of job b's row for one pass, by the calling wave alone: it
+// synchronises only itself, so the other waves of its work-group can wait at
+// a barrier meanwhile.  Writes the pass's result (sum pass: S and the
+// fallback flag; CDF pass: the drawn index, and the outputs in cpp mode) and
+// returns the final running value.
+__device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const MwJob &j,
+                                         const MwElem &e, MwWalkLds &L) {
   using namespace seq;
-  __shared__ MwChunk cr[kMwWin];
-  __shared__ MwRec tr[kMwChunkTiles];
-  __shared__ MwBad bad[kMwMaxBad];
-  __shared__ __align__(16) float xs[kMwChunk];
-  const int b = blockIdx.x, lane = threadIdx.x;
+  MwChunk *cr = L.cr;
+  MwRec *tr = L.tr;
+  MwRec(&pft)[kMwPf][kMwChunkTiles] = L.pft;
+  MwBad *bad = L.bad;
+  float *xs = L.xs;
+  const int lane = threadIdx.x & 63;
   const long long rowrec = ((long long)pass * a.B + b);
   const MwChunk *crec = a.crec + rowrec * a.NC;
   const MwRec *trec = a.trec + rowrec * a.NC * kMwChunkTiles;
 
   // One round of loads before the first wait: chunk 0's values and tile
-  // records, the first window of chunk records and every cache slot (all
-  // written by mw_records for active jobs; in-bounds, unused otherwise), the
-  // job and the cache count.
+  // records, the first window of chunk records, every cache slot (all
+  // written by mw_records for active jobs; in-bounds, unused otherwise) and
+  // the cache count.
   {
     const float4 *src = reinterpret_cast<const float4 *>(a.x0 + rowrec * kMwChunk + lane * kMwTile);
     float4 *dst = reinterpret_cast<float4 *>(xs + lane * kMwTile);
@@ -978,16 +1064,33 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
   for (int c = 1 + lane; c < min(a.NC, 1 + kMwWin); c += 64) cr[c - 1] = crec[c];
   static_assert(kMwMaxBad <= 64, "one cache slot per lane");
   bad[lane] = a.bad[rowrec * kMwMaxBad + lane];
-  const MwJob j = a.jobs[b];
   const int nbad = min(a.badcnt[rowrec], kMwMaxBad);
-  __syncthreads();
-  if (!mw_active(j, pass)) {
-    if (pass == kPassCdf && a.mode == CFA_MODE_CPP && lane == 0) finish_one(a, b, j, -1);
-    return;
-  }
-  const MwElem e = mw_elem(a, b, j, pass);
+  wave_sync();
   const bool cdf = (pass == kPassCdf);
   const float r = j.u;
+
+  // The first kMwPf chunks of the first window that the records kernel
+  // flagged `near`: lane p < npf holds the p-th one's index.  Their tile
+  // records travel straight to LDS during the chunk-0 walk (which touches
+  // no global memory), so a tile-level walk there costs no round trip.
+  int pfc = -1, npf = 0;
+  {
+    const int cnt0 = min(kMwWin, a.NC - 1);
+    for (int base = 0; base < cnt0 && npf < kMwPf; base += 64) {
+      const int i = base + lane;
+      unsigned long long m = __ballot(i < cnt0 && cr[i].near != 0);
+      while (m != 0ull && npf < kMwPf) {
+        const int k = (int)__builtin_ctzll(m);
+        if (lane == npf) pfc = 1 + base + k;
+        ++npf;
+        m &= m - 1ull;
+      }
+    }
+  }
+  for (int p = 0; p < npf; ++p) {
+    const int cp = (int)lane_bcast((uint32_t)pfc, p);
+    dma16(trec + (long long)cp * kMwChunkTiles + lane, (CFA_LDS void *)pft[p]);
+  }
 
   // Serial replay of a tile's 16 values from s (CDF: first hit index).  The
   // running value never decreases (x >= 0), so the first i with r <= s_i is
@@ -1031,18 +1134,35 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
     return replay16(x, tile * kMwTile, s);
   };
 
-  // chunk 0: runs of tiles applied from their records, the tiles straddling
-  // a binade (every doubling of the small running value) replayed serially
-  // from LDS
+  // chunk 0: its first kMwSerialTiles tiles replayed serially (the small
+  // running value doubles every few elements there: 1, 2, 4, ... 32 for a
+  // flat row), then runs of tiles applied from their records, the tiles
+  // straddling a binade replayed serially from LDS
   float s = 0.0f;
-  long long found;
+  long long found = -1;
   {
+    const float4 *h4 = reinterpret_cast<const float4 *>(xs);
+    float xh[kMwSerialTiles * kMwTile];
+#pragma unroll
+    for (int k = 0; k < kMwSerialTiles * kMwTile / 4; ++k) {
+      const float4 q = h4[k];
+      xh[4 * k] = q.x;
+      xh[4 * k + 1] = q.y;
+      xh[4 * k + 2] = q.z;
+      xh[4 * k + 3] = q.w;
+    }
+#pragma unroll
+    for (int t = 0; t < kMwSerialTiles; ++t)
+      if (found < 0) found = replay16(xh + t * kMwTile, (long long)t * kMwTile, s);
+  }
+  if (found < 0) {
     auto item0 = [&](int i, int &reg) -> Inc {
-      const MwRec q = tr[i];
+      const MwRec q = tr[kMwSerialTiles + i];
       reg = q.reg;
       return q.pad ? Inc{kBad, kBad} : Inc{q.e, q.o};
     };
-    auto desc0 = [&](int i, float &s2) -> long long {
+    auto desc0 = [&](int i0, float &s2) -> long long {
+      const int i = kMwSerialTiles + i0;
       const float4 *x4 = reinterpret_cast<const float4 *>(xs + i * kMwTile);
       float x[kMwTile];
 #pragma unroll
@@ -1055,16 +1175,25 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
       }
       return replay16(x, (long long)i * kMwTile, s2);
     };
-    found = walk(kMwChunkTiles, s, cdf, r, item0, desc0);
+    found = walk(kMwChunkTiles - kMwSerialTiles, s, cdf, r, item0, desc0);
   }
+  wait_vmcnt<0>();
+  wave_sync();
 
-  // tile-level walk of chunk c from its tile t0 (records from memory)
+  // tile-level walk of chunk c from its tile t0 (records from the prefetch
+  // table, else from memory)
   auto tile_walk = [&](int c, int t0, float &ss) -> long long {
-    __syncthreads();
-    tr[lane] = trec[(long long)c * kMwChunkTiles + lane];
-    __syncthreads();
+    const unsigned long long pm = __ballot(lane < npf && pfc == c);
+    const MwRec *trs = tr;
+    if (pm != 0ull) {
+      trs = pft[__builtin_ctzll(pm)];
+    } else {
+      wave_sync();
+      tr[lane] = trec[(long long)c * kMwChunkTiles + lane];
+      wave_sync();
+    }
     auto tile_item = [&](int i, int &reg) -> Inc {
-      const MwRec q = tr[t0 + i];
+      const MwRec q = trs[t0 + i];
       reg = q.reg;
       return q.pad ? Inc{kBad, kBad} : Inc{q.e, q.o};
     };
@@ -1098,9 +1227,9 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
   for (int w0 = 1; w0 < a.NC && found < 0; w0 += kMwWin) {
     const int cnt = min(kMwWin, a.NC - w0);
     if (w0 > 1) {
-      __syncthreads();
+      wave_sync();
       for (int c = lane; c < cnt; c += 64) cr[c] = crec[w0 + c];
-      __syncthreads();
+      wave_sync();
     }
     auto chunk_item = [&](int i, int &reg) -> Inc {
       const MwChunk q = cr[i];
@@ -1150,6 +1279,19 @@ __global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
     const long long last = mw_last_positive(a, e);
     if (lane == 0) a.res[b].idx = (int)last;
   }
+  return s;
+}
+
+// One wave per job: the exact walk of one pass.
+__global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
+  __shared__ MwWalkLds L;
+  const int b = blockIdx.x;
+  const MwJob j = a.jobs[b];
+  if (!mw_active(j, pass)) {
+    if (pass == kPassCdf && a.mode == CFA_MODE_CPP && threadIdx.x == 0) finish_one(a, b, j, -1);
+    return;
+  }
+  mw_walk(a, b, pass, j, mw_elem(a, b, j, pass), L);
 }
 
 // ---------------------------------------------------------------------------
@@ -1213,7 +1355,8 @@ __global__ __launch_bounds__(kSampleNT) void pybonus_kernel(Args a) {
 
 // Outputs of sequence b; idx is the drawn token (ignored without a draw).
 // idx2: the python-mode bonus that follows a resample (j.extra).
-__device__ void finish_one(const Args &a, int b, const MwJob &j, int idx, int idx2) {
+__device__ __forceinline__ void finish_one(const Args &a, int b, const MwJob &j, int idx,
+                                           int idx2) {
   const int K = a.K;
   const int n = j.n, eos_acc = j.eos_acc;
   int fin = (j.kind == kNone) ? -1 : idx;

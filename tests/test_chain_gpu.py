@@ -174,6 +174,30 @@ def test_uniforms_on_cdf_boundaries(device):
     _check_vs_oracle(out, t, d, tok, U, -1, "cpp")
 
 
+def test_uniforms_on_cdf_boundaries_of_first_tiles(device):
+    """u on (and one ulp below) the prefix sums at the start of the row: the
+    serially replayed leading tiles (indices 0..63), the first walked tile,
+    the end of chunk 0 and the start of chunk 1 (1024 elements a chunk)."""
+    js = [0, 1, 2, 15, 16, 31, 63, 64, 65, 79, 1023, 1024, 1040]
+    B, K, V = 2 * len(js), 0, 5000
+    rng = np.random.default_rng(12)
+    t = rng.random((B, 1, V)).astype(np.float32) ** 8
+    t /= t.sum(-1, keepdims=True)
+    U = np.zeros((B, 1), np.float32)
+    for b in range(B):
+        pref = np.cumsum(t[b, 0], dtype=np.float32)
+        j = js[b // 2]
+        U[b, 0] = pref[j] if b % 2 == 0 else np.nextafter(pref[j], np.float32(0))
+    d = np.zeros((B, 0, V), np.float32)
+    tok = np.zeros((B, 0), np.int32)
+    t_d, d_d, tok_d, U_d = _to_dev(device, t, d, tok, U)
+    out = chain_verify(t_d, d_d, tok_d, U_d, input_kind="probs", mode="cpp")
+    _check_vs_oracle(out, t, d, tok, U, -1, "cpp")
+    got = out.tokens.cpu().numpy()[:, 0]
+    for b in range(0, B, 2):  # u = s_j draws j exactly (speculative.cpp:19)
+        assert got[b] == js[b // 2], (b, got[b])
+
+
 def test_residual_fallback_equal_rows(device):
     tok, d, t, eos = chain_case(31, 32, 4, 500, equal=True)
     U = np.random.default_rng(2).random((32, 5)).astype(np.float32)
