@@ -222,51 +222,51 @@ __device__ __forceinline__ int set_row(const Args &a, int set, int y) {
   return ub < groups ? ub * a.rpb + (q <= K - P ? P + q : K + 1 + P + (q - (K - P + 1))) : -1;
 }
 
-// Whether row group ub accepted every head position under the cpp rules
+// Whether row group ub accepted head position i under the cpp rules
 // (speculative.cpp:66-80: position i takes the i-th uniform when all before
-// it were accepted, and an accepted EOS ends the walk), i.e. needs its tail
-// rows; from the head pass's statistics and the raw logits at the draft
-// tokens it recorded, so that every load here is independent of the others.
-// Every thread of the work-group gets the answer.
+// it were accepted, and an accepted EOS ends the walk), from the head pass's
+// statistics and the raw logit at the draft token it recorded.
+__device__ __forceinline__ bool head_accepts(const Args &a, int ub, int i) {
+  const int rt = ub * a.rpb + i, rd = ub * a.rpb + a.K + 1 + i;
+  const int traw = a.tokens[(long long)ub * a.K + i];
+  const float u = a.U[(long long)ub * a.ustride + i];
+  const float2 st = row_stat(a, rt), sd = row_stat(a, rd);
+  const float pt = __builtin_amdgcn_exp2f((a.rawtok[rt] - st.x) * a.c) * st.y;
+  const float qd = __builtin_amdgcn_exp2f((a.rawtok[rd] - sd.x) * a.c) * sd.y;
+  const bool valid = traw >= 0 && traw < a.V;
+  return valid && u <= ratio_cpp(pt, qd) && traw != a.eos;
+}
+
+// Whether row group ub accepted every head position, i.e. needs its tail
+// rows.  Every thread of the work-group gets the answer; every load is
+// independent of the others.
 template <int NT>
 __device__ bool tail_needed(const Args &a, int ub) {
   __shared__ int all_ok;
   if (threadIdx.x == 0) all_ok = 1;
   __syncthreads();
-  for (int i = threadIdx.x; i < a.P; i += NT) {
-    const int rt = ub * a.rpb + i, rd = ub * a.rpb + a.K + 1 + i;
-    const int traw = a.tokens[(long long)ub * a.K + i];
-    const float u = a.U[(long long)ub * a.ustride + i];
-    const float2 st = row_stat(a, rt), sd = row_stat(a, rd);
-    const float pt = __builtin_amdgcn_exp2f((a.rawtok[rt] - st.x) * a.c) * st.y;
-    const float qd = __builtin_amdgcn_exp2f((a.rawtok[rd] - sd.x) * a.c) * sd.y;
-    const bool valid = traw >= 0 && traw < a.V;
-    if (!(valid && u <= ratio_cpp(pt, qd)) || traw == a.eos) atomicAnd(&all_ok, 0);
-  }
+  for (int i = threadIdx.x; i < a.P; i += NT)
+    if (!head_accepts(a, ub, i)) atomicAnd(&all_ok, 0);
   __syncthreads();
   return all_ok != 0;
 }
 
-// One work-group per (entry y of the row set, slice x): online
-// (max, sum exp2) over the slice.
-template <int NT, int W>
-__global__ __launch_bounds__(NT) void stats_kernel(Args a, int set) {
-  const int r = set_row(a, set, (int)blockIdx.x);
-  if (r < 0) return;
-  if (set == kRowsTail && !tail_needed<NT>(a, r / a.rpb)) return;
+// Online (max, sum exp2) of slice `slice` of row r (W: elements per vector
+// load), block-wide.  U (16-byte vectors per thread in flight per round)
+// does not change the result: a thread folds its vectors in index order.
+template <int NT, int W, int U>
+__device__ __forceinline__ float2 slice_partial(const Args &a, int r, int slice) {
   const float c = a.c;
-  const long long s0 = (long long)blockIdx.y * a.Vw / a.S;
-  const long long s1 = (long long)(blockIdx.y + 1) * a.Vw / a.S;
+  const long long s0 = (long long)slice * a.Vw / a.S;
+  const long long s1 = (long long)(slice + 1) * a.Vw / a.S;
   const float *row = row_ptr_u(a, r / a.rpb, r % a.rpb);
   float m = -INFINITY, s = 0.0f;
   if (W == 4) {
     // rounds of U vectors per thread, every load of a round issued before
     // the first use; in the last round a lane past the slice reloads its
     // last vector and folds -inf instead (exp2(-inf) = 0 and the max is
-    // unchanged, so that is exactly nothing).  A thread folds its vectors
-    // in index order, so the partial does not depend on U.
+    // unchanged, so that is exactly nothing)
     const float4 *p4 = reinterpret_cast<const float4 *>(row);
-    constexpr int U = 4;
     for (long long i0 = s0 + threadIdx.x; i0 < s1; i0 += U * NT) {
       float4 v[U];
 #pragma unroll
@@ -297,15 +297,82 @@ __global__ __launch_bounds__(NT) void stats_kernel(Args a, int set) {
       s += __builtin_amdgcn_exp2f((v - ms) * c);
     }
   }
-  const float2 out = block_ms<NT>(m, s, c);
+  return block_ms<NT>(m, s, c);
+}
+
+// One work-group per (entry y of the row set, slice x): online
+// (max, sum exp2) over the slice.
+template <int NT, int W>
+__global__ __launch_bounds__(NT) void stats_kernel(Args a, int set) {
+  const int r = set_row(a, set, (int)blockIdx.x);
+  if (r < 0) return;
+  if (set == kRowsTail && !tail_needed<NT>(a, r / a.rpb)) return;
+  const float2 out = slice_partial<NT, W, 4>(a, r, (int)blockIdx.y);
   if (threadIdx.x == 0) {
     a.part[(long long)r * a.S + blockIdx.y] = out;
     if (set == kRowsHead) {
       // the raw logit at this position's draft token, by the slice holding it
+      const long long s0 = (long long)blockIdx.y * a.Vw / a.S;
+      const long long s1 = (long long)(blockIdx.y + 1) * a.Vw / a.S;
       const int j = r % a.rpb, i = j <= a.K ? j : j - a.K - 1;
       const int t = min(max(a.tokens[(long long)(r / a.rpb) * a.K + i], 0), a.V - 1);
-      if ((long long)t >= s0 * W && (long long)t < s1 * W) a.rawtok[r] = row[t];
+      if ((long long)t >= s0 * W && (long long)t < s1 * W)
+        a.rawtok[r] = row_ptr_u(a, r / a.rpb, j)[t];
     }
+  }
+}
+
+// Threads of a statistics work-group (512 and 1024 measured 1% and 10%
+// slower per C2 step).
+constexpr int kStatsNT = 256;
+// Row groups the balanced tail pass can list in LDS.
+constexpr int kTailMaxGroups = 4096;
+
+// The tail pass, balanced over the device (16-byte loads; row groups <=
+// kTailMaxGroups).  A grid of one work-group per (tail row, slice) leaves
+// most work-groups with nothing to do (their sequence rejected a head
+// position), and the CUs that happen to hold several busy ones pace the
+// pass.  Here every work-group lists the groups that need their tail rows
+// (one thread per group) and takes every gridDim.x-th (group, tail row,
+// slice) item of that list, so every CU streams about the same bytes.  Each
+// item's partial is the one stats_kernel computes for that (row, slice).
+template <int NT>
+__global__ __launch_bounds__(NT) void stats_tail_kernel(Args a) {
+  __shared__ int list[kTailMaxGroups];
+  __shared__ int wcnt[NT / 64];
+  __shared__ int base;
+  const int groups = a.R / a.rpb;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) base = 0;
+  __syncthreads();
+  for (int g0 = 0; g0 < groups; g0 += NT) {
+    const int ub = g0 + (int)threadIdx.x;
+    bool need = ub < groups;
+    if (need) {
+      bool ok = true;  // every position's loads issued together
+      for (int i = 0; i < a.P; ++i) ok &= head_accepts(a, ub, i);
+      need = ok;
+    }
+    const unsigned long long m = __ballot(need);
+    if (lane == 0) wcnt[wave] = (int)__popcll(m);
+    __syncthreads();
+    int off = base;
+    for (int w = 0; w < wave; ++w) off += wcnt[w];
+    if (need) list[off + (int)__popcll(m & ((1ull << lane) - 1ull))] = ub;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int w = 0; w < NT / 64; ++w) base += wcnt[w];
+    __syncthreads();
+  }
+  const int K = a.K, P = a.P, per = 2 * (K - P) + 1;
+  const long long total = (long long)base * per * a.S;
+  for (long long k = blockIdx.x; k < total; k += gridDim.x) {
+    const int ub = list[k / ((long long)per * a.S)];
+    const int rem = (int)(k % ((long long)per * a.S));
+    const int q = rem / a.S, slice = rem % a.S;
+    const int r = ub * a.rpb + (q <= K - P ? P + q : K + 1 + P + (q - (K - P + 1)));
+    const float2 out = slice_partial<NT, 4, 4>(a, r, slice);
+    if (threadIdx.x == 0) a.part[(long long)r * a.S + slice] = out;
   }
 }
 
@@ -1514,6 +1581,10 @@ static size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
 // 1024 work-groups (slices of at least 256 units).  A function of the shape
 // only, so every pass over a row combines the same partials in the same
 // order.
+// Work-groups per CU of the balanced tail pass (1 and 2 measured slower;
+// busy work-groups need other waves beside them on their CU to keep enough
+// loads in flight).
+constexpr int kTailPerCU = 3;
 static int stats_slices(long long R, long long Vw) {
   const long long by_len = (Vw + 16383) / 16384;
   const long long by_rows = std::min<long long>((1024 + R - 1) / R, std::max<long long>(1, Vw / 256));
@@ -1680,15 +1751,21 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
       const char *name = set == kRowsHead ? "chain_stats_head"
                          : set == kRowsTail ? "chain_stats_tail" : "chain_stats";
       if (vec)
-        CFA_LAUNCH(name, (stats_kernel<256, 4>), grid, dim3(256), 0, st, a, set);
+        CFA_LAUNCH(name, (stats_kernel<kStatsNT, 4>), grid, dim3(kStatsNT), 0, st, a, set);
       else
-        CFA_LAUNCH(name, (stats_kernel<256, 1>), grid, dim3(256), 0, st, a, set);
+        CFA_LAUNCH(name, (stats_kernel<kStatsNT, 1>), grid, dim3(kStatsNT), 0, st, a, set);
       return CFA_OK;
     };
     int rc;
     if (two_pass) {
       if ((rc = stats(kRowsHead, groups * 2 * a.P)) != CFA_OK) return rc;
-      if ((rc = stats(kRowsTail, groups * (2 * (K - a.P) + 1))) != CFA_OK) return rc;
+      if (vec && groups <= kTailMaxGroups) {
+        const long long items = (long long)groups * (2 * (K - a.P) + 1) * a.S;
+        const int grid = (int)std::min<long long>(items, (long long)kTailPerCU * device_cu_count());
+        CFA_LAUNCH("chain_stats_tail", stats_tail_kernel<kStatsNT>, dim3(grid), dim3(kStatsNT), 0, st, a);
+      } else if ((rc = stats(kRowsTail, groups * (2 * (K - a.P) + 1))) != CFA_OK) {
+        return rc;
+      }
     } else if ((rc = stats(kRowsAll, R)) != CFA_OK) {
       return rc;
     }

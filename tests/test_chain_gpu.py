@@ -239,16 +239,21 @@ def _chain_outputs(out):
                                        out.eos)]
 
 
-@pytest.mark.parametrize("case", ["c2", "all_accept", "eos_in_head", "small_v"])
+@pytest.mark.parametrize("case", ["c2", "all_accept", "eos_in_head", "small_v", "many_groups"])
 def test_two_pass_statistics_match_one_pass(device, case):
     """cpp rules with logits read the rows of positions 0..2 first, and the
     rest only for sequences that accepted all three.  Every row is cut into
     the same slices in both passes, so the outputs are bit-identical to the
     one-pass run (return_probs=True reads every row), which the oracle checks
-    in test_logits_path_matches_oracle."""
+    in test_logits_path_matches_oracle.  The tail pass is the balanced one
+    (stats_tail_kernel) for 16-byte rows and at most 4096 sequences, else the
+    one-work-group-per-(row, slice) kernel: small_v (V % 4 != 0) and
+    many_groups (B > 4096) take the latter."""
     T, eos = 0.7, -1
     if case == "small_v":
         tl, dl, tok, U = c2_inputs(seed=91, B=33, K=5, V=3001, temperature=T)
+    elif case == "many_groups":
+        tl, dl, tok, U = c2_inputs(seed=93, B=4100, K=4, V=256, temperature=T)
     else:
         tl, dl, tok, U = c2_inputs(seed=92, B=64, K=8, V=128256, temperature=T)
     if case == "all_accept":   # draft = target: every ratio is 1, every sequence needs its tail
