@@ -485,7 +485,7 @@ def main() -> int:
 
     kern = {}
     for name in ("chain_stats_head", "chain_stats_tail", "chain_decide", "chain_plan",
-                 "chain_mw_sums", "chain_mw_records", "chain_mw_walk", "chain_finish"):
+                 "chain_mw_first", "chain_mw_records", "chain_mw_walk", "chain_finish"):
         n, ms = _lib.profile_query(name)
         kern[name] = ms / args.steps  # per step (records and walk run twice)
     _lib.profile_reset()

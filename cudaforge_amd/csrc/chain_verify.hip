@@ -118,6 +118,8 @@ struct Args {
   int *badcnt;            // [2, B]
   MwBad *bad;             // [2, B, kMwMaxBad]
   float *x0;              // [2, B, kMwChunk] chunk 0's element values per pass
+  unsigned long long *flags;  // [B, NC] look-back words of the first exact pass
+  int mw_reset;           // the first statistics pass zeroes flags and badcnt
   float *rawtok;          // [R] head pass: a row's raw logit at its position's draft token
   int32_t *out_accept_len, *out_tokens, *out_num_emitted, *out_final, *out_eos;
 };
@@ -302,8 +304,12 @@ __device__ __forceinline__ float2 slice_partial(const Args &a, int r, int slice)
 
 // One work-group per (entry y of the row set, slice x): online
 // (max, sum exp2) over the slice.
+__device__ void mw_reset_share(const Args &a, long long wg, long long nwg);
+
 template <int NT, int W>
 __global__ __launch_bounds__(NT) void stats_kernel(Args a, int set) {
+  if (a.mw_reset && set != kRowsTail)
+    mw_reset_share(a, (long long)blockIdx.y * gridDim.x + blockIdx.x, (long long)gridDim.x * gridDim.y);
   const int r = set_row(a, set, (int)blockIdx.x);
   if (r < 0) return;
   if (set == kRowsTail && !tail_needed<NT>(a, r / a.rpb)) return;
@@ -856,52 +862,6 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return v;
 }
 
-// One wave per chunk: chunk c = 4 * blockIdx.x + wave, lane = tile in chunk.
-// With `decide` (cpp rules) every work-group first takes sequence b's
-// decision itself (decide_cpp: the same inputs, so the same job everywhere)
-// and the first one stores it, which saves the separate decide launch.
-__global__ __launch_bounds__(kMwNT) void mw_sums_kernel(Args a, int decide) {
-  const int b = blockIdx.y, lane = threadIdx.x & 63;
-  const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
-  MwJob j;
-  if (decide) {
-    __shared__ DecideLds L;
-    __shared__ MwJob sj;
-    decide_gather(a, b, threadIdx.x, kMwNT, L);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      sj = decide_cpp(a, b, L);
-      if (blockIdx.x == 0) write_job(a, b, sj);
-    }
-    __syncthreads();
-    j = sj;
-  } else {
-    j = a.jobs[b];
-  }
-  if (j.kind != kResid && j.kind != kPlain) return;
-  if (c >= a.NC) return;
-  const MwElem e = mw_elem(a, b, j, kPassSum);
-  const long long i0 = ((long long)c * kMwChunkTiles + lane) * kMwTile;
-  float tv[kMwTile], dv[kMwTile];
-  mw_load16(a, e.t.p, i0, tv);
-  if (j.kind == kResid) mw_load16(a, e.d.p, i0, dv);
-  float st = 0.0f, sx = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kMwTile; ++k) {
-    if (i0 + k < a.V) {
-      const float tp = e.t.eval(tv[k]);
-      st += tp;
-      if (j.kind == kResid) sx += relu_ref(tp - e.d.eval(dv[k]));
-    }
-  }
-  st = wave_sum_f32(st);
-  sx = wave_sum_f32(sx);
-  if (lane == 0) {
-    a.csum_t[(long long)b * a.NC + c] = st;
-    a.csum_x[(long long)b * a.NC + c] = sx;
-  }
-}
-
 // Approximate running value at the start of chunk c: the chunk sums before
 // it, in a fixed order (one wave).
 __device__ float mw_entry_prefix(const float *csum, int c) {
@@ -1041,6 +1001,144 @@ __device__ __forceinline__ void mw_records_chunk(const Args &a, int b, int c, in
   }
   if (rec.status == kChunkTiles) rec.near = 1;
   if (lane == 0) crec[c] = rec;
+}
+
+// Zeroes this work-group's share (work-group wg of nwg) of the first exact
+// pass's look-back words and of both passes' cache counters.  The first
+// kernel of every call that draws exactly runs this, so nothing in the
+// workspace has to start at zero.
+__device__ void mw_reset_share(const Args &a, long long wg, long long nwg) {
+  const long long nt = blockDim.x, i0 = wg * nt + threadIdx.x, step = nwg * nt;
+  for (long long i = i0; i < (long long)a.B * a.NC; i += step) a.flags[i] = 0ull;
+  for (long long i = i0; i < 2LL * a.B; i += step) a.badcnt[i] = 0;
+}
+
+__global__ __launch_bounds__(256) void mw_reset_kernel(Args a) {
+  mw_reset_share(a, blockIdx.x, gridDim.x);
+}
+
+// Look-back words: status in bits 62-63 (0 none, 1 the chunk's own sum,
+// 2 the inclusive prefix through the chunk), the fp32 value in bits 0-31.
+// They cross work-groups (and XCDs, whose L2s are not coherent with each
+// other) as agent-scope atomic stores and loads.
+constexpr unsigned long long kLbAgg = 1ull << 62, kLbIncl = 2ull << 62;
+constexpr long kLbSpins = 1l << 16;  // a bounded wait: the value only steers region guesses
+
+__device__ __forceinline__ void lb_store(unsigned long long *p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long lb_load(unsigned long long *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Approximate running value at the start of chunk c of job b by decoupled
+// look-back over the chunks before it (one wave): publish the chunk's own
+// sum, add the predecessors' published sums back to the nearest inclusive
+// prefix, publish the inclusive prefix.  Work-groups start in block order, so
+// a predecessor is already running or done; still, every wait is bounded,
+// and one that runs out keeps what it has -- the value only guides the
+// region guesses of the records, which the walk checks against the exact
+// running value, so a poor value costs time, never correctness.
+__device__ float mw_lookback(const Args &a, int b, int c, float own) {
+  const int lane = threadIdx.x & 63;
+  unsigned long long *fl = a.flags + (long long)b * a.NC;
+  if (c == 0) {
+    if (lane == 0) lb_store(fl, kLbIncl | f2u(own));
+    return 0.0f;
+  }
+  if (lane == 0) lb_store(fl + c, kLbAgg | f2u(own));
+  float pre = 0.0f;
+  long spins = 0;
+  for (int j = c - 1; j >= 0; j -= 64) {
+    const int idx = j - lane;  // lanes look at chunks j, j - 1, ..., j - 63
+    unsigned long long w = 0;
+    int stop = 63;      // lanes 0 .. stop add their value
+    bool done = false;  // an inclusive prefix (or a wait that ran out) ends the look-back
+    for (;;) {
+      w = idx >= 0 ? lb_load(fl + idx) : kLbIncl;  // before chunk 0: an inclusive zero
+      const unsigned long long ready = __ballot((w >> 62) != 0ull);
+      const unsigned long long incl = __ballot((w >> 62) == 2ull);
+      const int fi = incl ? (int)__builtin_ctzll(incl) : 64;
+      const int fw = ~ready ? (int)__builtin_ctzll(~ready) : 64;
+      if (fi < fw) {  // every chunk down to the nearest inclusive prefix has published
+        stop = fi;
+        done = true;
+        break;
+      }
+      if (fw == 64) break;  // 64 own sums: go on below them
+      if (++spins > kLbSpins) {  // keep the chunks before the first silent one
+        stop = fw - 1;
+        done = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    pre += wave_sum_f32(lane <= stop && idx >= 0 ? u2f((uint32_t)w) : 0.0f);
+    if (done) break;
+  }
+  if (lane == 0) lb_store(fl + c, kLbIncl | f2u(pre + own));
+  return pre;
+}
+
+// The first exact pass, with the chunk sums: one wave per chunk (chunk c =
+// 4 * blockIdx.x + wave of job blockIdx.y, lane = tile in the chunk).  With
+// `decide` (cpp rules) every work-group first takes sequence b's decision
+// itself (decide_cpp: the same inputs, so the same job everywhere) and the
+// first one stores it.  Every active job stores its chunk sums of t (the CDF
+// pass of a plain draw, or of the fallback, starts from them); a residual
+// job also stores those of max(0, t - d), finds its chunk's entry value by
+// look-back, and writes the sum pass's records (mw_records_chunk).
+__global__ __launch_bounds__(kMwNT) void mw_first_kernel(Args a, int decide) {
+  const int b = blockIdx.y, lane = threadIdx.x & 63;
+  const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
+  MwJob j;
+  if (decide) {
+    __shared__ DecideLds L;
+    __shared__ MwJob sj;
+    decide_gather(a, b, threadIdx.x, kMwNT, L);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      sj = decide_cpp(a, b, L);
+      if (blockIdx.x == 0) {  // the cache counters were zeroed by an earlier kernel
+        a.jobs[b] = sj;
+        a.res[b] = MwRes{0.0f, 0, -1, -1};
+      }
+    }
+    __syncthreads();
+    j = sj;
+  } else {
+    j = a.jobs[b];
+  }
+  if (j.kind != kResid && j.kind != kPlain) return;
+  if (c >= a.NC) return;
+  const bool resid = j.kind == kResid;
+  const MwElem e = mw_elem(a, b, j, kPassSum);
+  const long long tile = (long long)c * kMwChunkTiles + lane, i0 = tile * kMwTile;
+  float tv[kMwTile], dv[kMwTile], x[kMwTile];
+  mw_load16(a, e.t.p, i0, tv);
+  if (resid) mw_load16(a, e.d.p, i0, dv);
+  float st = 0.0f, sx = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kMwTile; ++k) {
+    x[k] = 0.0f;
+    if (i0 + k < a.V) {
+      const float tp = e.t.eval(tv[k]);
+      st += tp;
+      if (resid) {
+        x[k] = relu_ref(tp - e.d.eval(dv[k]));
+        sx += x[k];
+      }
+    }
+  }
+  st = wave_sum_f32(st);
+  sx = wave_sum_f32(sx);
+  if (lane == 0) {
+    a.csum_t[(long long)b * a.NC + c] = st;
+    a.csum_x[(long long)b * a.NC + c] = sx;
+  }
+  if (!resid) return;
+  const float E0 = mw_lookback(a, b, c, sx);
+  mw_records_chunk(a, b, c, kPassSum, j, E0, x);
 }
 
 // One wave per chunk: chunk c = 4 * blockIdx.x + wave of job blockIdx.y.
@@ -1597,7 +1695,8 @@ constexpr int kHeadPositions = 3;
 
 // Workspace layout (each region 256-byte aligned).
 struct WsLayout {
-  size_t part, apart, rawtok, dec, ufin, jobs, res, csum_x, csum_t, crec, trec, badcnt, bad, x0, total;
+  size_t part, apart, rawtok, dec, ufin, jobs, res, csum_x, csum_t, crec, trec, badcnt, bad, x0, flags,
+      total;
 };
 
 static WsLayout ws_layout(int B, int K, int V, int mode) {
@@ -1627,6 +1726,7 @@ static WsLayout ws_layout(int B, int K, int V, int mode) {
   L.badcnt = take(2 * (size_t)B * sizeof(int));
   L.bad = take(mw ? 2 * (size_t)B * kMwMaxBad * sizeof(MwBad) : 0);
   L.x0 = take(mw ? 2 * (size_t)B * kMwChunk * sizeof(float) : 0);
+  L.flags = take(mw ? (size_t)B * NC * sizeof(unsigned long long) : 0);
   L.total = o;
   return L;
 }
@@ -1743,7 +1843,16 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   a.badcnt = (int *)(ws + L.badcnt);
   a.bad = (MwBad *)(ws + L.bad);
   a.x0 = (float *)(ws + L.x0);
+  a.flags = (unsigned long long *)(ws + L.flags);
+  // the first statistics pass zeroes the look-back words and cache counters;
+  // without one (probabilities input) a small kernel does
+  a.mw_reset = (mode != CFA_MODE_GREEDY && a.logits) ? 1 : 0;
 
+  if (mode != CFA_MODE_GREEDY && !a.logits) {
+    const long long n = std::max<long long>((long long)B * a.NC, 2LL * B);
+    const int grid = (int)std::min<long long>((n + 255) / 256, 1024);
+    CFA_LAUNCH("chain_mw_reset", mw_reset_kernel, dim3(grid), dim3(256), 0, st, a);
+  }
   if (a.logits) {
     const int groups = R / a.rpb;
     auto stats = [&](int set, int entries) -> int {
@@ -1779,8 +1888,7 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   if (mode != CFA_MODE_GREEDY) {
     const dim3 cg((a.NC + kMwNT / 64 - 1) / (kMwNT / 64), B);
     if (mode == CFA_MODE_PYTHON) CFA_LAUNCH("chain_plan", plan_kernel, dim3(1), dim3(256), 0, st, a);
-    CFA_LAUNCH("chain_mw_sums", mw_sums_kernel, cg, dim3(kMwNT), 0, st, a, fused_decide);
-    CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassSum);
+    CFA_LAUNCH("chain_mw_first", mw_first_kernel, cg, dim3(kMwNT), 0, st, a, fused_decide);
     CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassSum);
     CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassCdf);
     CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassCdf);
