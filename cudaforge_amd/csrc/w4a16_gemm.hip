@@ -1,0 +1,379 @@
+// w4a16_gemm.hip -- fused W4A16 GEMM for many rows (bf16 activations), the
+// target model's projections at the verify step (M = B * tree nodes = 504).
+//
+// C [M, N] = A [M, K] . W [K, N], W dequantised from the reference's packed
+// INT4 format (csrc/include/cudaforge/kernels/dequantize.cuh:12-25,
+// tests/unit/test_int4_dequant.py:6-15): word (k / 8, n) of B_quant [K/8, N]
+// holds nibble k % 8 at bits 4 (k % 8); fp16 group scales s and optional fp16
+// zero points z [K / group, N];  w = bf16((nibble - z) * s) formed in fp32,
+// exactly the value cfa_w4a16_dequant writes, so the result equals
+// dequantise-then-GEMM up to the order of the fp32 accumulation.
+//
+// Work-group: a 256 x 256 output tile, eight waves of 128 rows x 64 columns
+// (2 x 4), two per SIMD so that one's waits overlap the other's products.
+// (A 512 x 128 tile dequantises each weight once, but every work-group then
+// re-reads all of A: 0.9 GB per gate/up call, which bounded the kernel.)  K runs in slices of 32 (one
+// v_mfma_f32_16x16x32_bf16 k-step).  Everything a slice needs from memory --
+// its A tile (256 x 32 bf16), packed words (4 x 256) and scale and zero rows
+// -- moves by direct HBM -> LDS transfers into a 3-stage ring, two slices
+// ahead; the packed words of slice s + 1 are dequantised once per work-group
+// (two words per thread) into one of two [n][k] bf16 tiles while slice s is
+// multiplied from the other.  One barrier per slice.  LDS rows of A and of
+// the dequantised tiles are 64 bytes; their 16-byte chunks are swizzled by
+// row so that the operand reads of 16 lanes (16 rows, one chunk) hit
+// distinct banks.
+// Split-K (gridDim.z > 1) writes fp32 partials that a second kernel sums in
+// split order, so every result is reproducible.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+
+#include "abi_internal.hpp"
+#include "lds_dma.hpp"
+
+namespace cfa {
+namespace w4mm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8;
+constexpr int kNT = 64 * kWaves;
+constexpr int kBM = 256;             // rows per work-group
+constexpr int kBN = 256;             // columns per work-group
+constexpr int kWM = 128, kWN = 64;   // rows / columns per wave (2 x 4 waves)
+constexpr int kSK = 32;              // k per slice
+constexpr int kMT = kWM / 16;        // 16-row MFMA tiles per wave
+constexpr int kNTl = kWN / 16;       // 16-column MFMA tiles per wave
+constexpr int kStages = 3;                    // A ring (two slices ahead)
+constexpr int kWSlots = 8;                    // packed-word ring
+constexpr int kABytes = kBM * kSK * 2;        // 16 KiB
+constexpr int kQBytes = (kSK / 8) * kBN * 4;  // 4 KiB of packed words
+constexpr int kSBytes = kBN * 2;              // one scale row (and one zero row)
+constexpr int kWSlot = kQBytes + 2 * kSBytes;
+constexpr int kBTile = kBN * kSK * 2;         // one dequantised slice [n][k], 16 KiB
+constexpr int kAX = kABytes / 1024 / kWaves;  // A transfers per wave per slice (2)
+constexpr int kDW = kBN * (kSK / 8) / kNT;    // packed words a thread dequantises per slice (2)
+static_assert(kBN == 4 * kWN && kBM == 2 * kWM, "2 x 4 waves");
+static_assert(kBN * 2 * 2 == 1024, "one transfer moves the scale and zero rows");
+#ifndef CFA_W4_SGB
+#define CFA_W4_SGB 0
+#endif
+
+struct Args {
+  const uint16_t *A;   // [M, K] bf16
+  const uint32_t *q;   // [K / 8, N]
+  const __half *s;     // [K / group, N]
+  const __half *z;     // [K / group, N] or null
+  uint16_t *C;         // [M, N] bf16
+  float *part;         // [splits, M, N] fp32 partials (splits > 1)
+  int M, N, K, group;
+  int slices_per_split;
+  int mtiles;  // row tiles
+};
+
+// Byte offset of the 16-byte chunk holding k = 8 c .. 8 c + 7 of a 64-byte
+// LDS row r.
+__device__ __forceinline__ int sw_off(int r, int c) { return r * (kSK * 2) + ((c ^ ((r >> 2) & 3)) << 4); }
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// The 8 weights of one packed word as bf16 pairs (k, k + 1): bf16((nibble -
+// z) * s) with the difference and the product rounded in fp32, as
+// cfa_w4a16_dequant.  Even nibbles are the low halves of the bytes of
+// w & 0x0f0f0f0f and odd ones of (w >> 4) & 0x0f0f0f0f, so each converts
+// with one byte-to-float instruction; each pair packs with one conversion.
+__device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float z) {
+  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  uint32_t o[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float f0 = ((float)((lo >> (8 * p)) & 0xffu) - z) * s;
+    const float f1 = ((float)((hi >> (8 * p)) & 0xffu) - z) * s;
+    o[p] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{f0, f1}, bf16x2));
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// vmcnt(N) lgkmcnt(0)
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | (((N >> 4) & 3) << 14));
+}
+
+__global__ __launch_bounds__(kNT, 1) void w4mm_kernel(Args a) {
+  __shared__ __align__(16) uint8_t aring[kStages * kABytes];
+  __shared__ __align__(16) uint8_t wring[kWSlots * kWSlot];
+  __shared__ __align__(16) uint8_t btile[2][kBTile];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  // the row tiles of one column tile take linear indices 8 apart: one XCD
+  // (work-groups go to the 8 XCDs round-robin), whose L2 then serves their
+  // common packed weights
+  const int L = blockIdx.x, mt = a.mtiles;
+  const int ntile = (L % 8) + 8 * (L / (8 * mt)), mti = (L / 8) % mt;
+  if (ntile >= a.N / kBN) return;  // padding of the last group of 8 column tiles
+  const int n0 = ntile * kBN, mb = mti * kBM;
+  const int nsl = a.K / kSK;
+  const int s0 = blockIdx.z * a.slices_per_split;
+  const int s1 = min(nsl, s0 + a.slices_per_split);
+  const int g = lane >> 4, col = lane & 15;
+  if (s0 >= s1) return;  // (never: the host sizes the splits) -- uniform per work-group
+
+  // Transfer sources (the slice's k offset is added per issue).  A transfer
+  // x of this wave covers stage rows 16 x .. 16 x + 15: lane i lands at row
+  // 16 x + i / 4, chunk position i % 4, and so fetches chunk
+  // (i % 4) ^ ((row / 4) % 4) of that row (rows past M re-read row M - 1).
+  const uint16_t *asrc[kAX];
+#pragma unroll
+  for (int j = 0; j < kAX; ++j) {
+    const int row = 16 * (wave * kAX + j) + (lane >> 2);
+    const int c = (lane & 3) ^ ((row >> 2) & 3);
+    asrc[j] = a.A + (long long)min(mb + row, a.M - 1) * a.K + 8 * c;
+  }
+  // the word-ring transfer of each wave: waves 0-3 packed row w of the slice
+  // (lane: words 4 lane ..), wave 4 the scale row (lanes < 32) and the zero
+  // row (lanes >= 32), 8 columns per lane; waves 5-7 repeat wave 0's (the
+  // same bytes to the same place), so that every wave issues one word-ring
+  // transfer and then kAX A transfers per slice
+  const int ww = wave >= 5 ? 0 : wave;
+  const uint32_t *qsrc = a.q + (long long)(ww & 3) * a.N + n0 + 4 * lane;
+  const __half *ssrc = (lane >= 32 && a.z ? a.z : a.s) + n0 + 8 * (lane & 31);
+  // Slices past the last are clamped to it: a repeat transfer rewrites the
+  // same bytes in place, keeping every wave's transfer count per iteration
+  // fixed (the waits below count transfers).
+  auto issue_w = [&](int u) {
+    u = min(u, s1 - 1);
+    uint8_t *dst = wring + (u % kWSlots) * kWSlot;
+    const int k0 = u * kSK;
+    if (ww < 4)
+      dma16(qsrc + (long long)(k0 / 8) * a.N, (CFA_LDS void *)(dst + 1024 * ww));
+    else
+      dma16(ssrc + (long long)(k0 / a.group) * a.N, (CFA_LDS void *)(dst + kQBytes));
+  };
+  auto issue_a = [&](int u) {
+    u = min(u, s1 - 1);
+    uint8_t *dst = aring + (u % kStages) * kABytes;
+    const int k0 = u * kSK;
+#pragma unroll
+    for (int j = 0; j < kAX; ++j) dma16(asrc[j] + k0, (CFA_LDS void *)(dst + 1024 * (wave * kAX + j)));
+  };
+
+  // this thread's dequantisation share: column dc, packed rows kDW dp ..
+  // kDW dp + kDW - 1 of a slice
+  const int dc = tid & (kBN - 1), dp = tid / kBN;
+  // without zero points the zero row holds the scales again, multiplied by 0
+  // here (scales are finite), so that no branch splits the loop body
+  const float zmul = a.z != nullptr ? 1.0f : 0.0f;
+  auto words_of = [&](int u, uint32_t (&w)[kDW], float &sf, float &zf) {
+    const uint8_t *st = wring + (u % kWSlots) * kWSlot;
+#pragma unroll
+    for (int j = 0; j < kDW; ++j)
+      w[j] = *reinterpret_cast<const uint32_t *>(st + ((kDW * dp + j) * kBN + dc) * 4);
+    const __half *sc = reinterpret_cast<const __half *>(st + kQBytes);
+    sf = __half2float(sc[dc]);
+    zf = __half2float(sc[kBN + dc]) * zmul;
+  };
+
+  f32x4 acc[kMT][kNTl];
+#pragma unroll
+  for (int i = 0; i < kMT; ++i)
+#pragma unroll
+    for (int j = 0; j < kNTl; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // operand read offsets of this lane
+  int aoff[kMT], boff[kNTl];
+#pragma unroll
+  for (int i = 0; i < kMT; ++i) aoff[i] = sw_off(wm * kWM + 16 * i + col, g);
+#pragma unroll
+  for (int j = 0; j < kNTl; ++j) boff[j] = sw_off(wn * kWN + 16 * j + col, g);
+
+  // Issue order, per wave: W(s0), W(s0 + 1), then per iteration u = s0 - 2,
+  // s0 - 1, s0, ...: W(u + 4), A(u + 2).  At the top of iteration sl, A(sl)
+  // and everything issued before it (among them W(sl + 1)) have landed once
+  // at most the 1 + kAX transfers of iteration sl - 1 are in flight.
+  issue_w(s0);
+  issue_w(s0 + 1);
+  issue_w(s0 + 2);
+  issue_a(s0);
+  issue_w(s0 + 3);
+  issue_a(s0 + 1);
+  {
+    // W(s0) landed: 1 + 1 + kAX + 1 + kAX transfers after it
+    static_assert(kAX == 2, "wait count below");
+    wait_vm_lgkm0<3 + 2 * kAX>();
+    block_barrier();
+    uint32_t w[kDW];
+    float sf, zf;
+    words_of(s0, w, sf, zf);
+#pragma unroll
+    for (int j = 0; j < kDW; ++j)
+      *reinterpret_cast<uint4 *>(btile[s0 & 1] + sw_off(dc, kDW * dp + j)) = dequant_word(w[j], sf, zf);
+  }
+  for (int sl = s0; sl < s1; ++sl) {
+    // A(sl), W(sl + 1) and this wave's dequantised writes of slice sl are
+    // done (and, after the barrier, every wave's); slice sl - 1's A stage
+    // and dequantised tile, and the word slot of slice sl, are free
+    wait_vm_lgkm0<1 + kAX>();
+    block_barrier();
+    issue_w(sl + 4);
+    issue_a(sl + 2);
+    // The next slice's packed word and scales first (its dequantisation can
+    // start while this slice's operands are in flight), then this slice's
+    // operands, the products with the dequantisation's VALU work spread
+    // between them, and its LDS write.  Branch-free: past the last slice the
+    // word of the last one is dequantised again into the tile nobody reads.
+    uint32_t w[kDW];
+    float sf, zf;
+    words_of(min(sl + 1, s1 - 1), w, sf, zf);
+    const uint8_t *as = aring + (sl % kStages) * kABytes;
+    const uint8_t *bs = btile[sl & 1];
+    bf16x8 bfr[kNTl], afr[kMT];
+#pragma unroll
+    for (int j = 0; j < kNTl; ++j) bfr[j] = *reinterpret_cast<const bf16x8 *>(bs + boff[j]);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) afr[i] = *reinterpret_cast<const bf16x8 *>(as + aoff[i]);
+    uint4 dq[kDW];
+#pragma unroll
+    for (int j = 0; j < kDW; ++j) dq[j] = dequant_word(w[j], sf, zf);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+      for (int j = 0; j < kNTl; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[i], bfr[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kDW; ++j)
+      *reinterpret_cast<uint4 *>(btile[(sl + 1) & 1] + sw_off(dc, kDW * dp + j)) = dq[j];
+#if CFA_W4_SGB
+    __builtin_amdgcn_sched_group_barrier(0x0100, kNTl + kMT + 3, 0);
+#pragma unroll
+    for (int k = 0; k < kMT * kNTl; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x0002, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);
+#endif
+  }
+  // drain: the last iterations' repeat transfers must land before exit
+  wait_vm_lgkm0<0>();
+
+  // acc[i][j][e]: row mb + 128 wm + 16 i + 4 g + e, column n0 + 64 wn + 16 j + lane % 16
+  const int r0 = mb + wm * kWM + 4 * g, c0 = n0 + wn * kWN + col;
+  if (gridDim.z == 1) {
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = r0 + 16 * i + e;
+        if (row >= a.M) continue;
+        uint16_t *cr = a.C + (long long)row * a.N + c0;
+#pragma unroll
+        for (int j = 0; j < kNTl; ++j) cr[16 * j] = __builtin_bit_cast(uint16_t, (__bf16)acc[i][j][e]);
+      }
+  } else {
+    float *pp = a.part + (long long)blockIdx.z * a.M * a.N;
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = r0 + 16 * i + e;
+        if (row >= a.M) continue;
+        float *pr = pp + (long long)row * a.N + c0;
+#pragma unroll
+        for (int j = 0; j < kNTl; ++j) pr[16 * j] = acc[i][j][e];
+      }
+  }
+}
+
+// C = bf16(sum of the split partials in split order), four columns per thread.
+__global__ __launch_bounds__(256) void w4mm_reduce_kernel(const float *part, uint16_t *C, long long MN,
+                                                          int splits) {
+  const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= MN) return;
+  float4 acc = *reinterpret_cast<const float4 *>(part + i);
+  for (int s = 1; s < splits; ++s) {
+    const float4 v = *reinterpret_cast<const float4 *>(part + (long long)s * MN + i);
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  uint2 o;
+  o.x = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)acc.x) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)acc.y) << 16);
+  o.y = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)acc.z) |
+        ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)acc.w) << 16);
+  *reinterpret_cast<uint2 *>(C + i) = o;
+}
+
+// Splits of K: enough work-groups for every CU, each split at least 8
+// slices; *spp slices per split, and no split empty.
+int choose_splits(int M, int N, int K, int cus, int *spp) {
+  const long long tiles = (long long)((M + kBM - 1) / kBM) * (N / kBN);
+  const int nsl = K / kSK;
+  // as many splits as fit in one round of work-groups (one per CU)
+  const int s = (int)std::max<long long>(1, std::min<long long>({(long long)cus / std::max(tiles, 1LL), (long long)nsl / 8, 16LL}));
+  const int per = (nsl + s - 1) / s;
+  if (spp) *spp = per;
+  return (nsl + per - 1) / per;
+}
+
+}  // namespace w4mm
+}  // namespace cfa
+
+extern "C" size_t cfa_w4a16_gemm_zp_workspace_size(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || N % cfa::w4mm::kBN != 0 || K % cfa::w4mm::kSK != 0) return 0;
+  const int s = cfa::w4mm::choose_splits(M, N, K, cfa::abi::device_cu_count(), nullptr);
+  return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
+}
+
+extern "C" int cfa_w4a16_gemm_zp(const void *a, const uint32_t *b_quant, const void *scales,
+                                 const void *zeros, int M, int N, int K, int group_size, void *c,
+                                 void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace cfa::abi;
+  using namespace cfa::w4mm;
+  clear_error();
+  if (M <= 0 || N <= 0 || K <= 0) return fail_arg("M, N and K must be positive");
+  if (N % kBN != 0) return fail_arg("N must be a multiple of 256");
+  if (K % kSK != 0) return fail_arg("K must be a multiple of 32");
+  if (group_size <= 0 || group_size % kSK != 0 || K % group_size != 0)
+    return fail_arg("group_size must be a multiple of 32 that divides K");
+  if (!a || !b_quant || !scales || !c) return fail_arg("null pointer");
+  if ((((uintptr_t)a | (uintptr_t)c | (uintptr_t)b_quant | (uintptr_t)scales | (uintptr_t)zeros) & 15) != 0)
+    return fail_arg("a, b_quant, scales, zeros and c must be 16-byte aligned");
+  int spp = 0;
+  const int splits = choose_splits(M, N, K, device_cu_count(), &spp);
+  const size_t need = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
+  if (need && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15) != 0))
+    return fail_arg("workspace too small (see cfa_w4a16_gemm_zp_workspace_size)");
+  Args g{};
+  g.A = (const uint16_t *)a;
+  g.q = b_quant;
+  g.s = (const __half *)scales;
+  g.z = (const __half *)zeros;
+  g.C = (uint16_t *)c;
+  g.part = (float *)workspace;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.group = group_size;
+  g.slices_per_split = spp;
+  const long long mt = (M + kBM - 1) / kBM;
+  if (mt > 65535) return fail_arg("M too large");
+  hipStream_t st = (hipStream_t)stream;
+  const long long blocks = mt * ((N / kBN + 7) / 8) * 8;  // column tiles padded to groups of 8
+  if (blocks > 0x7fffffffLL) return fail_arg("problem too large");
+  g.mtiles = (int)mt;
+  CFA_LAUNCH("w4a16_gemm_zp", w4mm_kernel, dim3((unsigned)blocks, 1, (unsigned)splits),
+             dim3(kNT), 0, st, g);
+  if (splits > 1) {
+    const long long MN = (long long)M * N;  // N % 128 == 0: four columns per thread
+    CFA_LAUNCH("w4a16_gemm_zp_reduce", w4mm_reduce_kernel, dim3((unsigned)((MN / 4 + 255) / 256)),
+               dim3(256), 0, st, (const float *)workspace, (uint16_t *)c, MN, splits);
+  }
+  return CFA_OK;
+}

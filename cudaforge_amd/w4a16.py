@@ -20,8 +20,8 @@ import torch
 from . import _lib
 from .verify import _stream_ptr
 
-__all__ = ["pack_int4_weights", "w4a16_dequant", "w4a16_gemm", "int4_gemm_dequant",
-           "W4A16Linear"]
+__all__ = ["pack_int4_weights", "w4a16_dequant", "w4a16_gemm", "w4a16_gemm_zp",
+           "int4_gemm_dequant", "W4A16Linear"]
 
 
 def pack_int4_weights(w_int4: torch.Tensor) -> torch.Tensor:
@@ -98,6 +98,48 @@ def w4a16_gemm(a: torch.Tensor, b_quant: torch.Tensor, scales: torch.Tensor, *,
     return out
 
 
+def gemm_zp_ok(a: torch.Tensor, b_quant: torch.Tensor, group_size: int) -> bool:
+    """Whether cfa_w4a16_gemm_zp takes this problem (else dequantise + GEMM)."""
+    K, N = b_quant.shape[0] * 8, b_quant.shape[1]
+    return (a.dtype == torch.bfloat16 and a.dim() == 2 and a.shape[1] == K and N % 256 == 0
+            and K % 32 == 0 and group_size % 32 == 0 and K % group_size == 0
+            and a.is_contiguous() and b_quant.is_contiguous() and a.data_ptr() % 16 == 0)
+
+
+def w4a16_gemm_zp(a: torch.Tensor, b_quant: torch.Tensor, scales: torch.Tensor,
+                  zeros: Optional[torch.Tensor] = None, *, group_size: int = 128,
+                  out: Optional[torch.Tensor] = None,
+                  workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused a [M, K] bf16 x W -> [M, N] bf16 with W = bf16((nibble - z) * s),
+    the weights cfa_w4a16_dequant writes (cfa_w4a16_gemm_zp); `workspace`
+    (uint8, cfa_w4a16_gemm_zp_workspace_size bytes) holds split-K partials."""
+    if a.dtype != torch.bfloat16 or a.dim() != 2:
+        raise ValueError("a must be a bf16 [M, K] tensor")
+    M, K = a.shape
+    N = b_quant.shape[1]
+    if b_quant.shape[0] * 8 != K:
+        raise ValueError("K of a and b_quant differ")
+    if scales.dtype != torch.float16 or tuple(scales.shape) != (K // group_size, N):
+        raise ValueError("scales must be fp16 [K/group_size, N]")
+    if zeros is not None and (zeros.dtype != torch.float16 or zeros.shape != scales.shape):
+        raise ValueError("zeros must be fp16 [K/group_size, N]")
+    lib = _lib.load()
+    need = lib.cfa_w4a16_gemm_zp_workspace_size(M, N, K)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=a.device)
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    sc = scales.contiguous()
+    zz = zeros.contiguous() if zeros is not None else None
+    with torch.cuda.device(a.device):
+        rc = lib.cfa_w4a16_gemm_zp(a.data_ptr(), b_quant.data_ptr(), sc.data_ptr(),
+                                   zz.data_ptr() if zz is not None else None, M, N, K,
+                                   group_size, out.data_ptr(), workspace.data_ptr(),
+                                   workspace.numel(), _stream_ptr(a.device))
+    _lib.check(rc, "cfa_w4a16_gemm_zp")
+    return out
+
+
 class W4A16Linear:
     """y = x @ W with W [K, N] held as packed INT4 + fp16 group scales and
     zero points, w = (nibble - z) * s (dequantize.cuh:12-25).
@@ -117,12 +159,23 @@ class W4A16Linear:
                        ).to(torch.float16)
         self.zeros = torch.full_like(self.scales, 7.5)
 
-    # class-wide switch: the fused GEMM (cfa_w4a16_gemm) where the shape
-    # allows; off by default because dequantise + hipBLASLt is faster at the
-    # verify step's shapes on MI355X (M = 504: 70 vs 105 us for QKV)
+    # class-wide switches: `fused_zp` (default) multiplies with
+    # cfa_w4a16_gemm_zp, which dequantises in LDS per output tile, where the
+    # shape allows (bf16, N % 256 == 0); at the verify step's M = 504 it takes
+    # 51 / 42 / 150 / 85 us for QKV / O / gate-up / down against 51 / 43 / 175
+    # / 110 us for dequantise + hipBLASLt.  `fused` selects the older
+    # cfa_w4a16_gemm (no zero points) instead; off.
+    fused_zp = True
     fused = False
 
     def __call__(self, x: torch.Tensor, scratch: torch.Tensor) -> torch.Tensor:
+        if self.fused_zp and gemm_zp_ok(x, self.qweight, self.group):
+            # the scratch that would hold the dequantised matrix holds the
+            # split-K partials instead (at most 16 x M x N fp32, far less than
+            # K x N bf16 at the model's shapes)
+            ws = scratch.view(torch.uint8)
+            return w4a16_gemm_zp(x, self.qweight, self.scales, self.zeros, group_size=self.group,
+                                 workspace=ws)
         if self.fused and fused_gemm_ok(x, self.qweight, self.zeros, self.group):
             return w4a16_gemm(x, self.qweight, self.scales, group_size=self.group)
         # [N, K] (K contiguous): x @ w^T runs about 20% faster on hipBLASLt

@@ -307,6 +307,22 @@ int cfa_w4a16_dequant_t(const uint32_t *b_quant, const void *scales, const void 
 int cfa_w4a16_gemm(const void *a, const uint32_t *b_quant, const void *scales, int M, int N,
                    int K, int group_size, int fp16, void *c, void *stream);
 
+/* Fused W4A16 GEMM with zero points, for many rows (the verify step's target
+ * projections; replaces launch_int4_gemm_dequant / int4_gemm_dequant_triton,
+ * int4_dequant_triton.py:86-131, for bf16 activations): c [M, N] bf16 =
+ * a [M, K] bf16 x W with W = bf16((nibble - z) * s) exactly as
+ * cfa_w4a16_dequant writes it (zeros may be NULL: z = 0), dequantised once
+ * per 256 x 256 output tile into LDS, fp32 accumulation on MFMA.  N % 256 ==
+ * 0, K % 32 == 0, group_size % 32 == 0 dividing K; a and c 16-byte aligned,
+ * b_quant 4-byte, scales and zeros 2-byte.  Splits K over the work-groups
+ * when the output tiles alone leave CUs idle: the fp32 partials go to
+ * `workspace` (cfa_w4a16_gemm_zp_workspace_size bytes, 0 when no split is
+ * used) and are summed in split order, so results are reproducible. */
+size_t cfa_w4a16_gemm_zp_workspace_size(int M, int N, int K);
+int cfa_w4a16_gemm_zp(const void *a, const uint32_t *b_quant, const void *scales,
+                      const void *zeros, int M, int N, int K, int group_size, void *c,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Fused layers of the model-scale verify step (bf16 activations, fp32 math;
  * no counterpart in the reference, whose model runner is out of this

@@ -144,3 +144,50 @@ def test_dequant_t_wide_tiles_bit_exact(device, K, N, with_zeros):
     kn = w4a16_dequant(q, sd, zd, group_size=128)
     nk = w4a16_dequant(q, sd, zd, group_size=128, transposed=True)
     assert torch.equal(nk.view(torch.int16), kn.t().contiguous().view(torch.int16))
+
+
+_ZP_SHAPES = [(504, 28672, 4096), (504, 6144, 4096), (504, 4096, 4096), (504, 4096, 14336),
+              (1, 256, 128), (37, 256, 512), (600, 768, 1024), (8, 1024, 256), (16, 256, 8448),
+              (300, 2304, 512)]
+
+
+@pytest.mark.parametrize("M,N,K", _ZP_SHAPES)
+@pytest.mark.parametrize("with_zeros", [True, False])
+def test_gemm_zp_vs_dequantised_fp32(device, M, N, K, with_zeros):
+    """cfa_w4a16_gemm_zp against an fp32 product of the bit-exact dequantised
+    weights (the kernel dequantises exactly as cfa_w4a16_dequant): differences
+    come from the fp32 accumulation order and the final bf16 rounding
+    (tolerance 1e-2 of the output scale + 2^-7 relative).  The verify step's
+    four target shapes (M = 504: QKV, O, gate/up, down), a single row, a
+    partial row tile, three row tiles (M = 600), column tiles that are not a
+    multiple of 8 (N = 768, 2304) and split-K shapes (the small ones leave
+    CUs idle without a split; K = 8448 splits into odd slice counts)."""
+    from cudaforge_amd.w4a16 import w4a16_gemm_zp
+
+    g = torch.Generator().manual_seed(M + N + K + with_zeros)
+    group = 128
+    a = torch.randn(M, K, generator=g).bfloat16().to(device)
+    w_int4 = torch.randint(0, 16, (K, N), generator=g, dtype=torch.int32)
+    scales = ((torch.rand(K // group, N, generator=g) * 0.5 + 0.5) / K ** 0.5).half().to(device)
+    zeros = torch.full((K // group, N), 7.5, dtype=torch.float16, device=device) if with_zeros else None
+    q = pack_int4_weights(w_int4).to(device)
+    c = w4a16_gemm_zp(a, q, scales, zeros, group_size=group)
+    w = w4a16_dequant(q, scales, zeros, group_size=group, dtype=torch.bfloat16).float()
+    ref = a.float() @ w
+    torch.cuda.synchronize()
+    err = (c.float() - ref).abs()
+    tol = 1e-2 * ref.abs().max() + 2.0 ** -7 * ref.abs()
+    assert (err <= tol).all(), err.max().item()
+    # reproducible: the same call gives the same bits
+    c2 = w4a16_gemm_zp(a, q, scales, zeros, group_size=group)
+    assert torch.equal(c, c2)
+
+
+def test_gemm_zp_rejects_bad_shapes(device):
+    from cudaforge_amd.w4a16 import w4a16_gemm_zp
+
+    a = torch.randn(4, 128, device=device).bfloat16()
+    q = torch.zeros(16, 100, dtype=torch.int32, device=device)  # N % 256 != 0
+    s = torch.ones(1, 100, dtype=torch.float16, device=device)
+    with pytest.raises(ValueError):
+        w4a16_gemm_zp(a, q, s)
