@@ -6,8 +6,9 @@
 // tests/unit/test_int4_dequant.py:6-15): word (k / 8, n) of B_quant [K/8, N]
 // holds nibble k % 8 at bits 4 (k % 8); fp16 group scales s and optional fp16
 // zero points z [K / group, N];  w = bf16((nibble - z) * s) formed in fp32,
-// exactly the value cfa_w4a16_dequant writes, so the result equals
-// dequantise-then-GEMM up to the order of the fp32 accumulation.
+// (one fp32 fma, then bf16), within one bf16 step of what
+// cfa_w4a16_dequant writes, so the result equals dequantise-then-GEMM up to
+// that and the order of the fp32 accumulation.
 //
 // Work-group: a 256 x 256 output tile, eight waves of 128 rows x 64 columns
 // (2 x 4), two per SIMD so that one's waits overlap the other's products.
@@ -44,22 +45,27 @@ constexpr int kNT = 64 * kWaves;
 constexpr int kBM = 256;             // rows per work-group
 constexpr int kBN = 256;             // columns per work-group
 constexpr int kWM = 128, kWN = 64;   // rows / columns per wave (2 x 4 waves)
-constexpr int kSK = 32;              // k per slice
+constexpr int kSK = 32;              // k per slice (one MFMA k-step)
 constexpr int kMT = kWM / 16;        // 16-row MFMA tiles per wave
 constexpr int kNTl = kWN / 16;       // 16-column MFMA tiles per wave
-constexpr int kStages = 3;                    // A ring (two slices ahead)
-constexpr int kWSlots = 8;                    // packed-word ring
-constexpr int kABytes = kBM * kSK * 2;        // 16 KiB
-constexpr int kQBytes = (kSK / 8) * kBN * 4;  // 4 KiB of packed words
+// A moves in stages of two slices (128-byte row segments, one cache line:
+// half the requests of one-slice stages), a ring of three
+constexpr int kAStages = 3;
+constexpr int kARow = 2 * kSK * 2;            // 128 bytes of a row per stage
+constexpr int kAStage = kBM * kARow;          // 32 KiB
+constexpr int kAXS = kAStage / 1024 / kWaves; // A transfers per wave per stage (4)
+constexpr int kAX = kAXS / 2;                 // ... per iteration (2)
+constexpr int kWSlots = 6;                    // packed-word ring
+constexpr int kQBytes = (kSK / 8) * kBN * 4;  // 4 KiB of packed words per slice
 constexpr int kSBytes = kBN * 2;              // one scale row (and one zero row)
 constexpr int kWSlot = kQBytes + 2 * kSBytes;
 constexpr int kBTile = kBN * kSK * 2;         // one dequantised slice [n][k], 16 KiB
-constexpr int kAX = kABytes / 1024 / kWaves;  // A transfers per wave per slice (2)
 constexpr int kDW = kBN * (kSK / 8) / kNT;    // packed words a thread dequantises per slice (2)
 static_assert(kBN == 4 * kWN && kBM == 2 * kWM, "2 x 4 waves");
 static_assert(kBN * 2 * 2 == 1024, "one transfer moves the scale and zero rows");
+static_assert(kAX == 2, "wait counts below");
 #ifndef CFA_W4_SGB
-#define CFA_W4_SGB 0
+#define CFA_W4_SGB 2
 #endif
 
 struct Args {
@@ -75,24 +81,30 @@ struct Args {
 };
 
 // Byte offset of the 16-byte chunk holding k = 8 c .. 8 c + 7 of a 64-byte
-// LDS row r.
-__device__ __forceinline__ int sw_off(int r, int c) { return r * (kSK * 2) + ((c ^ ((r >> 2) & 3)) << 4); }
+// LDS row r (dequantised tiles): 16 lanes reading rows r0 .. r0 + 15 (r0 % 16
+// == 0) at one chunk hit 16 distinct groups of 4 banks.
+__host__ __device__ constexpr int sw_off(int r, int c) { return r * (kSK * 2) + ((c ^ ((r >> 2) & 3)) << 4); }
+// The same for a 128-byte A row of a stage (chunks 0 .. 7).
+__host__ __device__ constexpr int sw_off_a(int r, int c) { return r * kARow + ((c ^ ((r >> 1) & 7)) << 4); }
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-// The 8 weights of one packed word as bf16 pairs (k, k + 1): bf16((nibble -
-// z) * s) with the difference and the product rounded in fp32, as
-// cfa_w4a16_dequant.  Even nibbles are the low halves of the bytes of
-// w & 0x0f0f0f0f and odd ones of (w >> 4) & 0x0f0f0f0f, so each converts
-// with one byte-to-float instruction; each pair packs with one conversion.
-__device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float z) {
+// The 8 weights of one packed word as bf16 pairs (k, k + 1):
+// bf16(fma(nibble, s, c)) with c = -z * s, i.e. (nibble - z) * s with one
+// fp32 rounding before the bf16 one (cfa_w4a16_dequant rounds the difference
+// and the product separately; the two agree to within one bf16 step, far
+// inside the GEMM's accumulation-order differences).  Even nibbles are the
+// low halves of the bytes of w & 0x0f0f0f0f and odd ones of
+// (w >> 4) & 0x0f0f0f0f, so each converts with one byte-to-float
+// instruction; each pair packs with one conversion.
+__device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float c) {
   const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
   uint32_t o[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const float f0 = ((float)((lo >> (8 * p)) & 0xffu) - z) * s;
-    const float f1 = ((float)((hi >> (8 * p)) & 0xffu) - z) * s;
+    const float f0 = __builtin_fmaf((float)((lo >> (8 * p)) & 0xffu), s, c);
+    const float f1 = __builtin_fmaf((float)((hi >> (8 * p)) & 0xffu), s, c);
     o[p] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{f0, f1}, bf16x2));
   }
   return make_uint4(o[0], o[1], o[2], o[3]);
@@ -105,7 +117,7 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 }
 
 __global__ __launch_bounds__(kNT, 1) void w4mm_kernel(Args a) {
-  __shared__ __align__(16) uint8_t aring[kStages * kABytes];
+  __shared__ __align__(16) uint8_t aring[kAStages * kAStage];
   __shared__ __align__(16) uint8_t wring[kWSlots * kWSlot];
   __shared__ __align__(16) uint8_t btile[2][kBTile];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -124,43 +136,56 @@ __global__ __launch_bounds__(kNT, 1) void w4mm_kernel(Args a) {
   const int g = lane >> 4, col = lane & 15;
   if (s0 >= s1) return;  // (never: the host sizes the splits) -- uniform per work-group
 
-  // Transfer sources (the slice's k offset is added per issue).  A transfer
-  // x of this wave covers stage rows 16 x .. 16 x + 15: lane i lands at row
-  // 16 x + i / 4, chunk position i % 4, and so fetches chunk
-  // (i % 4) ^ ((row / 4) % 4) of that row (rows past M re-read row M - 1).
-  const uint16_t *asrc[kAX];
+  // Slices are counted from s0 (relative slice r = absolute s0 + r), so the
+  // two slices of A stage t are r = 2t, 2t + 1 whatever s0 is.  Indices past
+  // the split are clamped to its last slice: a repeat transfer rewrites the
+  // same bytes in place, keeping every wave's transfer count per iteration
+  // fixed (the waits below count transfers).
+  const int nr = s1 - s0;
+  auto abs_slice = [&](int r) { return s0 + min(r, nr - 1); };
+
+  // A transfer x of a stage covers its rows 8 x .. 8 x + 7: lane i lands at
+  // row 8 x + i / 8, chunk position i % 8, and so fetches chunk
+  // (i % 8) ^ ((row / 2) % 8) of that row -- slice 2t + chunk / 4, k offset
+  // 8 (chunk % 4) (rows past M re-read row M - 1).  This wave's transfers
+  // of a stage are x = 4 wave .. 4 wave + 3, two per iteration.
+  // (element offsets into A, 32-bit: M * K < 2^31 is checked on the host;
+  // bit j of ahi: transfer j's chunk lies in the stage's second slice)
+  uint32_t aoffs[kAXS];
+  uint32_t ahi = 0;
 #pragma unroll
-  for (int j = 0; j < kAX; ++j) {
-    const int row = 16 * (wave * kAX + j) + (lane >> 2);
-    const int c = (lane & 3) ^ ((row >> 2) & 3);
-    asrc[j] = a.A + (long long)min(mb + row, a.M - 1) * a.K + 8 * c;
+  for (int j = 0; j < kAXS; ++j) {
+    const int row = 8 * (wave * kAXS + j) + (lane >> 3);
+    const int ch = (lane & 7) ^ ((row >> 1) & 7);
+    aoffs[j] = (uint32_t)min(mb + row, a.M - 1) * (uint32_t)a.K + 8u * (uint32_t)(ch & 3);
+    ahi |= (uint32_t)(ch >> 2) << j;
   }
+  // half h (0 or 1) of A stage t
+  auto issue_a = [&](int t, int h) {
+    uint8_t *dst = aring + (t % kAStages) * kAStage;
+    const uint32_t k0 = (uint32_t)abs_slice(2 * t) * kSK, k1 = (uint32_t)abs_slice(2 * t + 1) * kSK;
+#pragma unroll
+    for (int jj = 0; jj < kAX; ++jj) {
+      const int j = 2 * h + jj;
+      const uint32_t off = aoffs[j] + (((ahi >> j) & 1u) ? k1 : k0);
+      dma16(a.A + off, (CFA_LDS void *)(dst + 1024 * (wave * kAXS + j)));
+    }
+  };
   // the word-ring transfer of each wave: waves 0-3 packed row w of the slice
   // (lane: words 4 lane ..), wave 4 the scale row (lanes < 32) and the zero
   // row (lanes >= 32), 8 columns per lane; waves 5-7 repeat wave 0's (the
   // same bytes to the same place), so that every wave issues one word-ring
-  // transfer and then kAX A transfers per slice
+  // transfer and then kAX A transfers per iteration
   const int ww = wave >= 5 ? 0 : wave;
   const uint32_t *qsrc = a.q + (long long)(ww & 3) * a.N + n0 + 4 * lane;
   const __half *ssrc = (lane >= 32 && a.z ? a.z : a.s) + n0 + 8 * (lane & 31);
-  // Slices past the last are clamped to it: a repeat transfer rewrites the
-  // same bytes in place, keeping every wave's transfer count per iteration
-  // fixed (the waits below count transfers).
-  auto issue_w = [&](int u) {
-    u = min(u, s1 - 1);
-    uint8_t *dst = wring + (u % kWSlots) * kWSlot;
-    const int k0 = u * kSK;
+  auto issue_w = [&](int r) {
+    uint8_t *dst = wring + (((r % kWSlots) + kWSlots) % kWSlots) * kWSlot;
+    const int k0 = abs_slice(r) * kSK;
     if (ww < 4)
       dma16(qsrc + (long long)(k0 / 8) * a.N, (CFA_LDS void *)(dst + 1024 * ww));
     else
       dma16(ssrc + (long long)(k0 / a.group) * a.N, (CFA_LDS void *)(dst + kQBytes));
-  };
-  auto issue_a = [&](int u) {
-    u = min(u, s1 - 1);
-    uint8_t *dst = aring + (u % kStages) * kABytes;
-    const int k0 = u * kSK;
-#pragma unroll
-    for (int j = 0; j < kAX; ++j) dma16(asrc[j] + k0, (CFA_LDS void *)(dst + 1024 * (wave * kAX + j)));
   };
 
   // this thread's dequantisation share: column dc, packed rows kDW dp ..
@@ -169,14 +194,14 @@ __global__ __launch_bounds__(kNT, 1) void w4mm_kernel(Args a) {
   // without zero points the zero row holds the scales again, multiplied by 0
   // here (scales are finite), so that no branch splits the loop body
   const float zmul = a.z != nullptr ? 1.0f : 0.0f;
-  auto words_of = [&](int u, uint32_t (&w)[kDW], float &sf, float &zf) {
-    const uint8_t *st = wring + (u % kWSlots) * kWSlot;
+  auto words_of = [&](int r, uint32_t (&w)[kDW], float &sf, float &zf) {
+    const uint8_t *st = wring + (min(r, nr - 1) % kWSlots) * kWSlot;
 #pragma unroll
     for (int j = 0; j < kDW; ++j)
       w[j] = *reinterpret_cast<const uint32_t *>(st + ((kDW * dp + j) * kBN + dc) * 4);
     const __half *sc = reinterpret_cast<const __half *>(st + kQBytes);
     sf = __half2float(sc[dc]);
-    zf = __half2float(sc[kBN + dc]) * zmul;
+    zf = -(__half2float(sc[kBN + dc]) * zmul) * sf;  // the fma's addend -z * s
   };
 
   f32x4 acc[kMT][kNTl];
@@ -185,79 +210,91 @@ __global__ __launch_bounds__(kNT, 1) void w4mm_kernel(Args a) {
 #pragma unroll
     for (int j = 0; j < kNTl; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // operand read offsets of this lane
-  int aoff[kMT], boff[kNTl];
-#pragma unroll
-  for (int i = 0; i < kMT; ++i) aoff[i] = sw_off(wm * kWM + 16 * i + col, g);
-#pragma unroll
-  for (int j = 0; j < kNTl; ++j) boff[j] = sw_off(wn * kWN + 16 * j + col, g);
+  // operand read offsets of this lane (A: slice half 0 of a stage; half 1 is
+  // chunk + 4, i.e. the byte offset with bit 6 flipped)
+  // (rows 16 i apart share the swizzle, so tile i is tile 0 + 2048 i bytes;
+  // B tile j is tile 0 + 1024 j bytes)
+  const int aoff0 = sw_off_a(wm * kWM + col, g), boff0 = sw_off(wn * kWN + col, g);
+  static_assert(sw_off_a(16, 0) == 16 * kARow && sw_off(16, 0) == 16 * kSK * 2, "offsets");
 
-  // Issue order, per wave: W(s0), W(s0 + 1), then per iteration u = s0 - 2,
-  // s0 - 1, s0, ...: W(u + 4), A(u + 2).  At the top of iteration sl, A(sl)
-  // and everything issued before it (among them W(sl + 1)) have landed once
-  // at most the 1 + kAX transfers of iteration sl - 1 are in flight.
-  issue_w(s0);
-  issue_w(s0 + 1);
-  issue_w(s0 + 2);
-  issue_a(s0);
-  issue_w(s0 + 3);
-  issue_a(s0 + 1);
-  {
-    // W(s0) landed: 1 + 1 + kAX + 1 + kAX transfers after it
-    static_assert(kAX == 2, "wait count below");
-    wait_vm_lgkm0<3 + 2 * kAX>();
-    block_barrier();
+  // Pipeline, per iteration r: after the barrier, A of slice r + 1 and the
+  // dequantised tile of slice r + 1 are complete; this wave issues W(r + 5)
+  // and half r % 2 of A stage r / 2 + 2, reads slice r + 1's operands into
+  // its spare registers, dequantises slice r + 2 into the tile slice r used,
+  // and multiplies slice r from the registers read one iteration earlier --
+  // so the MFMAs never wait for LDS.  The prologue issues W(0), then for the
+  // virtual iterations r = -4 .. -1 the same pairs: W(1 .. 4), A stages 0
+  // and 1.  At the top of iteration r every transfer of iterations <= r - 2
+  // has landed once at most the 1 + kAX transfers of iteration r - 1 are in
+  // flight: among them the whole stage of slice r + 1 (its second half was
+  // issued at iteration 2 ((r + 1) / 2) - 3 <= r - 2) and W(r + 2) (issued
+  // at r - 3).  A stage t goes to slot t % 3 at iteration 2 t - 4, after the
+  // operands of stage t - 3 were read (iterations <= 2 t - 6).
+  issue_w(0);
+#pragma unroll
+  for (int r = -4; r < 0; ++r) {
+    issue_w(r + 5);
+    issue_a((r >> 1) + 2, r & 1);
+  }
+  auto dequant_into = [&](int r) {
     uint32_t w[kDW];
     float sf, zf;
-    words_of(s0, w, sf, zf);
+    words_of(r, w, sf, zf);
 #pragma unroll
     for (int j = 0; j < kDW; ++j)
-      *reinterpret_cast<uint4 *>(btile[s0 & 1] + sw_off(dc, kDW * dp + j)) = dequant_word(w[j], sf, zf);
-  }
-  for (int sl = s0; sl < s1; ++sl) {
-    // A(sl), W(sl + 1) and this wave's dequantised writes of slice sl are
-    // done (and, after the barrier, every wave's); slice sl - 1's A stage
-    // and dequantised tile, and the word slot of slice sl, are free
+      *reinterpret_cast<uint4 *>(btile[r & 1] + sw_off(dc, kDW * dp + j)) = dequant_word(w[j], sf, zf);
+  };
+  bf16x8 a0[kMT], b0[kNTl], a1[kMT], b1[kNTl];
+  auto read_ops = [&](int r, bf16x8 (&af)[kMT], bf16x8 (&bf)[kNTl]) {
+    r = min(r, nr - 1);
+    const uint8_t *as = aring + ((r >> 1) % kAStages) * kAStage + (aoff0 ^ ((r & 1) << 6));
+    const uint8_t *bs = btile[r & 1] + boff0;
+#pragma unroll
+    for (int j = 0; j < kNTl; ++j) bf[j] = *reinterpret_cast<const bf16x8 *>(bs + 1024 * j);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(as + 2048 * i);
+  };
+  wait_vm_lgkm0<kAX + 3 * (1 + kAX)>();  // W(0), W(1)
+  block_barrier();
+  dequant_into(0);
+  dequant_into(1);
+  wait_vm_lgkm0<2 * (1 + kAX)>();  // A stage 0; and the dequantised writes
+  block_barrier();
+  read_ops(0, a0, b0);
+
+  auto step = [&](int r, bf16x8 (&ac)[kMT], bf16x8 (&bc)[kNTl], bf16x8 (&an)[kMT],
+                  bf16x8 (&bn)[kNTl]) {
     wait_vm_lgkm0<1 + kAX>();
     block_barrier();
-    issue_w(sl + 4);
-    issue_a(sl + 2);
-    // The next slice's packed word and scales first (its dequantisation can
-    // start while this slice's operands are in flight), then this slice's
-    // operands, the products with the dequantisation's VALU work spread
-    // between them, and its LDS write.  Branch-free: past the last slice the
-    // word of the last one is dequantised again into the tile nobody reads.
-    uint32_t w[kDW];
-    float sf, zf;
-    words_of(min(sl + 1, s1 - 1), w, sf, zf);
-    const uint8_t *as = aring + (sl % kStages) * kABytes;
-    const uint8_t *bs = btile[sl & 1];
-    bf16x8 bfr[kNTl], afr[kMT];
-#pragma unroll
-    for (int j = 0; j < kNTl; ++j) bfr[j] = *reinterpret_cast<const bf16x8 *>(bs + boff[j]);
-#pragma unroll
-    for (int i = 0; i < kMT; ++i) afr[i] = *reinterpret_cast<const bf16x8 *>(as + aoff[i]);
-    uint4 dq[kDW];
-#pragma unroll
-    for (int j = 0; j < kDW; ++j) dq[j] = dequant_word(w[j], sf, zf);
+    issue_w(r + 5);
+    issue_a((r >> 1) + 2, r & 1);
+    read_ops(r + 1, an, bn);
+    dequant_into(r + 2);
 #pragma unroll
     for (int i = 0; i < kMT; ++i)
 #pragma unroll
       for (int j = 0; j < kNTl; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[i], bfr[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int j = 0; j < kDW; ++j)
-      *reinterpret_cast<uint4 *>(btile[(sl + 1) & 1] + sw_off(dc, kDW * dp + j)) = dq[j];
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[i], bc[j], acc[i][j], 0, 0, 0);
 #if CFA_W4_SGB
-    __builtin_amdgcn_sched_group_barrier(0x0100, kNTl + kMT + 3, 0);
+    // LDS reads first (the next slice's operands, the words), then the
+    // dequantisation's VALU work spread between the MFMAs, so that the two
+    // waves of a SIMD (which reach this point together) overlap VALU with
+    // products instead of taking turns; its LDS writes last
+    __builtin_amdgcn_sched_group_barrier(0x0100, kNTl + kMT + 2 * kDW + 2, 0);
 #pragma unroll
     for (int k = 0; k < kMT * kNTl; ++k) {
       __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x0002, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x0002, CFA_W4_SGB, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x0200, kDW, 0);
 #endif
+  };
+  int r = 0;
+  for (; r + 1 < nr; r += 2) {
+    step(r, a0, b0, a1, b1);
+    step(r + 1, a1, b1, a0, b0);
   }
+  if (r < nr) step(r, a0, b0, a1, b1);
   // drain: the last iterations' repeat transfers must land before exit
   wait_vm_lgkm0<0>();
 
@@ -346,6 +383,7 @@ extern "C" int cfa_w4a16_gemm_zp(const void *a, const uint32_t *b_quant, const v
   if ((((uintptr_t)a | (uintptr_t)c | (uintptr_t)b_quant | (uintptr_t)scales | (uintptr_t)zeros) & 15) != 0)
     return fail_arg("a, b_quant, scales, zeros and c must be 16-byte aligned");
   int spp = 0;
+  if ((long long)M * K >= (1LL << 31)) return fail_arg("M * K must be below 2^31");
   const int splits = choose_splits(M, N, K, device_cu_count(), &spp);
   const size_t need = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
   if (need && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15) != 0))
