@@ -364,6 +364,60 @@ def tree_accept_commit_leg(dev, reps=10):
             "commit_gbs": round(alg_commit / t_com / 1e9, 1) if moved else None}
 
 
+def w4a16_gemm_leg(dev, reps=20):
+    """The 8B target's four W4A16 projections at the verify step's M = B * 63
+    = 504 rows (QKV 4096 -> 6144, O 4096 -> 4096, gate/up 4096 -> 28672,
+    down 14336 -> 4096; group 128, zero point 7.5): cfa_w4a16_gemm_zp beside
+    dequantise-to-[N, K] + hipBLASLt (the path it replaces), HIP-event time
+    per call on the launch stream."""
+    import torch
+    from cudaforge_amd.w4a16 import w4a16_dequant, w4a16_gemm_zp
+
+    M = 504
+    shapes = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 28672),
+              "down": (14336, 4096)}
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    ws = torch.empty(80 << 20, dtype=torch.uint8, device=dev)
+    out = {}
+    for name, (K, N) in shapes.items():
+        a = torch.randn(M, K, device=dev, generator=g).bfloat16()
+        q = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), dtype=torch.int32, device=dev,
+                          generator=g)
+        sc = ((torch.rand(K // 128, N, device=dev, generator=g) * 0.5 + 0.5) / K ** 0.5).half()
+        z = torch.full_like(sc, 7.5)
+        c = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        wt = torch.empty(N, K, dtype=torch.bfloat16, device=dev)
+
+        def fused():
+            w4a16_gemm_zp(a, q, sc, z, out=c, workspace=ws)
+
+        def base():
+            w4a16_dequant(q, sc, z, dtype=torch.bfloat16, out=wt, transposed=True)
+            torch.matmul(a, wt.t(), out=c)
+
+        row = {}
+        for label, fn in (("fused_us", fused), ("dequant_hipblaslt_us", base)):
+            for _ in range(3):
+                fn()
+            stream = torch.cuda.current_stream(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(reps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            row[label] = round(e0.elapsed_time(e1) / reps * 1e3, 1)
+        flops = 2.0 * M * N * K
+        row["fused_tflops"] = round(flops / (row["fused_us"] * 1e-6) / 1e12, 1)
+        row["fused_mfma_frac"] = round(flops / (row["fused_us"] * 1e-6) / MFMA_BF16_PEAK, 4)
+        out[name] = row
+        del a, q, sc, z, c, wt
+    out["config"] = "M=504 (B=8 x 63 nodes), bf16 activations, INT4 group 128, zero point 7.5"
+    return out
+
+
 def verify_step_8b_leg(dev, steps=6, warmup=2):
     """one speculative verify step at Llama-3-8B shape --
     random-init W4A16 (group 128) target (32L, d4096, GQA 32/8, FFN 14336,
@@ -414,7 +468,8 @@ def main() -> int:
     ap.add_argument("--no-tree", action="store_true",
                     help="skip the extra legs (tree attention, tree accept/commit, 8B verify step)")
     ap.add_argument("--legs",
-                    default="chain_step_c1,tree_attention,tree_accept_commit,verify_step_8b",
+                    default="chain_step_c1,tree_attention,tree_accept_commit,w4a16_gemm,"
+                            "verify_step_8b",
                     help="comma-separated extra legs to run")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (reference for HBM byte counters)")
@@ -496,7 +551,7 @@ def main() -> int:
     # the whole step on the workload's algorithmic bytes (every logit once)
     step_gbs = ALG_BYTES / (ms_per_step * 1e-3) / 1e9
     head_t = traffic_from_profile("cfa::chain::stats_kernel<256, 4> (head)")
-    tail_t = traffic_from_profile("cfa::chain::stats_kernel<256, 4> (tail)")
+    tail_t = traffic_from_profile("cfa::chain::stats_tail_kernel<256>")
 
     line = {
         "metric": METRIC,
@@ -529,6 +584,7 @@ def main() -> int:
     }
     legs = [] if args.no_tree else [x for x in args.legs.split(",") if x]
     known = {"chain_step_c1": chain_step_c1_leg, "tree_attention": tree_attention_leg,
+             "w4a16_gemm": w4a16_gemm_leg,
              "tree_accept_commit": tree_accept_commit_leg, "verify_step_8b": verify_step_8b_leg}
     if legs:
         del sets
