@@ -396,8 +396,24 @@ def w4a16_gemm_leg(dev, reps=20):
             w4a16_dequant(q, sc, z, dtype=torch.bfloat16, out=wt, transposed=True)
             torch.matmul(a, wt.t(), out=c)
 
+        legs = [("fused_us", fused), ("dequant_hipblaslt_us", base)]
+        if name == "gate_up":
+            # the target's FFN input: silu(gate) * up, by the SiLU-gated
+            # epilogue or by the plain product followed by cfa_silu_mul
+            from cudaforge_amd.spec_step import silu_mul
+            act = torch.empty(M, N // 2, dtype=torch.bfloat16, device=dev)
+
+            def fused_silu():
+                w4a16_gemm_zp(a, q, sc, z, out=act, workspace=ws, silu=True)
+
+            def fused_then_silu_mul():
+                w4a16_gemm_zp(a, q, sc, z, out=c, workspace=ws)
+                silu_mul(c)
+
+            legs += [("fused_silu_epilogue_us", fused_silu),
+                     ("fused_then_silu_mul_us", fused_then_silu_mul)]
         row = {}
-        for label, fn in (("fused_us", fused), ("dequant_hipblaslt_us", base)):
+        for label, fn in legs:
             for _ in range(3):
                 fn()
             stream = torch.cuda.current_stream(dev)

@@ -6,6 +6,7 @@
 #include <hip/hip_bf16.h>
 
 #include "abi_internal.hpp"
+#include "silu.hpp"
 
 namespace cfa {
 namespace ops {
@@ -175,16 +176,13 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
 }
 
 // out[m, f] = bf16(bf16(silu(g)) * u) for gu [M, 2F] = [g | u] (the rounding
-// of silu(g) * u in two bf16 PyTorch ops).
+// of silu(g) * u in two bf16 PyTorch ops; silu_gate).
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *gu, uint16_t *out, int M,
                                                        int F) {
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   if (t >= (long long)M * F) return;
   const long long m = t / F, f = t % F;
-  const float g = bf2f(gu[m * 2 * F + f]);
-  const float u = bf2f(gu[m * 2 * F + F + f]);
-  const float s = bf2f(f2bf(g / (1.0f + expf(-g))));
-  out[t] = f2bf(s * u);
+  out[t] = silu_gate(bf2f(gu[m * 2 * F + f]), bf2f(gu[m * 2 * F + F + f]));
 }
 
 // The same, eight features per thread with 16-byte loads and stores
@@ -201,15 +199,7 @@ __global__ __launch_bounds__(256) void silu_mul8_kernel(const uint16_t *gu, uint
   uint32_t ow[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    uint32_t r = 0;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float g = bf2f((uint16_t)(gw[j] >> (16 * h)));
-      const float u = bf2f((uint16_t)(uw[j] >> (16 * h)));
-      const float s = bf2f(f2bf(g / (1.0f + expf(-g))));
-      r |= (uint32_t)f2bf(s * u) << (16 * h);
-    }
-    ow[j] = r;
+    ow[j] = silu_gate2(silu_lo(gw[j]), silu_lo(uw[j]), silu_hi(gw[j]), silu_hi(uw[j]));
   }
   *reinterpret_cast<uint4 *>(out + m * F + f) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
 }

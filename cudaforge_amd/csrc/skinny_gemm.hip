@@ -27,6 +27,7 @@
 
 #include "abi_internal.hpp"
 #include "lds_dma.hpp"
+#include "silu.hpp"
 
 namespace cfa {
 namespace sg {
@@ -69,15 +70,6 @@ template <int N>
 __device__ __forceinline__ void wait_vm_lgkm0() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | (((N >> 4) & 3) << 14));
-}
-
-// The SiLU-gated epilogue rounds exactly as a bf16 GEMM followed by
-// cfa_silu_mul: g and u to bf16, then bf16(bf16(silu(g)) * u).
-__device__ __forceinline__ float bf16_round(float f) { return (float)(__bf16)f; }
-__device__ __forceinline__ uint16_t f2bf_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
-  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
 template <int MT, bool SILU>
@@ -224,9 +216,7 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(Args a) {
         for (int e = 0; e < 4; ++e) {
           const int row = 16 * i + 4 * g + e;
           if (row >= a.M) continue;
-          const float gv = bf16_round(v[i][e]), uv = bf16_round(up[e]);
-          const float sv = __uint_as_float((uint32_t)f2bf_rne(gv / (1.0f + expf(-gv))) << 16);
-          a.C[(long long)row * F + fcol] = f2bf_rne(sv * uv);
+          a.C[(long long)row * F + fcol] = silu_gate(v[i][e], up[e]);
         }
       }
     }

@@ -33,6 +33,7 @@
 
 #include "abi_internal.hpp"
 #include "lds_dma.hpp"
+#include "silu.hpp"
 
 namespace cfa {
 namespace w4mm {
@@ -78,6 +79,7 @@ struct Args {
   int M, N, K, group;
   int slices_per_split;
   int mtiles;  // row tiles
+  int silu;    // C [M, N / 2] = silu(gate) * up, W's columns in the interleaved gate/up layout
 };
 
 // Byte offset of the 16-byte chunk holding k = 8 c .. 8 c + 7 of a 64-byte
@@ -300,7 +302,24 @@ __global__ __launch_bounds__(kNT, 1) void w4mm_kernel(Args a) {
 
   // acc[i][j][e]: row mb + 128 wm + 16 i + 4 g + e, column n0 + 64 wn + 16 j + lane % 16
   const int r0 = mb + wm * kWM + 4 * g, c0 = n0 + wn * kWN + col;
-  if (gridDim.z == 1) {
+  if (gridDim.z == 1 && a.silu) {
+    // this wave's 64 columns are gate features f .. f + 31 (tiles j = 0, 1)
+    // and then their up columns (j = 2, 3): a lane holds both halves of its
+    // features
+    const int F = a.N / 2, f0 = (n0 + wn * kWN) / 2 + col;
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = r0 + 16 * i + e;
+        if (row >= a.M) continue;
+        uint16_t *cr = a.C + (long long)row * F + f0;
+        static_assert(kNTl == 4, "two gate and two up tiles per wave");
+        const uint32_t p = silu_gate2(acc[i][0][e], acc[i][2][e], acc[i][1][e], acc[i][3][e]);
+        cr[0] = (uint16_t)p;
+        cr[16] = (uint16_t)(p >> 16);
+      }
+  } else if (gridDim.z == 1) {
 #pragma unroll
     for (int i = 0; i < kMT; ++i)
 #pragma unroll
@@ -347,6 +366,36 @@ __global__ __launch_bounds__(256) void w4mm_reduce_kernel(const float *part, uin
   *reinterpret_cast<uint2 *>(C + i) = o;
 }
 
+// The same for the SiLU-gated output: four features f .. f + 3 per thread
+// (gate columns 64 (f / 32) + f % 32 .., up columns 32 further on).
+__global__ __launch_bounds__(256) void w4mm_reduce_silu_kernel(const float *part, uint16_t *C, int M,
+                                                               int N, int splits) {
+  const int F = N / 2;
+  const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= (long long)M * F) return;
+  const long long m = i / F;
+  const int f = (int)(i % F);
+  const long long gi = m * N + 64 * (f / 32) + f % 32, MN = (long long)M * N;
+  float4 gs = *reinterpret_cast<const float4 *>(part + gi);
+  float4 us = *reinterpret_cast<const float4 *>(part + gi + 32);
+  for (int s = 1; s < splits; ++s) {
+    const float4 g = *reinterpret_cast<const float4 *>(part + s * MN + gi);
+    const float4 u = *reinterpret_cast<const float4 *>(part + s * MN + gi + 32);
+    gs.x += g.x;
+    gs.y += g.y;
+    gs.z += g.z;
+    gs.w += g.w;
+    us.x += u.x;
+    us.y += u.y;
+    us.z += u.z;
+    us.w += u.w;
+  }
+  uint2 o;
+  o.x = silu_gate2(gs.x, us.x, gs.y, us.y);
+  o.y = silu_gate2(gs.z, us.z, gs.w, us.w);
+  *reinterpret_cast<uint2 *>(C + i) = o;
+}
+
 // Splits of K: enough work-groups for every CU, each split at least 8
 // slices; *spp slices per split, and no split empty.
 int choose_splits(int M, int N, int K, int cus, int *spp) {
@@ -368,9 +417,9 @@ extern "C" size_t cfa_w4a16_gemm_zp_workspace_size(int M, int N, int K) {
   return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
 }
 
-extern "C" int cfa_w4a16_gemm_zp(const void *a, const uint32_t *b_quant, const void *scales,
-                                 const void *zeros, int M, int N, int K, int group_size, void *c,
-                                 void *workspace, size_t workspace_bytes, void *stream) {
+static int w4mm_launch(const void *a, const uint32_t *b_quant, const void *scales, const void *zeros,
+                       int M, int N, int K, int group_size, void *c, void *workspace,
+                       size_t workspace_bytes, void *stream, bool silu) {
   using namespace cfa::abi;
   using namespace cfa::w4mm;
   clear_error();
@@ -400,18 +449,39 @@ extern "C" int cfa_w4a16_gemm_zp(const void *a, const uint32_t *b_quant, const v
   g.K = K;
   g.group = group_size;
   g.slices_per_split = spp;
+  g.silu = silu ? 1 : 0;
   const long long mt = (M + kBM - 1) / kBM;
   if (mt > 65535) return fail_arg("M too large");
   hipStream_t st = (hipStream_t)stream;
   const long long blocks = mt * ((N / kBN + 7) / 8) * 8;  // column tiles padded to groups of 8
   if (blocks > 0x7fffffffLL) return fail_arg("problem too large");
   g.mtiles = (int)mt;
-  CFA_LAUNCH("w4a16_gemm_zp", w4mm_kernel, dim3((unsigned)blocks, 1, (unsigned)splits),
-             dim3(kNT), 0, st, g);
-  if (splits > 1) {
+  CFA_LAUNCH(silu ? "w4a16_gemm_zp_silu" : "w4a16_gemm_zp", w4mm_kernel,
+             dim3((unsigned)blocks, 1, (unsigned)splits), dim3(kNT), 0, st, g);
+  if (splits > 1 && silu) {
+    const long long MF = (long long)M * (N / 2);  // N % 256 == 0: four features per thread
+    CFA_LAUNCH("w4a16_gemm_zp_reduce", w4mm_reduce_silu_kernel,
+               dim3((unsigned)((MF / 4 + 255) / 256)), dim3(256), 0, st, (const float *)workspace,
+               (uint16_t *)c, M, N, splits);
+  } else if (splits > 1) {
     const long long MN = (long long)M * N;  // N % 128 == 0: four columns per thread
     CFA_LAUNCH("w4a16_gemm_zp_reduce", w4mm_reduce_kernel, dim3((unsigned)((MN / 4 + 255) / 256)),
                dim3(256), 0, st, (const float *)workspace, (uint16_t *)c, MN, splits);
   }
   return CFA_OK;
+}
+
+extern "C" int cfa_w4a16_gemm_zp(const void *a, const uint32_t *b_quant, const void *scales,
+                                 const void *zeros, int M, int N, int K, int group_size, void *c,
+                                 void *workspace, size_t workspace_bytes, void *stream) {
+  return w4mm_launch(a, b_quant, scales, zeros, M, N, K, group_size, c, workspace, workspace_bytes,
+                     stream, false);
+}
+
+extern "C" int cfa_w4a16_gemm_zp_silu(const void *a, const uint32_t *b_quant, const void *scales,
+                                      const void *zeros, int M, int N, int K, int group_size,
+                                      void *c, void *workspace, size_t workspace_bytes,
+                                      void *stream) {
+  return w4mm_launch(a, b_quant, scales, zeros, M, N, K, group_size, c, workspace, workspace_bytes,
+                     stream, true);
 }

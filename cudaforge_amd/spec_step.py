@@ -221,6 +221,9 @@ class TargetModel:
                 wqkv=W4A16Linear(d, qkv_n, device, g, group),
                 wo=W4A16Linear(s.n_heads * hd, d, device, g, group),
                 ffn_norm=torch.ones(d, dtype=torch.bfloat16, device=device),
+                # gate/up in the interleaved layout of the SiLU-gated
+                # epilogue (interleave_gate_up; random weights, so drawn in
+                # that layout directly)
                 wgu=W4A16Linear(d, 2 * s.ffn, device, g, group),
                 wdown=W4A16Linear(s.ffn, d, device, g, group)))
         self.norm = torch.ones(d, dtype=torch.bfloat16, device=device)
@@ -259,7 +262,7 @@ class TargetModel:
                                layer=li, max_keys=max_keys, workspace=self.attn_ws)
             delta = L["wo"](o.reshape(M, Hq * hd), self.scratch)
             rmsnorm_(h, delta, L["ffn_norm"], s.eps, x)
-            a = silu_mul(L["wgu"](x, self.scratch))
+            a = L["wgu"].silu_gated(x, self.scratch)
             delta = L["wdown"](a, self.scratch)
         rmsnorm_(h, delta, self.norm, s.eps, x)
         return (x @ self.lm_head).float().view(B, N, s.vocab)

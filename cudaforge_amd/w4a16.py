@@ -109,10 +109,15 @@ def gemm_zp_ok(a: torch.Tensor, b_quant: torch.Tensor, group_size: int) -> bool:
 def w4a16_gemm_zp(a: torch.Tensor, b_quant: torch.Tensor, scales: torch.Tensor,
                   zeros: Optional[torch.Tensor] = None, *, group_size: int = 128,
                   out: Optional[torch.Tensor] = None,
-                  workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  workspace: Optional[torch.Tensor] = None, silu: bool = False) -> torch.Tensor:
     """Fused a [M, K] bf16 x W -> [M, N] bf16 with W = bf16((nibble - z) * s),
     the weights cfa_w4a16_dequant writes (cfa_w4a16_gemm_zp); `workspace`
-    (uint8, cfa_w4a16_gemm_zp_workspace_size bytes) holds split-K partials."""
+    (uint8, cfa_w4a16_gemm_zp_workspace_size bytes) holds split-K partials.
+    silu=True: W's columns are in the interleaved gate/up layout (64-column
+    tile t = gate features 32t .. 32t + 31, then their up columns) and the
+    result is silu(gate) * up, [M, N / 2] (cfa_w4a16_gemm_zp_silu),
+    bit-identical to the plain product de-interleaved and passed through
+    cfa_silu_mul."""
     if a.dtype != torch.bfloat16 or a.dim() != 2:
         raise ValueError("a must be a bf16 [M, K] tensor")
     M, K = a.shape
@@ -127,16 +132,20 @@ def w4a16_gemm_zp(a: torch.Tensor, b_quant: torch.Tensor, scales: torch.Tensor,
     need = lib.cfa_w4a16_gemm_zp_workspace_size(M, N, K)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=a.device)
+    Nout = N // 2 if silu else N
     if out is None:
-        out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+        out = torch.empty(M, Nout, dtype=torch.bfloat16, device=a.device)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (M, Nout) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous bf16 [{M}, {Nout}] tensor")
     sc = scales.contiguous()
     zz = zeros.contiguous() if zeros is not None else None
+    name = "cfa_w4a16_gemm_zp_silu" if silu else "cfa_w4a16_gemm_zp"
     with torch.cuda.device(a.device):
-        rc = lib.cfa_w4a16_gemm_zp(a.data_ptr(), b_quant.data_ptr(), sc.data_ptr(),
-                                   zz.data_ptr() if zz is not None else None, M, N, K,
-                                   group_size, out.data_ptr(), workspace.data_ptr(),
-                                   workspace.numel(), _stream_ptr(a.device))
-    _lib.check(rc, "cfa_w4a16_gemm_zp")
+        rc = getattr(lib, name)(a.data_ptr(), b_quant.data_ptr(), sc.data_ptr(),
+                                zz.data_ptr() if zz is not None else None, M, N, K,
+                                group_size, out.data_ptr(), workspace.data_ptr(),
+                                workspace.numel(), _stream_ptr(a.device))
+    _lib.check(rc, name)
     return out
 
 
@@ -184,6 +193,17 @@ class W4A16Linear:
         w4a16_dequant(self.qweight, self.scales, self.zeros, group_size=self.group,
                       dtype=x.dtype, out=wt, transposed=True)
         return x @ wt.t()
+
+    def silu_gated(self, x: torch.Tensor, scratch: torch.Tensor) -> torch.Tensor:
+        """silu(x @ W_gate) * (x @ W_up) [M, N / 2] for W in the interleaved
+        gate/up layout (64-column tile t = gate features 32t .. 32t + 31,
+        then their up columns): the fused epilogue where cfa_w4a16_gemm_zp
+        takes the shape, else the product de-interleaved and cfa_silu_mul."""
+        if self.fused_zp and gemm_zp_ok(x, self.qweight, self.group):
+            return w4a16_gemm_zp(x, self.qweight, self.scales, self.zeros, group_size=self.group,
+                                 workspace=scratch.view(torch.uint8), silu=True)
+        from .spec_step import deinterleave_gate_up, silu_mul
+        return silu_mul(deinterleave_gate_up(self(x, scratch)).contiguous())
 
 
 def int4_gemm_dequant(a: torch.Tensor, b_quant: torch.Tensor, scales: torch.Tensor,

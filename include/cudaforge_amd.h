@@ -322,6 +322,17 @@ size_t cfa_w4a16_gemm_zp_workspace_size(int M, int N, int K);
 int cfa_w4a16_gemm_zp(const void *a, const uint32_t *b_quant, const void *scales,
                       const void *zeros, int M, int N, int K, int group_size, void *c,
                       void *workspace, size_t workspace_bytes, void *stream);
+/* The same product with a SiLU-gated epilogue (the gate/up projection of a
+ * Llama FFN; no counterpart in the reference, whose model runner is out of
+ * this library's scope): the N columns of W hold, in each 64-column tile t,
+ * gate columns for features 32t .. 32t + 31 followed by the up columns of the
+ * same features; out [M, N / 2] = bf16(bf16(silu(g)) * u) with g and u the
+ * product's columns rounded to bf16, bit-identical to cfa_w4a16_gemm_zp
+ * followed by cfa_silu_mul on the de-interleaved [g | u] columns.  Shape
+ * rules and workspace as cfa_w4a16_gemm_zp. */
+int cfa_w4a16_gemm_zp_silu(const void *a, const uint32_t *b_quant, const void *scales,
+                           const void *zeros, int M, int N, int K, int group_size, void *out,
+                           void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
  * Fused layers of the model-scale verify step (bf16 activations, fp32 math;

@@ -73,7 +73,7 @@ def _ref_forward(tm: TargetModel, tokens, positions, kv, tables, base, N):
                 o[b, :, hh] = torch.softmax(sc, -1) @ vv[:, hh // G]
         h = h + o.reshape(B * N, Hq * hd) @ W(L["wo"])
         x = rms(h, L["ffn_norm"])
-        gu = x @ W(L["wgu"])
+        gu = deinterleave_gate_up(x @ W(L["wgu"]))           # stored gate/up-interleaved
         h = h + (torch.nn.functional.silu(gu[:, : s.ffn]) * gu[:, s.ffn:]) @ W(L["wdown"])
     h = rms(h, tm.norm)
     return (h @ tm.lm_head.float()).view(B, N, s.vocab)

@@ -183,6 +183,30 @@ def test_gemm_zp_vs_dequantised_fp32(device, M, N, K, with_zeros):
     assert torch.equal(c, c2)
 
 
+@pytest.mark.parametrize("M,N,K", [(504, 28672, 4096), (1, 512, 128), (37, 256, 512),
+                                   (600, 768, 1024), (16, 512, 8448)])
+def test_gemm_zp_silu_bit_exact(device, M, N, K):
+    """cfa_w4a16_gemm_zp_silu equals cfa_w4a16_gemm_zp on the same
+    interleaved gate/up weights, de-interleaved and passed through
+    cfa_silu_mul, bit for bit: the target's gate/up shape (one K split), and
+    split-K shapes whose partials the SiLU-gated reduce sums (M = 1, 16, 37)."""
+    from cudaforge_amd.spec_step import deinterleave_gate_up, silu_mul
+    from cudaforge_amd.w4a16 import w4a16_gemm_zp
+
+    g = torch.Generator().manual_seed(7 * M + N + K)
+    group = 128
+    a = torch.randn(M, K, generator=g).bfloat16().to(device)
+    q = pack_int4_weights(torch.randint(0, 16, (K, N), generator=g, dtype=torch.int32)).to(device)
+    scales = ((torch.rand(K // group, N, generator=g) * 0.5 + 0.5) / K ** 0.5).half().to(device)
+    zeros = torch.full((K // group, N), 7.5, dtype=torch.float16, device=device)
+    fused = w4a16_gemm_zp(a, q, scales, zeros, group_size=group, silu=True)
+    plain = silu_mul(deinterleave_gate_up(w4a16_gemm_zp(a, q, scales, zeros, group_size=group))
+                     .contiguous())
+    torch.cuda.synchronize()
+    assert fused.shape == (M, N // 2)
+    assert torch.equal(fused, plain)
+
+
 def test_gemm_zp_rejects_bad_shapes(device):
     from cudaforge_amd.w4a16 import w4a16_gemm_zp
 
