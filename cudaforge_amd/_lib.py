@@ -140,7 +140,10 @@ SIGNATURES: dict[str, tuple] = {
     "cfa_w4a16_gemm_zp_workspace_size": (_sz, [_i, _i, _i]),
     "cfa_w4a16_gemm_zp": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _p, _sz, _p]),
     "cfa_w4a16_gemm_zp_silu": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _p, _sz, _p]),
+    "cfa_w4a16_gemm_zp_splits": (_i, [_i, _i, _i]),
+    "cfa_w4a16_gemm_zp_partials": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _sz, _p]),
     "cfa_rmsnorm": (_i, [_p, _p, _p, _p, _i, _i, _f, _p]),
+    "cfa_rmsnorm_partials": (_i, [_p, _p, _i, _p, _p, _i, _i, _f, _p]),
     "cfa_rope_kv_paged": (
         _i, [_p, _p, _i, _i, _i, _i, _i, _f, _p, _p, _p, _i, _i, _i, _p, _i, _p, _p]),
     "cfa_rope_kv_strided": (

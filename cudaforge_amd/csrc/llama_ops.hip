@@ -25,19 +25,46 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 // ---------------------------------------------------------------------------
 constexpr int kNormNT = 256;
 
+// With `part` (and delta NULL) the delta is bf16 of the sum of `splits` fp32
+// slabs part[s][M][d] taken in slab order -- what the W4A16 GEMM's split-K
+// reduce writes -- so that the GEMM's partials need no separate reduce.
 __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(uint16_t *h, const uint16_t *delta,
                                                           const uint16_t *w, uint16_t *out, int d,
-                                                          float eps) {
+                                                          float eps, const float *part, int splits,
+                                                          long long slab) {
   const long long row = blockIdx.x;
   uint16_t *hr = h + row * d;
   const uint16_t *dr = delta ? delta + row * d : nullptr;
+  const float *pr = part ? part + row * d : nullptr;
   uint16_t *orow = out + row * d;
   const int nvec = d / 8;
   float ss = 0.0f;
   for (int v = threadIdx.x; v < nvec; v += kNormNT) {
     uint4 x = reinterpret_cast<const uint4 *>(hr)[v];
-    if (dr) {
-      const uint4 y = reinterpret_cast<const uint4 *>(dr)[v];
+    if (dr || pr) {
+      uint4 y;
+      if (pr) {
+        float4 lo = reinterpret_cast<const float4 *>(pr)[2 * v];
+        float4 hi = reinterpret_cast<const float4 *>(pr)[2 * v + 1];
+        for (int sp = 1; sp < splits; ++sp) {
+          const float4 l2 = reinterpret_cast<const float4 *>(pr + sp * slab)[2 * v];
+          const float4 h2 = reinterpret_cast<const float4 *>(pr + sp * slab)[2 * v + 1];
+          lo.x += l2.x;
+          lo.y += l2.y;
+          lo.z += l2.z;
+          lo.w += l2.w;
+          hi.x += h2.x;
+          hi.y += h2.y;
+          hi.z += h2.z;
+          hi.w += h2.w;
+        }
+        y.x = (uint32_t)f2bf(lo.x) | ((uint32_t)f2bf(lo.y) << 16);
+        y.y = (uint32_t)f2bf(lo.z) | ((uint32_t)f2bf(lo.w) << 16);
+        y.z = (uint32_t)f2bf(hi.x) | ((uint32_t)f2bf(hi.y) << 16);
+        y.w = (uint32_t)f2bf(hi.z) | ((uint32_t)f2bf(hi.w) << 16);
+      } else {
+        y = reinterpret_cast<const uint4 *>(dr)[v];
+      }
       uint32_t *xs = reinterpret_cast<uint32_t *>(&x);
       const uint32_t *ys = reinterpret_cast<const uint32_t *>(&y);
 #pragma unroll
@@ -219,7 +246,22 @@ extern "C" int cfa_rmsnorm(void *h, const void *delta, const void *weight, void 
     return fail_arg("rows must be 16-byte aligned");
   CFA_LAUNCH("rmsnorm", rmsnorm_kernel, dim3(M), dim3(kNormNT), 0, (hipStream_t)stream,
              (uint16_t *)h, (const uint16_t *)delta, (const uint16_t *)weight, (uint16_t *)out, d,
-             eps);
+             eps, (const float *)nullptr, 0, 0LL);
+  return CFA_OK;
+}
+
+extern "C" int cfa_rmsnorm_partials(void *h, const float *part, int splits, const void *weight,
+                                    void *out, int M, int d, float eps, void *stream) {
+  using namespace cfa::abi;
+  clear_error();
+  if (M <= 0 || d <= 0 || d % 8 != 0) return fail_arg("M > 0 and d a positive multiple of 8");
+  if (splits <= 0) return fail_arg("splits must be positive");
+  if (!h || !part || !weight || !out) return fail_arg("null pointer");
+  if ((((uintptr_t)h | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)part) & 15) != 0)
+    return fail_arg("rows must be 16-byte aligned");
+  CFA_LAUNCH("rmsnorm", rmsnorm_kernel, dim3(M), dim3(kNormNT), 0, (hipStream_t)stream,
+             (uint16_t *)h, (const uint16_t *)nullptr, (const uint16_t *)weight, (uint16_t *)out,
+             d, eps, part, splits, (long long)M * d);
   return CFA_OK;
 }
 

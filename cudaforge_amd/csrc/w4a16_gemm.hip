@@ -80,12 +80,19 @@ struct Args {
   int slices_per_split;
   int mtiles;  // row tiles
   int silu;    // C [M, N / 2] = silu(gate) * up, W's columns in the interleaved gate/up layout
+  int to_part; // fp32 partials even with one split (the caller sums them)
 };
 
 // Byte offset of the 16-byte chunk holding k = 8 c .. 8 c + 7 of a 64-byte
-// LDS row r (dequantised tiles): 16 lanes reading rows r0 .. r0 + 15 (r0 % 16
-// == 0) at one chunk hit 16 distinct groups of 4 banks.
-__host__ __device__ constexpr int sw_off(int r, int c) { return r * (kSK * 2) + ((c ^ ((r >> 2) & 3)) << 4); }
+// LDS row r (dequantised tiles): 16 lanes at rows r0 .. r0 + 15 (r0 % 16 ==
+// 0) and one chunk hit 16 distinct groups of 4 banks, and so do 8 lanes at
+// rows r0 .. r0 + 7 within 128 bytes.  (The earlier swizzle c ^ ((r >> 2) &
+// 3) met only the first condition: the dequantised tile's writes, 64 lanes
+// at 64 consecutive rows, then took half of the kernel's LDS bank-conflict
+// cycles, SQ_LDS_BANK_CONFLICT 7.43M -> 3.70M per gate/up call.)
+__host__ __device__ constexpr int sw_off(int r, int c) {
+  return r * (kSK * 2) + ((c ^ ((r >> 1) & 3) ^ ((r >> 3) & 1)) << 4);
+}
 // The same for a 128-byte A row of a stage (chunks 0 .. 7).
 __host__ __device__ constexpr int sw_off_a(int r, int c) { return r * kARow + ((c ^ ((r >> 1) & 7)) << 4); }
 
@@ -302,7 +309,8 @@ __global__ __launch_bounds__(kNT, 1) void w4mm_kernel(Args a) {
 
   // acc[i][j][e]: row mb + 128 wm + 16 i + 4 g + e, column n0 + 64 wn + 16 j + lane % 16
   const int r0 = mb + wm * kWM + 4 * g, c0 = n0 + wn * kWN + col;
-  if (gridDim.z == 1 && a.silu) {
+  const bool to_part = gridDim.z > 1 || a.to_part;
+  if (!to_part && a.silu) {
     // this wave's 64 columns are gate features f .. f + 31 (tiles j = 0, 1)
     // and then their up columns (j = 2, 3): a lane holds both halves of its
     // features
@@ -319,7 +327,7 @@ __global__ __launch_bounds__(kNT, 1) void w4mm_kernel(Args a) {
         cr[0] = (uint16_t)p;
         cr[16] = (uint16_t)(p >> 16);
       }
-  } else if (gridDim.z == 1) {
+  } else if (!to_part) {
 #pragma unroll
     for (int i = 0; i < kMT; ++i)
 #pragma unroll
@@ -417,9 +425,11 @@ extern "C" size_t cfa_w4a16_gemm_zp_workspace_size(int M, int N, int K) {
   return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
 }
 
+// mode: 0 bf16 C, 1 SiLU-gated bf16 C, 2 fp32 partials only (in workspace)
 static int w4mm_launch(const void *a, const uint32_t *b_quant, const void *scales, const void *zeros,
                        int M, int N, int K, int group_size, void *c, void *workspace,
-                       size_t workspace_bytes, void *stream, bool silu) {
+                       size_t workspace_bytes, void *stream, int mode) {
+  const bool silu = mode == 1, part_only = mode == 2;
   using namespace cfa::abi;
   using namespace cfa::w4mm;
   clear_error();
@@ -428,15 +438,16 @@ static int w4mm_launch(const void *a, const uint32_t *b_quant, const void *scale
   if (K % kSK != 0) return fail_arg("K must be a multiple of 32");
   if (group_size <= 0 || group_size % kSK != 0 || K % group_size != 0)
     return fail_arg("group_size must be a multiple of 32 that divides K");
-  if (!a || !b_quant || !scales || !c) return fail_arg("null pointer");
+  if (!a || !b_quant || !scales || (!c && !part_only)) return fail_arg("null pointer");
   if ((((uintptr_t)a | (uintptr_t)c | (uintptr_t)b_quant | (uintptr_t)scales | (uintptr_t)zeros) & 15) != 0)
     return fail_arg("a, b_quant, scales, zeros and c must be 16-byte aligned");
   int spp = 0;
   if ((long long)M * K >= (1LL << 31)) return fail_arg("M * K must be below 2^31");
   const int splits = choose_splits(M, N, K, device_cu_count(), &spp);
-  const size_t need = splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
+  const size_t need = (splits > 1 || part_only) ? (size_t)splits * M * N * sizeof(float) : 0;
   if (need && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15) != 0))
-    return fail_arg("workspace too small (see cfa_w4a16_gemm_zp_workspace_size)");
+    return fail_arg(part_only ? "part too small (cfa_w4a16_gemm_zp_splits x M x N fp32)"
+                              : "workspace too small (see cfa_w4a16_gemm_zp_workspace_size)");
   Args g{};
   g.A = (const uint16_t *)a;
   g.q = b_quant;
@@ -450,6 +461,7 @@ static int w4mm_launch(const void *a, const uint32_t *b_quant, const void *scale
   g.group = group_size;
   g.slices_per_split = spp;
   g.silu = silu ? 1 : 0;
+  g.to_part = part_only ? 1 : 0;
   const long long mt = (M + kBM - 1) / kBM;
   if (mt > 65535) return fail_arg("M too large");
   hipStream_t st = (hipStream_t)stream;
@@ -458,6 +470,7 @@ static int w4mm_launch(const void *a, const uint32_t *b_quant, const void *scale
   g.mtiles = (int)mt;
   CFA_LAUNCH(silu ? "w4a16_gemm_zp_silu" : "w4a16_gemm_zp", w4mm_kernel,
              dim3((unsigned)blocks, 1, (unsigned)splits), dim3(kNT), 0, st, g);
+  if (part_only) return CFA_OK;
   if (splits > 1 && silu) {
     const long long MF = (long long)M * (N / 2);  // N % 256 == 0: four features per thread
     CFA_LAUNCH("w4a16_gemm_zp_reduce", w4mm_reduce_silu_kernel,
@@ -475,7 +488,7 @@ extern "C" int cfa_w4a16_gemm_zp(const void *a, const uint32_t *b_quant, const v
                                  const void *zeros, int M, int N, int K, int group_size, void *c,
                                  void *workspace, size_t workspace_bytes, void *stream) {
   return w4mm_launch(a, b_quant, scales, zeros, M, N, K, group_size, c, workspace, workspace_bytes,
-                     stream, false);
+                     stream, 0);
 }
 
 extern "C" int cfa_w4a16_gemm_zp_silu(const void *a, const uint32_t *b_quant, const void *scales,
@@ -483,5 +496,17 @@ extern "C" int cfa_w4a16_gemm_zp_silu(const void *a, const uint32_t *b_quant, co
                                       void *c, void *workspace, size_t workspace_bytes,
                                       void *stream) {
   return w4mm_launch(a, b_quant, scales, zeros, M, N, K, group_size, c, workspace, workspace_bytes,
-                     stream, true);
+                     stream, 1);
+}
+
+extern "C" int cfa_w4a16_gemm_zp_splits(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || N % cfa::w4mm::kBN != 0 || K % cfa::w4mm::kSK != 0) return 0;
+  return cfa::w4mm::choose_splits(M, N, K, cfa::abi::device_cu_count(), nullptr);
+}
+
+extern "C" int cfa_w4a16_gemm_zp_partials(const void *a, const uint32_t *b_quant, const void *scales,
+                                          const void *zeros, int M, int N, int K, int group_size,
+                                          float *part, size_t part_bytes, void *stream) {
+  return w4mm_launch(a, b_quant, scales, zeros, M, N, K, group_size, nullptr, part, part_bytes,
+                     stream, 2);
 }

@@ -83,6 +83,22 @@ def rmsnorm_(h: torch.Tensor, delta: Optional[torch.Tensor], w: torch.Tensor, ep
     return out
 
 
+def add_norm_(h: torch.Tensor, delta: Optional[torch.Tensor], w: torch.Tensor, eps: float,
+              out: torch.Tensor) -> torch.Tensor:
+    """rmsnorm_ with delta given as bf16 [M, d], as fp32 split-K partials
+    [S, M, d] of the W4A16 GEMM (summed in slab order, rounded to bf16, then
+    added: cfa_rmsnorm_partials), or None."""
+    if delta is None or delta.dim() == 2:
+        return rmsnorm_(h, delta, w, eps, out)
+    S, M, d = delta.shape
+    if h.shape != (M, d) or delta.dtype != torch.float32 or not delta.is_contiguous():
+        raise ValueError("partials must be contiguous fp32 [S, M, d]")
+    rc = _lib.load().cfa_rmsnorm_partials(h.data_ptr(), delta.data_ptr(), S, w.data_ptr(),
+                                          out.data_ptr(), M, d, float(eps), _stream_ptr(h.device))
+    _lib.check(rc, "cfa_rmsnorm_partials")
+    return out
+
+
 def silu_mul(gu: torch.Tensor) -> torch.Tensor:
     """[M, 2F] = [g | u] -> silu(g) * u in bf16 (cfa_silu_mul)."""
     M, F2 = gu.shape
@@ -254,17 +270,20 @@ class TargetModel:
         x = torch.empty_like(h)
         q = torch.empty(B, N, Hq, hd, dtype=torch.bfloat16, device=tokens.device)
         delta = None
+        # the O and down projections hand their split-K partials (in
+        # self.scratch) straight to the next residual add + RMSNorm, which
+        # sums them (add_norm_) before the next GEMM reuses the scratch
         for li, L in enumerate(self.layers):
-            rmsnorm_(h, delta, L["attn_norm"], s.eps, x)         # h += delta; x = norm(h)
+            add_norm_(h, delta, L["attn_norm"], s.eps, x)        # h += delta; x = norm(h)
             qkv = L["wqkv"](x, self.scratch)
             rope_kv_paged(qkv, pos, B, N, s, q, kv, li, block_tables, base_i)
             o = tree_attention(q, kv.key_pool, kv.value_pool, block_tables, base_lens, masks,
                                layer=li, max_keys=max_keys, workspace=self.attn_ws)
-            delta = L["wo"](o.reshape(M, Hq * hd), self.scratch)
-            rmsnorm_(h, delta, L["ffn_norm"], s.eps, x)
+            add_norm_(h, L["wo"].partials(o.reshape(M, Hq * hd), self.scratch), L["ffn_norm"],
+                      s.eps, x)
             a = L["wgu"].silu_gated(x, self.scratch)
-            delta = L["wdown"](a, self.scratch)
-        rmsnorm_(h, delta, self.norm, s.eps, x)
+            delta = L["wdown"].partials(a, self.scratch)
+        add_norm_(h, delta, self.norm, s.eps, x)
         return (x @ self.lm_head).float().view(B, N, s.vocab)
 
 

@@ -21,6 +21,7 @@ from . import _lib
 from .verify import _stream_ptr
 
 __all__ = ["pack_int4_weights", "w4a16_dequant", "w4a16_gemm", "w4a16_gemm_zp",
+           "w4a16_gemm_zp_partials",
            "int4_gemm_dequant", "W4A16Linear"]
 
 
@@ -149,6 +150,43 @@ def w4a16_gemm_zp(a: torch.Tensor, b_quant: torch.Tensor, scales: torch.Tensor,
     return out
 
 
+def w4a16_gemm_zp_partials(a: torch.Tensor, b_quant: torch.Tensor, scales: torch.Tensor,
+                           zeros: Optional[torch.Tensor] = None, *, group_size: int = 128,
+                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The fused product left as its split-K partials: fp32 [S, M, N]
+    (cfa_w4a16_gemm_zp_partials), a view of `workspace` (uint8) when it is
+    large enough; bf16 of their sum in slab order is w4a16_gemm_zp's result
+    (cfa_rmsnorm_partials sums them)."""
+    if a.dtype != torch.bfloat16 or a.dim() != 2:
+        raise ValueError("a must be a bf16 [M, K] tensor")
+    M, K = a.shape
+    N = b_quant.shape[1]
+    if b_quant.shape[0] * 8 != K:
+        raise ValueError("K of a and b_quant differ")
+    if scales.dtype != torch.float16 or tuple(scales.shape) != (K // group_size, N):
+        raise ValueError("scales must be fp16 [K/group_size, N]")
+    if zeros is not None and (zeros.dtype != torch.float16 or zeros.shape != scales.shape):
+        raise ValueError("zeros must be fp16 [K/group_size, N]")
+    lib = _lib.load()
+    S = lib.cfa_w4a16_gemm_zp_splits(M, N, K)
+    if S <= 0:
+        raise ValueError("shape not taken by cfa_w4a16_gemm_zp (N % 256, K % 32)")
+    need = S * M * N * 4
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        part = torch.empty(S, M, N, dtype=torch.float32, device=a.device)
+    else:
+        part = workspace.view(torch.uint8)[:need].view(torch.float32).view(S, M, N)
+    sc = scales.contiguous()
+    zz = zeros.contiguous() if zeros is not None else None
+    with torch.cuda.device(a.device):
+        rc = lib.cfa_w4a16_gemm_zp_partials(a.data_ptr(), b_quant.data_ptr(), sc.data_ptr(),
+                                            zz.data_ptr() if zz is not None else None, M, N, K,
+                                            group_size, part.data_ptr(), need,
+                                            _stream_ptr(a.device))
+    _lib.check(rc, "cfa_w4a16_gemm_zp_partials")
+    return part
+
+
 class W4A16Linear:
     """y = x @ W with W [K, N] held as packed INT4 + fp16 group scales and
     zero points, w = (nibble - z) * s (dequantize.cuh:12-25).
@@ -193,6 +231,15 @@ class W4A16Linear:
         w4a16_dequant(self.qweight, self.scales, self.zeros, group_size=self.group,
                       dtype=x.dtype, out=wt, transposed=True)
         return x @ wt.t()
+
+    def partials(self, x: torch.Tensor, scratch: torch.Tensor) -> torch.Tensor:
+        """x @ W as fp32 split-K partials [S, M, N] in `scratch` (for a
+        consumer that sums them, cfa_rmsnorm_partials) where the fused kernel
+        takes the shape; else the bf16 product [M, N]."""
+        if self.fused_zp and gemm_zp_ok(x, self.qweight, self.group):
+            return w4a16_gemm_zp_partials(x, self.qweight, self.scales, self.zeros,
+                                          group_size=self.group, workspace=scratch)
+        return self(x, scratch)
 
     def silu_gated(self, x: torch.Tensor, scratch: torch.Tensor) -> torch.Tensor:
         """silu(x @ W_gate) * (x @ W_up) [M, N / 2] for W in the interleaved

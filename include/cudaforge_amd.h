@@ -333,6 +333,16 @@ int cfa_w4a16_gemm_zp(const void *a, const uint32_t *b_quant, const void *scales
 int cfa_w4a16_gemm_zp_silu(const void *a, const uint32_t *b_quant, const void *scales,
                            const void *zeros, int M, int N, int K, int group_size, void *out,
                            void *workspace, size_t workspace_bytes, void *stream);
+/* The same product left as its split-K fp32 partials (no counterpart in the
+ * reference; for a consumer that sums them itself, cfa_rmsnorm_partials):
+ * part [S, M, N] fp32 with S = cfa_w4a16_gemm_zp_splits(M, N, K) (>= 1; 0
+ * for a shape the kernel does not take), slab s the product over split s's
+ * k range, so that bf16 of their sum in slab order is cfa_w4a16_gemm_zp's
+ * output.  part_bytes >= S * M * N * 4, 16-byte aligned. */
+int cfa_w4a16_gemm_zp_splits(int M, int N, int K);
+int cfa_w4a16_gemm_zp_partials(const void *a, const uint32_t *b_quant, const void *scales,
+                               const void *zeros, int M, int N, int K, int group_size,
+                               float *part, size_t part_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
  * Fused layers of the model-scale verify step (bf16 activations, fp32 math;
@@ -354,6 +364,11 @@ int cfa_w4a16_gemm_zp_silu(const void *a, const uint32_t *b_quant, const void *s
  */
 int cfa_rmsnorm(void *h, const void *delta, const void *weight, void *out, int M, int d,
                 float eps, void *stream);
+/* The same with delta = bf16(sum of part[0 .. splits) in slab order), part
+ * [splits, M, d] fp32 (the partials of cfa_w4a16_gemm_zp_partials): the bits
+ * of cfa_w4a16_gemm_zp followed by cfa_rmsnorm, without the reduce pass. */
+int cfa_rmsnorm_partials(void *h, const float *part, int splits, const void *weight, void *out,
+                         int M, int d, float eps, void *stream);
 int cfa_rope_kv_paged(const void *qkv, const int32_t *positions, int B, int n, int Hq, int Hkv,
                       int D, float theta, void *q_out, void *k_pool, void *v_pool, int layer,
                       int num_layers, int block_size, const int32_t *block_tables, int max_blocks,

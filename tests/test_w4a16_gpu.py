@@ -207,6 +207,35 @@ def test_gemm_zp_silu_bit_exact(device, M, N, K):
     assert torch.equal(fused, plain)
 
 
+@pytest.mark.parametrize("M,N,K", [(504, 4096, 4096), (504, 4096, 14336), (600, 768, 1024),
+                                   (37, 256, 512), (1, 256, 128)])
+def test_gemm_zp_partials_rmsnorm_bit_exact(device, M, N, K):
+    """The GEMM's split-K partials summed by cfa_rmsnorm_partials give the
+    bits of cfa_w4a16_gemm_zp followed by cfa_rmsnorm (residual h and the
+    normalised output), with 8, 4 and 1 split(s) -- one split forced to
+    fp32 partials as well."""
+    from cudaforge_amd import _lib
+    from cudaforge_amd.spec_step import add_norm_, rmsnorm_
+    from cudaforge_amd.w4a16 import w4a16_gemm_zp, w4a16_gemm_zp_partials
+
+    g = torch.Generator().manual_seed(3 * M + N + K)
+    group = 128
+    a = torch.randn(M, K, generator=g).bfloat16().to(device)
+    q = pack_int4_weights(torch.randint(0, 16, (K, N), generator=g, dtype=torch.int32)).to(device)
+    scales = ((torch.rand(K // group, N, generator=g) * 0.5 + 0.5) / K ** 0.5).half().to(device)
+    zeros = torch.full((K // group, N), 7.5, dtype=torch.float16, device=device)
+    h0 = torch.randn(M, N, generator=g).bfloat16().to(device)
+    w = (1 + 0.1 * torch.randn(N, generator=g)).bfloat16().to(device)
+    part = w4a16_gemm_zp_partials(a, q, scales, zeros, group_size=group)
+    assert part.shape[0] == _lib.load().cfa_w4a16_gemm_zp_splits(M, N, K) >= 1
+    h1, x1 = h0.clone(), torch.empty_like(h0)
+    add_norm_(h1, part, w, 1e-5, x1)
+    h2, x2 = h0.clone(), torch.empty_like(h0)
+    rmsnorm_(h2, w4a16_gemm_zp(a, q, scales, zeros, group_size=group), w, 1e-5, x2)
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h2) and torch.equal(x1, x2)
+
+
 def test_gemm_zp_rejects_bad_shapes(device):
     from cudaforge_amd.w4a16 import w4a16_gemm_zp
 
