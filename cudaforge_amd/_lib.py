@@ -146,6 +146,8 @@ SIGNATURES: dict[str, tuple] = {
     "cfa_rmsnorm_partials": (_i, [_p, _p, _i, _p, _p, _i, _i, _f, _p]),
     "cfa_rope_kv_paged": (
         _i, [_p, _p, _i, _i, _i, _i, _i, _f, _p, _p, _p, _i, _i, _i, _p, _i, _p, _p]),
+    "cfa_rope_kv_paged_partials": (
+        _i, [_p, _i, _p, _i, _i, _i, _i, _i, _f, _p, _p, _p, _i, _i, _i, _p, _i, _p, _p]),
     "cfa_rope_kv_strided": (
         _i, [_p, _p, _i, _i, _i, _i, _i, _f, _p, _p, _i64p, _p, _i64p, _p, _p]),
     "cfa_silu_mul": (_i, [_p, _p, _i, _i, _p]),

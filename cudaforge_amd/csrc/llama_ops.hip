@@ -137,50 +137,119 @@ struct RopeArgs {
   // strided
   const int32_t *slots;  // [M]
   long long k_sb, k_sh, k_ss, k_se, v_sb, v_sh, v_ss;
+  // qkv given as `splits` fp32 slabs part[s][M][H * D] (split-K partials of
+  // the W4A16 GEMM) instead: element = bf16 of their sum in slab order
+  const float *part;
+  int splits;
+  long long slab;
 };
 
+// bf16 bits of elements idx .. idx + P - 1 of the fused projection (P = 4:
+// one 8-byte bf16 load, or one 16-byte load per fp32 slab)
+template <int P>
+__device__ __forceinline__ void qkv_load(const RopeArgs &a, long long idx, uint16_t (&v)[P]) {
+  if constexpr (P == 4) {
+    if (a.part) {
+      float4 s = *reinterpret_cast<const float4 *>(a.part + idx);
+      for (int sp = 1; sp < a.splits; ++sp) {
+        const float4 t = *reinterpret_cast<const float4 *>(a.part + sp * a.slab + idx);
+        s.x += t.x;
+        s.y += t.y;
+        s.z += t.z;
+        s.w += t.w;
+      }
+      v[0] = f2bf(s.x);
+      v[1] = f2bf(s.y);
+      v[2] = f2bf(s.z);
+      v[3] = f2bf(s.w);
+    } else {
+      const uint2 w = *reinterpret_cast<const uint2 *>(a.qkv + idx);
+      v[0] = (uint16_t)w.x;
+      v[1] = (uint16_t)(w.x >> 16);
+      v[2] = (uint16_t)w.y;
+      v[3] = (uint16_t)(w.y >> 16);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+      if (!a.part) {
+        v[k] = a.qkv[idx + k];
+        continue;
+      }
+      float x = a.part[idx + k];
+      for (int sp = 1; sp < a.splits; ++sp) x += a.part[sp * a.slab + idx + k];
+      v[k] = f2bf(x);
+    }
+  }
+}
+
+// P contiguous bf16 values to dst (P = 4: one 8-byte store)
+template <int P>
+__device__ __forceinline__ void store_p(uint16_t *dst, const uint16_t (&v)[P]) {
+  if constexpr (P == 4) {
+    *reinterpret_cast<uint2 *>(dst) =
+        make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
+  } else {
+#pragma unroll
+    for (int k = 0; k < P; ++k) dst[k] = v[k];
+  }
+}
+
+// One thread per (token, head, P consecutive rotation pairs), or per P
+// consecutive v elements; P = 4 when D / 2 % 4 == 0 and the buffers are
+// 16-byte aligned, else 1.  Every element is computed the same way for both P.
+template <int P>
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
-  const int half = a.D / 2;
+  const int half = a.D / 2, hp = half / P, dp = a.D / P;
   const int H = a.Hq + 2 * a.Hkv;
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-  const long long total = (long long)a.M * (a.Hq + a.Hkv) * half;
-  const long long tv = (long long)a.M * a.Hkv * a.D;
+  const long long total = (long long)a.M * (a.Hq + a.Hkv) * hp;
+  const long long tv = (long long)a.M * a.Hkv * dp;
   if (t >= total + tv) return;
-  if (t >= total) {  // v copy: one element per thread
+  if (t >= total) {  // v copy
     const long long r = t - total;
-    const int e = (int)(r % a.D);
-    const int h = (int)((r / a.D) % a.Hkv);
-    const int m = (int)(r / ((long long)a.D * a.Hkv));
-    const uint16_t val = a.qkv[((long long)m * H + a.Hq + a.Hkv + h) * a.D + e];
+    const int e0 = (int)(r % dp) * P;
+    const int h = (int)((r / dp) % a.Hkv);
+    const int m = (int)(r / ((long long)dp * a.Hkv));
+    uint16_t val[P];
+    qkv_load<P>(a, ((long long)m * H + a.Hq + a.Hkv + h) * a.D + e0, val);
     const int b = m / a.n, j = m % a.n;
     if (a.kind == 0) {
       const int slot = a.base[b] + j;
       if (slot / a.bs >= a.max_blocks) return;
       const long long blk = a.block_tables[(long long)b * a.max_blocks + slot / a.bs];
       if (blk < 0) return;  // unmapped page: never written
-      a.vc[blk * a.blk_stride + a.layer * a.layer_stride + h * a.head_stride +
-           (long long)(slot % a.bs) * a.D + e] = val;
+      store_p<P>(a.vc + blk * a.blk_stride + a.layer * a.layer_stride + h * a.head_stride +
+                     (long long)(slot % a.bs) * a.D + e0,
+                 val);
     } else {
       const long long slot = a.slots[m];
-      a.vc[b * a.v_sb + h * a.v_sh + slot * a.v_ss + e] = val;
+      store_p<P>(a.vc + b * a.v_sb + h * a.v_sh + slot * a.v_ss + e0, val);
     }
     return;
   }
-  const int i = (int)(t % half);
-  const int hh = (int)((t / half) % (a.Hq + a.Hkv));
-  const int m = (int)(t / ((long long)half * (a.Hq + a.Hkv)));
-  const uint16_t *src = a.qkv + ((long long)m * H + hh) * a.D;
-  const float x0 = bf2f(src[i]), x1 = bf2f(src[i + half]);
-  const float inv_freq = exp2f(-(float)(2 * i) / (float)a.D * a.log2_theta);
-  const float ang = (float)a.pos[m] * inv_freq;
-  float sn, cs;
-  sincosf(ang, &sn, &cs);
-  const uint16_t y0 = f2bf(x0 * cs - x1 * sn);
-  const uint16_t y1 = f2bf(x1 * cs + x0 * sn);
+  const int i0 = (int)(t % hp) * P;
+  const int hh = (int)((t / hp) % (a.Hq + a.Hkv));
+  const int m = (int)(t / ((long long)hp * (a.Hq + a.Hkv)));
+  const long long src = ((long long)m * H + hh) * a.D;
+  uint16_t lo[P], hi[P], y0[P], y1[P];
+  qkv_load<P>(a, src + i0, lo);
+  qkv_load<P>(a, src + i0 + half, hi);
+#pragma unroll
+  for (int k = 0; k < P; ++k) {
+    const int i = i0 + k;
+    const float x0 = bf2f(lo[k]), x1 = bf2f(hi[k]);
+    const float inv_freq = exp2f(-(float)(2 * i) / (float)a.D * a.log2_theta);
+    const float ang = (float)a.pos[m] * inv_freq;
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    y0[k] = f2bf(x0 * cs - x1 * sn);
+    y1[k] = f2bf(x1 * cs + x0 * sn);
+  }
   if (hh < a.Hq) {
     uint16_t *dst = a.q_out + ((long long)m * a.Hq + hh) * a.D;
-    dst[i] = y0;
-    dst[i + half] = y1;
+    store_p<P>(dst + i0, y0);
+    store_p<P>(dst + i0 + half, y1);
     return;
   }
   const int h = hh - a.Hq;
@@ -192,14 +261,36 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
     if (blk < 0) return;
     uint16_t *dst = a.kc + blk * a.blk_stride + a.layer * a.layer_stride + h * a.head_stride +
                     (long long)(slot % a.bs) * a.D;
-    dst[i] = y0;
-    dst[i + half] = y1;
+    store_p<P>(dst + i0, y0);
+    store_p<P>(dst + i0 + half, y1);
   } else {
     const long long slot = a.slots[m];
     uint16_t *dst = a.kc + b * a.k_sb + h * a.k_sh + slot * a.k_ss;
-    dst[(long long)i * a.k_se] = y0;
-    dst[(long long)(i + half) * a.k_se] = y1;
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+      dst[(long long)(i0 + k) * a.k_se] = y0[k];
+      dst[(long long)(i0 + k + half) * a.k_se] = y1[k];
+    }
   }
+}
+
+static int launch_rope(const RopeArgs &a, void *stream) {
+  // four pairs per thread where every access of four elements is aligned
+  // (the strided cache's v rows: v_ss a multiple of 4 as well)
+  const bool aligned =
+      (((uintptr_t)a.qkv | (uintptr_t)a.part | (uintptr_t)a.q_out | (uintptr_t)a.kc |
+        (uintptr_t)a.vc) & 15) == 0 &&
+      (a.kind == 0 || (a.v_sb % 4 == 0 && a.v_sh % 4 == 0 && a.v_ss % 4 == 0));
+  const int P = (a.D % 8 == 0 && aligned) ? 4 : 1;
+  const long long total =
+      (long long)a.M * (a.Hq + a.Hkv) * (a.D / 2 / P) + (long long)a.M * a.Hkv * (a.D / P);
+  if (P == 4)
+    CFA_LAUNCH("rope_kv", rope_kv_kernel<4>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+               (hipStream_t)stream, a);
+  else
+    CFA_LAUNCH("rope_kv", rope_kv_kernel<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+               (hipStream_t)stream, a);
+  return CFA_OK;
 }
 
 // out[m, f] = bf16(bf16(silu(g)) * u) for gu [M, 2F] = [g | u] (the rounding
@@ -265,19 +356,23 @@ extern "C" int cfa_rmsnorm_partials(void *h, const float *part, int splits, cons
   return CFA_OK;
 }
 
-extern "C" int cfa_rope_kv_paged(const void *qkv, const int32_t *positions, int B, int n, int Hq,
-                                 int Hkv, int D, float theta, void *q_out, void *k_pool,
-                                 void *v_pool, int layer, int num_layers, int block_size,
-                                 const int32_t *block_tables, int max_blocks,
-                                 const int32_t *base_lens, void *stream) {
+static int rope_paged(const void *qkv, const float *part, int splits, const int32_t *positions,
+                      int B, int n, int Hq, int Hkv, int D, float theta, void *q_out,
+                      void *k_pool, void *v_pool, int layer, int num_layers, int block_size,
+                      const int32_t *block_tables, int max_blocks, const int32_t *base_lens,
+                      void *stream) {
   using namespace cfa::abi;
   clear_error();
   if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || D % 2) return fail_arg("bad shape");
   if (layer < 0 || layer >= num_layers || block_size <= 0) return fail_arg("bad layer or block size");
-  if (!qkv || !positions || !q_out || !k_pool || !v_pool || !block_tables || !base_lens)
+  if ((!qkv && !part) || !positions || !q_out || !k_pool || !v_pool || !block_tables || !base_lens)
     return fail_arg("null pointer");
+  if (part && splits <= 0) return fail_arg("splits must be positive");
   RopeArgs a{};
   a.qkv = (const uint16_t *)qkv;
+  a.part = part;
+  a.splits = splits;
+  a.slab = (long long)B * n * (Hq + 2 * Hkv) * D;
   a.pos = positions;
   a.q_out = (uint16_t *)q_out;
   a.kc = (uint16_t *)k_pool;
@@ -297,10 +392,31 @@ extern "C" int cfa_rope_kv_paged(const void *qkv, const int32_t *positions, int 
   a.head_stride = (long long)block_size * D;
   a.layer_stride = (long long)Hkv * a.head_stride;
   a.blk_stride = (long long)num_layers * a.layer_stride;
-  const long long total = (long long)a.M * (Hq + Hkv) * (D / 2) + (long long)a.M * Hkv * D;
-  CFA_LAUNCH("rope_kv", rope_kv_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-             (hipStream_t)stream, a);
-  return CFA_OK;
+  return launch_rope(a, stream);
+}
+
+extern "C" int cfa_rope_kv_paged(const void *qkv, const int32_t *positions, int B, int n, int Hq,
+                                 int Hkv, int D, float theta, void *q_out, void *k_pool,
+                                 void *v_pool, int layer, int num_layers, int block_size,
+                                 const int32_t *block_tables, int max_blocks,
+                                 const int32_t *base_lens, void *stream) {
+  return rope_paged(qkv, nullptr, 0, positions, B, n, Hq, Hkv, D, theta, q_out, k_pool, v_pool,
+                    layer, num_layers, block_size, block_tables, max_blocks, base_lens, stream);
+}
+
+extern "C" int cfa_rope_kv_paged_partials(const float *part, int splits, const int32_t *positions,
+                                          int B, int n, int Hq, int Hkv, int D, float theta,
+                                          void *q_out, void *k_pool, void *v_pool, int layer,
+                                          int num_layers, int block_size,
+                                          const int32_t *block_tables, int max_blocks,
+                                          const int32_t *base_lens, void *stream) {
+  if (!part) {
+    cfa::abi::clear_error();
+    return cfa::abi::fail_arg("null pointer");
+  }
+  return rope_paged(nullptr, part, splits, positions, B, n, Hq, Hkv, D, theta, q_out, k_pool,
+                    v_pool, layer, num_layers, block_size, block_tables, max_blocks, base_lens,
+                    stream);
 }
 
 extern "C" int cfa_rope_kv_strided(const void *qkv, const int32_t *positions, int B, int n, int Hq,
@@ -334,10 +450,7 @@ extern "C" int cfa_rope_kv_strided(const void *qkv, const int32_t *positions, in
   a.v_sb = v_strides[0];
   a.v_sh = v_strides[1];
   a.v_ss = v_strides[2];
-  const long long total = (long long)a.M * (Hq + Hkv) * (D / 2) + (long long)a.M * Hkv * D;
-  CFA_LAUNCH("rope_kv", rope_kv_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-             (hipStream_t)stream, a);
-  return CFA_OK;
+  return launch_rope(a, stream);
 }
 
 extern "C" int cfa_silu_mul(const void *gu, void *out, int M, int F, void *stream) {

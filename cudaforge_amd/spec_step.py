@@ -183,7 +183,19 @@ def rope_kv_pools(qkv: torch.Tensor, pos: torch.Tensor, B: int, n: int, s: "Llam
                   block_tables: torch.Tensor, base: torch.Tensor) -> None:
     """Rotary embedding of q and k from qkv [B*n, (Hq+2Hkv)*D]; q -> q_out,
     k and v -> slots base + j of `layer` in the paged pools
-    [blocks, layers, Hkv, block_size, D]."""
+    [blocks, layers, Hkv, block_size, D].  qkv may also be the W4A16 GEMM's
+    fp32 split-K partials [S, B*n, (Hq+2Hkv)*D], summed in slab order and
+    rounded to bf16 element by element (cfa_rope_kv_paged_partials)."""
+    if qkv.dim() == 3:
+        if qkv.dtype != torch.float32 or not qkv.is_contiguous():
+            raise ValueError("partials must be contiguous fp32 [S, M, N]")
+        rc = _lib.load().cfa_rope_kv_paged_partials(
+            qkv.data_ptr(), qkv.shape[0], pos.data_ptr(), B, n, s.n_heads, s.n_kv_heads,
+            s.head_dim, float(s.rope_theta), q_out.data_ptr(), k_pool.data_ptr(),
+            v_pool.data_ptr(), layer, k_pool.shape[1], k_pool.shape[3], block_tables.data_ptr(),
+            block_tables.shape[1], base.data_ptr(), _stream_ptr(qkv.device))
+        _lib.check(rc, "cfa_rope_kv_paged_partials")
+        return
     rc = _lib.load().cfa_rope_kv_paged(
         qkv.data_ptr(), pos.data_ptr(), B, n, s.n_heads, s.n_kv_heads, s.head_dim,
         float(s.rope_theta), q_out.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
@@ -270,12 +282,13 @@ class TargetModel:
         x = torch.empty_like(h)
         q = torch.empty(B, N, Hq, hd, dtype=torch.bfloat16, device=tokens.device)
         delta = None
-        # the O and down projections hand their split-K partials (in
-        # self.scratch) straight to the next residual add + RMSNorm, which
-        # sums them (add_norm_) before the next GEMM reuses the scratch
+        # the QKV, O and down projections hand their split-K partials (in
+        # self.scratch) straight to their consumers -- the rope / K-V write
+        # and the residual add + RMSNorm (add_norm_) -- which sum them before
+        # the next GEMM reuses the scratch
         for li, L in enumerate(self.layers):
             add_norm_(h, delta, L["attn_norm"], s.eps, x)        # h += delta; x = norm(h)
-            qkv = L["wqkv"](x, self.scratch)
+            qkv = L["wqkv"].partials(x, self.scratch)            # summed by the rope kernel
             rope_kv_paged(qkv, pos, B, N, s, q, kv, li, block_tables, base_i)
             o = tree_attention(q, kv.key_pool, kv.value_pool, block_tables, base_lens, masks,
                                layer=li, max_keys=max_keys, workspace=self.attn_ws)

@@ -373,6 +373,15 @@ int cfa_rope_kv_paged(const void *qkv, const int32_t *positions, int B, int n, i
                       int D, float theta, void *q_out, void *k_pool, void *v_pool, int layer,
                       int num_layers, int block_size, const int32_t *block_tables, int max_blocks,
                       const int32_t *base_lens, void *stream);
+/* The same from the fused projection's split-K fp32 partials part [splits,
+ * B*n, (Hq + 2*Hkv)*D] (cfa_w4a16_gemm_zp_partials): each element is bf16 of
+ * their sum in slab order, the bits of cfa_w4a16_gemm_zp followed by
+ * cfa_rope_kv_paged, without the reduce pass. */
+int cfa_rope_kv_paged_partials(const float *part, int splits, const int32_t *positions, int B,
+                               int n, int Hq, int Hkv, int D, float theta, void *q_out,
+                               void *k_pool, void *v_pool, int layer, int num_layers,
+                               int block_size, const int32_t *block_tables, int max_blocks,
+                               const int32_t *base_lens, void *stream);
 int cfa_rope_kv_strided(const void *qkv, const int32_t *positions, int B, int n, int Hq, int Hkv,
                         int D, float theta, void *q_out, void *k_cache, const int64_t *k_strides,
                         void *v_cache, const int64_t *v_strides, const int32_t *slots,

@@ -112,6 +112,44 @@ def test_rope_kv_paged(device):
             assert not kp[blk, 0, :, slot % bs].any()            # other layer untouched
 
 
+@pytest.mark.parametrize("splits", [1, 3, 5])
+def test_rope_kv_paged_partials_bit_exact(device, splits):
+    """cfa_rope_kv_paged_partials on fp32 split-K partials [S, M, H*D] gives
+    the bits of cfa_rope_kv_paged on bf16 of their sum in slab order (what
+    the W4A16 GEMM's reduce writes): q, the K/V pools, and the untouched
+    layer."""
+    s = LlamaShape(2, 512, 4, 2, 128, 256, 100)
+    B, n, bs = 3, 5, 16
+    H = s.n_heads + 2 * s.n_kv_heads
+    g = torch.Generator().manual_seed(11 + splits)
+    part = torch.randn(splits, B * n, H * 128, generator=g).to(device)
+    acc = part[0].clone()
+    for i in range(1, splits):
+        acc += part[i]                                   # fp32, slab order
+    qkv = acc.bfloat16()
+    pos = torch.tensor([c + j * 7 for c in (13, 30, 0) for j in range(n)], dtype=torch.int32,
+                       device=device)
+    outs = []
+    for src in (part, qkv):
+        cfg = KVCacheConfig(num_layers=2, num_kv_heads=2, head_dim=128, block_size=bs,
+                            total_gpu_blocks=32, max_supported_batch_size=4,
+                            max_blocks_per_sequence=8)
+        kv = PagedKVCache(cfg, device=device)
+        kv.key_pool.zero_()
+        kv.value_pool.zero_()
+        for b, c in enumerate((13, 30, 0)):
+            kv.register_sequence_with_prefix(b, list(range(c)))
+            kv.append_tokens(b, n)
+        desc = kv.prepare_batch_metadata(list(range(B)))
+        q = torch.empty(B * n, s.n_heads, 128, dtype=torch.bfloat16, device=device)
+        base = torch.tensor([13, 30, 0], dtype=torch.int32, device=device)
+        rope_kv_paged(src, pos, B, n, s, q, kv, 1, desc.block_tables, base)
+        outs.append((q, kv.key_pool.clone(), kv.value_pool.clone()))
+    torch.cuda.synchronize()
+    for x, y in zip(*outs):
+        assert torch.equal(x, y)
+
+
 def test_rope_kv_strided(device):
     s = LlamaShape(1, 256, 4, 2, 64, 256, 100)
     B, n, S = 2, 3, 40
