@@ -21,67 +21,37 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 
 // ---------------------------------------------------------------------------
 // h <- bf16(h + delta) (when delta is given); out <- bf16(h * rsqrt(mean(h^2)
-// + eps) * w).  One work-group per row, 8 elements (16 bytes) per access.
+// + eps) * w).  One work-group per row; thread t takes the 4-element vectors
+// (8 bytes of bf16, 16 of fp32) t, t + 256, ... in that order, so that every
+// wave access is contiguous, and sums its squares in that order before the
+// block reduction (both kernels below: the same bits).
 // ---------------------------------------------------------------------------
 constexpr int kNormNT = 256;
 
-// With `part` (and delta NULL) the delta is bf16 of the sum of `splits` fp32
-// slabs part[s][M][d] taken in slab order -- what the W4A16 GEMM's split-K
-// reduce writes -- so that the GEMM's partials need no separate reduce.
-__global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(uint16_t *h, const uint16_t *delta,
-                                                          const uint16_t *w, uint16_t *out, int d,
-                                                          float eps, const float *part, int splits,
-                                                          long long slab) {
-  const long long row = blockIdx.x;
-  uint16_t *hr = h + row * d;
-  const uint16_t *dr = delta ? delta + row * d : nullptr;
-  const float *pr = part ? part + row * d : nullptr;
-  uint16_t *orow = out + row * d;
-  const int nvec = d / 8;
-  float ss = 0.0f;
-  for (int v = threadIdx.x; v < nvec; v += kNormNT) {
-    uint4 x = reinterpret_cast<const uint4 *>(hr)[v];
-    if (dr || pr) {
-      uint4 y;
-      if (pr) {
-        float4 lo = reinterpret_cast<const float4 *>(pr)[2 * v];
-        float4 hi = reinterpret_cast<const float4 *>(pr)[2 * v + 1];
-        for (int sp = 1; sp < splits; ++sp) {
-          const float4 l2 = reinterpret_cast<const float4 *>(pr + sp * slab)[2 * v];
-          const float4 h2 = reinterpret_cast<const float4 *>(pr + sp * slab)[2 * v + 1];
-          lo.x += l2.x;
-          lo.y += l2.y;
-          lo.z += l2.z;
-          lo.w += l2.w;
-          hi.x += h2.x;
-          hi.y += h2.y;
-          hi.z += h2.z;
-          hi.w += h2.w;
-        }
-        y.x = (uint32_t)f2bf(lo.x) | ((uint32_t)f2bf(lo.y) << 16);
-        y.y = (uint32_t)f2bf(lo.z) | ((uint32_t)f2bf(lo.w) << 16);
-        y.z = (uint32_t)f2bf(hi.x) | ((uint32_t)f2bf(hi.y) << 16);
-        y.w = (uint32_t)f2bf(hi.z) | ((uint32_t)f2bf(hi.w) << 16);
-      } else {
-        y = reinterpret_cast<const uint4 *>(dr)[v];
-      }
-      uint32_t *xs = reinterpret_cast<uint32_t *>(&x);
-      const uint32_t *ys = reinterpret_cast<const uint32_t *>(&y);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float a0 = bf2f(xs[q] & 0xffff) + bf2f(ys[q] & 0xffff);
-        const float a1 = bf2f(xs[q] >> 16) + bf2f(ys[q] >> 16);
-        xs[q] = (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16);
-      }
-      reinterpret_cast<uint4 *>(hr)[v] = x;
-    }
-    const uint32_t *xs = reinterpret_cast<const uint32_t *>(&x);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float a0 = bf2f(xs[q] & 0xffff), a1 = bf2f(xs[q] >> 16);
-      ss += a0 * a0 + a1 * a1;
-    }
-  }
+// x (4 bf16) += the 4 values of d, each rounded to bf16 first; squares into ss
+__device__ __forceinline__ void norm_fold(uint2 &x, float d0, float d1, float d2, float d3,
+                                          float &ss) {
+  const float a0 = bf2f(x.x & 0xffff) + d0, a1 = bf2f(x.x >> 16) + d1;
+  const float a2 = bf2f(x.y & 0xffff) + d2, a3 = bf2f(x.y >> 16) + d3;
+  x.x = (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16);
+  x.y = (uint32_t)f2bf(a2) | ((uint32_t)f2bf(a3) << 16);
+}
+__device__ __forceinline__ void norm_sq(const uint2 &x, float &ss) {
+  const float a0 = bf2f(x.x & 0xffff), a1 = bf2f(x.x >> 16);
+  const float a2 = bf2f(x.y & 0xffff), a3 = bf2f(x.y >> 16);
+  ss += a0 * a0 + a1 * a1;
+  ss += a2 * a2 + a3 * a3;
+}
+__device__ __forceinline__ uint2 norm_scale(const uint2 &x, const uint2 &g, float inv) {
+  uint2 o;
+  o.x = (uint32_t)f2bf(bf2f(x.x & 0xffff) * inv * bf2f(g.x & 0xffff)) |
+        ((uint32_t)f2bf(bf2f(x.x >> 16) * inv * bf2f(g.x >> 16)) << 16);
+  o.y = (uint32_t)f2bf(bf2f(x.y & 0xffff) * inv * bf2f(g.y & 0xffff)) |
+        ((uint32_t)f2bf(bf2f(x.y >> 16) * inv * bf2f(g.y >> 16)) << 16);
+  return o;
+}
+// rsqrt(mean + eps) of the row from every thread's ss (fixed order)
+__device__ __forceinline__ float norm_inv(float ss, int d, float eps) {
   __shared__ float red[kNormNT / 64];
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
@@ -90,22 +60,120 @@ __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(uint16_t *h, const uin
   float tot = 0.0f;
 #pragma unroll
   for (int i = 0; i < kNormNT / 64; ++i) tot += red[i];
-  const float inv = rsqrtf(tot / (float)d + eps);
+  return rsqrtf(tot / (float)d + eps);
+}
+
+__global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(uint16_t *h, const uint16_t *delta,
+                                                          const uint16_t *w, uint16_t *out, int d,
+                                                          float eps) {
+  const long long row = blockIdx.x;
+  uint2 *hr = reinterpret_cast<uint2 *>(h + row * d);
+  const uint2 *dr = delta ? reinterpret_cast<const uint2 *>(delta + row * d) : nullptr;
+  uint2 *orow = reinterpret_cast<uint2 *>(out + row * d);
+  const uint2 *wr = reinterpret_cast<const uint2 *>(w);
+  const int nvec = d / 4;
+  float ss = 0.0f;
   for (int v = threadIdx.x; v < nvec; v += kNormNT) {
-    const uint4 x = reinterpret_cast<const uint4 *>(hr)[v];  // own writes, same thread
-    const uint4 g = reinterpret_cast<const uint4 *>(w)[v];
-    const uint32_t *xs = reinterpret_cast<const uint32_t *>(&x);
-    const uint32_t *gs = reinterpret_cast<const uint32_t *>(&g);
-    uint4 o;
-    uint32_t *os = reinterpret_cast<uint32_t *>(&o);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float a0 = bf2f(xs[q] & 0xffff) * inv * bf2f(gs[q] & 0xffff);
-      const float a1 = bf2f(xs[q] >> 16) * inv * bf2f(gs[q] >> 16);
-      os[q] = (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16);
+    uint2 x = hr[v];
+    if (dr) {
+      const uint2 y = dr[v];
+      norm_fold(x, bf2f(y.x & 0xffff), bf2f(y.x >> 16), bf2f(y.y & 0xffff), bf2f(y.y >> 16), ss);
+      hr[v] = x;
     }
-    reinterpret_cast<uint4 *>(orow)[v] = o;
+    norm_sq(x, ss);
   }
+  const float inv = norm_inv(ss, d, eps);
+  for (int v = threadIdx.x; v < nvec; v += kNormNT) orow[v] = norm_scale(hr[v], wr[v], inv);
+}
+
+// Sum, in slab order, of S fp32 slabs (4 consecutive values at p, p + slab,
+// ...): S > 0 a compile-time count, every load issued before the first add
+// (the sum is then one memory latency, not S); S == 0 the runtime count n.
+template <int S>
+__device__ __forceinline__ float4 slab_sum4(const float *p, long long slab, int n) {
+  if constexpr (S > 0) {
+    float4 v[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k) v[k] = *reinterpret_cast<const float4 *>(p + k * slab);
+    float4 acc = v[0];
+#pragma unroll
+    for (int k = 1; k < S; ++k) {
+      acc.x += v[k].x;
+      acc.y += v[k].y;
+      acc.z += v[k].z;
+      acc.w += v[k].w;
+    }
+    return acc;
+  } else {
+    float4 acc = *reinterpret_cast<const float4 *>(p);
+    for (int k = 1; k < n; ++k) {
+      const float4 t = *reinterpret_cast<const float4 *>(p + k * slab);
+      acc.x += t.x;
+      acc.y += t.y;
+      acc.z += t.z;
+      acc.w += t.w;
+    }
+    return acc;
+  }
+}
+
+__device__ __forceinline__ void norm_fold_part(uint2 &x, const float4 &p, float &ss) {
+  norm_fold(x, bf2f(f2bf(p.x)), bf2f(f2bf(p.y)), bf2f(f2bf(p.z)), bf2f(f2bf(p.w)), ss);
+}
+
+// rmsnorm_kernel with delta = bf16 of the sum of the split-K partials
+// part[s][M][d] (slab order) -- what the W4A16 GEMM's reduce writes, so the
+// partials need no separate pass; the same bits.  For d <= 4 * 4 * kNormNT
+// (4 vectors per thread) every load -- the partials, h and the weights -- is
+// issued before the first use and h stays in registers for the output.
+template <int S>
+__global__ __launch_bounds__(kNormNT) void rmsnorm_part_kernel(uint16_t *h, const float *part,
+                                                               const uint16_t *w, uint16_t *out,
+                                                               int d, float eps, long long slab,
+                                                               int splits) {
+  constexpr int kV = 4;
+  const long long row = blockIdx.x;
+  uint2 *hr = reinterpret_cast<uint2 *>(h + row * d);
+  const float *pr = part + row * d;
+  uint2 *orow = reinterpret_cast<uint2 *>(out + row * d);
+  const uint2 *wr = reinterpret_cast<const uint2 *>(w);
+  const int nvec = d / 4;
+  float ss = 0.0f;
+  if (nvec <= kV * kNormNT) {
+    float4 p[kV];
+    uint2 x[kV], g[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {  // clamped: every load issued and in bounds
+      const int c = min((int)threadIdx.x + k * kNormNT, nvec - 1);
+      p[k] = slab_sum4<S>(pr + 4 * c, slab, splits);
+      x[k] = hr[c];
+      g[k] = wr[c];
+    }
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const int v = threadIdx.x + k * kNormNT;
+      if (v < nvec) {
+        norm_fold_part(x[k], p[k], ss);
+        hr[v] = x[k];
+        norm_sq(x[k], ss);
+      }
+    }
+    const float inv = norm_inv(ss, d, eps);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const int v = threadIdx.x + k * kNormNT;
+      if (v < nvec) orow[v] = norm_scale(x[k], g[k], inv);
+    }
+    return;
+  }
+  for (int v = threadIdx.x; v < nvec; v += kNormNT) {
+    uint2 x = hr[v];
+    norm_fold_part(x, slab_sum4<S>(pr + 4 * v, slab, splits), ss);
+    hr[v] = x;
+    norm_sq(x, ss);
+  }
+  const float inv = norm_inv(ss, d, eps);
+  for (int v = threadIdx.x; v < nvec; v += kNormNT) orow[v] = norm_scale(hr[v], wr[v], inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -146,18 +214,11 @@ struct RopeArgs {
 
 // bf16 bits of elements idx .. idx + P - 1 of the fused projection (P = 4:
 // one 8-byte bf16 load, or one 16-byte load per fp32 slab)
-template <int P>
+template <int P, int S>
 __device__ __forceinline__ void qkv_load(const RopeArgs &a, long long idx, uint16_t (&v)[P]) {
   if constexpr (P == 4) {
     if (a.part) {
-      float4 s = *reinterpret_cast<const float4 *>(a.part + idx);
-      for (int sp = 1; sp < a.splits; ++sp) {
-        const float4 t = *reinterpret_cast<const float4 *>(a.part + sp * a.slab + idx);
-        s.x += t.x;
-        s.y += t.y;
-        s.z += t.z;
-        s.w += t.w;
-      }
+      const float4 s = slab_sum4<S>(a.part + idx, a.slab, a.splits);
       v[0] = f2bf(s.x);
       v[1] = f2bf(s.y);
       v[2] = f2bf(s.z);
@@ -198,7 +259,7 @@ __device__ __forceinline__ void store_p(uint16_t *dst, const uint16_t (&v)[P]) {
 // One thread per (token, head, P consecutive rotation pairs), or per P
 // consecutive v elements; P = 4 when D / 2 % 4 == 0 and the buffers are
 // 16-byte aligned, else 1.  Every element is computed the same way for both P.
-template <int P>
+template <int P, int S>
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
   const int half = a.D / 2, hp = half / P, dp = a.D / P;
   const int H = a.Hq + 2 * a.Hkv;
@@ -212,7 +273,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
     const int h = (int)((r / dp) % a.Hkv);
     const int m = (int)(r / ((long long)dp * a.Hkv));
     uint16_t val[P];
-    qkv_load<P>(a, ((long long)m * H + a.Hq + a.Hkv + h) * a.D + e0, val);
+    qkv_load<P, S>(a, ((long long)m * H + a.Hq + a.Hkv + h) * a.D + e0, val);
     const int b = m / a.n, j = m % a.n;
     if (a.kind == 0) {
       const int slot = a.base[b] + j;
@@ -233,8 +294,8 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
   const int m = (int)(t / ((long long)hp * (a.Hq + a.Hkv)));
   const long long src = ((long long)m * H + hh) * a.D;
   uint16_t lo[P], hi[P], y0[P], y1[P];
-  qkv_load<P>(a, src + i0, lo);
-  qkv_load<P>(a, src + i0 + half, hi);
+  qkv_load<P, S>(a, src + i0, lo);
+  qkv_load<P, S>(a, src + i0 + half, hi);
 #pragma unroll
   for (int k = 0; k < P; ++k) {
     const int i = i0 + k;
@@ -284,12 +345,15 @@ static int launch_rope(const RopeArgs &a, void *stream) {
   const int P = (a.D % 8 == 0 && aligned) ? 4 : 1;
   const long long total =
       (long long)a.M * (a.Hq + a.Hkv) * (a.D / 2 / P) + (long long)a.M * a.Hkv * (a.D / P);
-  if (P == 4)
-    CFA_LAUNCH("rope_kv", rope_kv_kernel<4>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-               (hipStream_t)stream, a);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  // the 8B target's QKV projection splits K five ways: its partial sums get
+  // a compile-time slab count (every load in flight at once)
+  if (P == 4 && a.part && a.splits == 5)
+    CFA_LAUNCH("rope_kv", (rope_kv_kernel<4, 5>), grid, dim3(256), 0, (hipStream_t)stream, a);
+  else if (P == 4)
+    CFA_LAUNCH("rope_kv", (rope_kv_kernel<4, 0>), grid, dim3(256), 0, (hipStream_t)stream, a);
   else
-    CFA_LAUNCH("rope_kv", rope_kv_kernel<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-               (hipStream_t)stream, a);
+    CFA_LAUNCH("rope_kv", (rope_kv_kernel<1, 0>), grid, dim3(256), 0, (hipStream_t)stream, a);
   return CFA_OK;
 }
 
@@ -337,7 +401,7 @@ extern "C" int cfa_rmsnorm(void *h, const void *delta, const void *weight, void 
     return fail_arg("rows must be 16-byte aligned");
   CFA_LAUNCH("rmsnorm", rmsnorm_kernel, dim3(M), dim3(kNormNT), 0, (hipStream_t)stream,
              (uint16_t *)h, (const uint16_t *)delta, (const uint16_t *)weight, (uint16_t *)out, d,
-             eps, (const float *)nullptr, 0, 0LL);
+             eps);
   return CFA_OK;
 }
 
@@ -350,9 +414,19 @@ extern "C" int cfa_rmsnorm_partials(void *h, const float *part, int splits, cons
   if (!h || !part || !weight || !out) return fail_arg("null pointer");
   if ((((uintptr_t)h | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)part) & 15) != 0)
     return fail_arg("rows must be 16-byte aligned");
-  CFA_LAUNCH("rmsnorm", rmsnorm_kernel, dim3(M), dim3(kNormNT), 0, (hipStream_t)stream,
-             (uint16_t *)h, (const uint16_t *)nullptr, (const uint16_t *)weight, (uint16_t *)out,
-             d, eps, part, splits, (long long)M * d);
+  const long long slab = (long long)M * d;
+#define CFA_NORM_PART(S)                                                                     \
+  CFA_LAUNCH("rmsnorm", rmsnorm_part_kernel<S>, dim3(M), dim3(kNormNT), 0, (hipStream_t)stream, \
+             (uint16_t *)h, part, (const uint16_t *)weight, (uint16_t *)out, d, eps, slab, splits)
+  switch (splits) {
+    case 1: CFA_NORM_PART(1); break;
+    case 2: CFA_NORM_PART(2); break;
+    case 4: CFA_NORM_PART(4); break;
+    case 5: CFA_NORM_PART(5); break;
+    case 8: CFA_NORM_PART(8); break;
+    default: CFA_NORM_PART(0); break;
+  }
+#undef CFA_NORM_PART
   return CFA_OK;
 }
 

@@ -208,12 +208,12 @@ def test_gemm_zp_silu_bit_exact(device, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(504, 4096, 4096), (504, 4096, 14336), (600, 768, 1024),
-                                   (37, 256, 512), (1, 256, 128)])
+                                   (37, 256, 512), (16, 256, 768), (1, 256, 128)])
 def test_gemm_zp_partials_rmsnorm_bit_exact(device, M, N, K):
     """The GEMM's split-K partials summed by cfa_rmsnorm_partials give the
     bits of cfa_w4a16_gemm_zp followed by cfa_rmsnorm (residual h and the
-    normalised output), with 8, 4 and 1 split(s) -- one split forced to
-    fp32 partials as well."""
+    normalised output), with 8, 4, 2, 3 (a count the kernel takes at run
+    time) and 1 split(s) -- one split forced to fp32 partials as well."""
     from cudaforge_amd import _lib
     from cudaforge_amd.spec_step import add_norm_, rmsnorm_
     from cudaforge_amd.w4a16 import w4a16_gemm_zp, w4a16_gemm_zp_partials
