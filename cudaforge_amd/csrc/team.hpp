@@ -33,17 +33,16 @@ namespace cfa {
 namespace team {
 
 constexpr int kMaxG = 8;
-constexpr int kKinds = 4;               // exchange kinds (each double-buffered)
 constexpr long kSpinLimit = 1l << 22;   // about 0.2-0.5 s of polling
 
 // One team's global state (part of the caller's workspace, zero before the
 // launch).
 struct alignas(256) State {
-  unsigned cnt;                                 // cumulative barrier arrivals
-  unsigned pad0[63];
   unsigned long long hand[2 * (kMaxG + 1)];     // exact-pass handoffs: (tag, value), (tag, hit)
   unsigned long long pad1[32 - 2 * (kMaxG + 1)];
-  uint4 xch[kMaxG][2 * kKinds];                 // published per-member values
+  // exchanged per-member values: four words (tag << 32 | value) per member,
+  // in the buffer of the exchange tag's parity
+  unsigned long long xw[kMaxG][2][4];
 };
 
 // LDS a team member needs besides seq::Shared.
@@ -57,7 +56,7 @@ struct Team {
   State *st;
   int *err;      // device-wide error flag
   int m, G;      // member index, members
-  unsigned nb;   // barriers passed (identical in every member)
+  unsigned nb;   // exchanges done (identical in every member; tags the exchange words)
   unsigned pass; // exact passes run (tags the handoff words)
 };
 
@@ -80,39 +79,49 @@ __device__ __forceinline__ void set_error(int *err) {
   __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Team barrier (every thread of every member calls it).
-__device__ void sync(Team &t, Lds &l) {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  ++t.nb;
-  if (threadIdx.x == 0 && !l.failed) {
-    __hip_atomic_fetch_add(&t.st->cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned target = t.nb * (unsigned)t.G;
+// Exchange of one 16-byte value per member, which is also the team's
+// barrier (every thread of every member calls it): thread 0 writes v as
+// four words (tag << 32 | value) into this member's buffer of the tag's
+// parity; thread j < G polls member j's four words until all carry the tag
+// (a bounded wait: one that runs out sets the error flag and yields zeros),
+// so l.got[j][0] = member j's value.  One round trip, where a barrier
+// counter and a separate read of published values took two.  A buffer is
+// written again two exchanges later: by then every member has published the
+// exchange in between, which it does only after reading this one.
+__device__ void exchange(Team &t, Lds &l, uint4 v) {
+  const unsigned tag = ++t.nb;  // the workspace starts at zero: 0 is never a tag
+  __syncthreads();              // every thread is done with the previous exchange's l.got
+  if (threadIdx.x == 0) {
+    unsigned long long *mine = &t.st->xw[t.m][tag & 1u][0];
+    const unsigned long long hi = (unsigned long long)tag << 32;
+    st64(mine, hi | v.x);
+    st64(mine + 1, hi | v.y);
+    st64(mine + 2, hi | v.z);
+    st64(mine + 3, hi | v.w);
+  }
+  if (threadIdx.x < t.G) {
+    unsigned long long *p = &t.st->xw[threadIdx.x][tag & 1u][0];
+    unsigned long long w0 = 0, w1 = 0, w2 = 0, w3 = 0;
     long spins = 0;
-    while (ld32(&t.st->cnt) < target) {
-      if (++spins > kSpinLimit || error_set(t.err)) {
+    for (;;) {
+      w0 = ld64(p);
+      w1 = ld64(p + 1);
+      w2 = ld64(p + 2);
+      w3 = ld64(p + 3);
+      if ((unsigned)(w0 >> 32) == tag && (unsigned)(w1 >> 32) == tag &&
+          (unsigned)(w2 >> 32) == tag && (unsigned)(w3 >> 32) == tag)
+        break;
+      if (l.failed || ++spins > kSpinLimit || error_set(t.err)) {
         l.failed = 1;
         set_error(t.err);
+        w0 = w1 = w2 = w3 = 0;
         break;
       }
       __builtin_amdgcn_s_sleep(1);
     }
+    l.got[threadIdx.x][0] = make_uint4((uint32_t)w0, (uint32_t)w1, (uint32_t)w2, (uint32_t)w3);
   }
   __syncthreads();
-}
-
-// Thread 0 publishes v as this member's value of exchange `kind`, before
-// the sync that makes it readable.  The two buffers of a kind alternate with
-// the parity of the barrier count: a buffer is written again only two syncs
-// later, after every member has passed the sync that follows its reads.
-__device__ __forceinline__ void publish(Team &t, int kind, uint4 v) {
-  if (threadIdx.x == 0) {
-    unsigned *p = reinterpret_cast<unsigned *>(&t.st->xch[t.m][2 * kind + (t.nb & 1u)]);
-    st32(p, v.x);
-    st32(p + 1, v.y);
-    st32(p + 2, v.z);
-    st32(p + 3, v.w);
-  }
 }
 __device__ __forceinline__ uint4 f4u(float4 v) {
   return make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
@@ -121,19 +130,6 @@ __device__ __forceinline__ uint4 f4u(float4 v) {
 __device__ __forceinline__ float4 u4f(uint4 v) {
   return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
                      __uint_as_float(v.w));
-}
-
-// Right after the sync that follows publish(): l.got[j][k] = member j's
-// value of exchange kind0 (k = 0) / kind1 (k = 1); ends with a work-group
-// barrier.
-__device__ void fetch(Team &t, Lds &l, int kind0, int kind1) {
-  if (threadIdx.x < 2 * t.G) {
-    const int j = threadIdx.x >> 1, k = threadIdx.x & 1;
-    const int slot = 2 * (k ? kind1 : kind0) + ((t.nb - 1u) & 1u);
-    unsigned *p = reinterpret_cast<unsigned *>(&t.st->xch[j][slot]);
-    l.got[j][k] = make_uint4(ld32(p), ld32(p + 1), ld32(p + 2), ld32(p + 3));
-  }
-  __syncthreads();
 }
 
 // Handoff k of pass `tag`: the exact value after segment k - 1 and the CDF
@@ -317,9 +313,7 @@ __device__ __attribute__((noinline)) float team_seq(Team &tm, Lds &tl, const XF 
     for (int q = 0; q < Shared<NT>::kWaves; ++q) T += sh.wscan[q];
     __syncthreads();
   }
-  publish(tm, 0, make_uint4(f2u(T), 0u, 0u, 0u));
-  sync(tm, tl);
-  fetch(tm, tl, 0, 0);
+  exchange(tm, tl, make_uint4(f2u(T), 0u, 0u, 0u));
   float E = 0.0f;
   for (int j = 0; j < tm.m; ++j) E += u2f(tl.got[j][0].x);
   if (!cdf) {
@@ -359,9 +353,7 @@ __device__ __attribute__((noinline)) float team_seq(Team &tm, Lds &tl, const XF 
     tl.got[0][1] = make_uint4(F.e, F.o, (uint32_t)reg, valid ? 1u : 0u);  // scratch
   }
   __syncthreads();
-  publish(tm, 1, tl.got[0][1]);
-  sync(tm, tl);
-  fetch(tm, tl, 1, 1);
+  exchange(tm, tl, tl.got[0][1]);
 
   // C: walk the segments from the exact running value
   float s = 0.0f;

@@ -272,9 +272,7 @@ __device__ void team_stats(const Args &a, team::Team &tm, Smem &sm, const float 
   long long lo, hi;
   slice(a, tm, lo, hi);
   const float4 p = slice_ms2(a, t, d, lo, hi, sm);
-  team::publish(tm, 2, team::f4u(p));
-  team::sync(tm, sm.tl);
-  team::fetch(tm, sm.tl, 2, 2);
+  team::exchange(tm, sm.tl, team::f4u(p));
   if (threadIdx.x == 0) {
     float4 acc = team::u4f(sm.tl.got[0][0]);
     for (int j = 1; j < tm.G; ++j) {
@@ -348,9 +346,7 @@ __device__ int team_argmax(const Args &a, team::Team &tm, Smem &sm, const Dist &
     sm.red[3][0] = __int_as_float(ix);
   }
   __syncthreads();
-  team::publish(tm, 3, make_uint4(__float_as_uint(sm.red[2][0]), __float_as_uint(sm.red[3][0]), 0u, 0u));
-  team::sync(tm, sm.tl);
-  team::fetch(tm, sm.tl, 3, 3);
+  team::exchange(tm, sm.tl, make_uint4(__float_as_uint(sm.red[2][0]), __float_as_uint(sm.red[3][0]), 0u, 0u));
   if (tid == 0) {
     float v = __uint_as_float(sm.tl.got[0][0].x);
     int ix = (int)sm.tl.got[0][0].y;
