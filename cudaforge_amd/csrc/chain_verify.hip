@@ -1080,17 +1080,26 @@ __device__ float mw_lookback(const Args &a, int b, int c, float own) {
   return pre;
 }
 
-// The first exact pass, with the chunk sums: one wave per chunk (chunk c =
-// 4 * blockIdx.x + wave of job blockIdx.y, lane = tile in the chunk).  With
-// `decide` (cpp rules) every work-group first takes sequence b's decision
-// itself (decide_cpp: the same inputs, so the same job everywhere) and the
-// first one stores it.  Every active job stores its chunk sums of t (the CDF
-// pass of a plain draw, or of the fallback, starts from them); a residual
-// job also stores those of max(0, t - d), finds its chunk's entry value by
-// look-back, and writes the sum pass's records (mw_records_chunk).
+// Chunks per wave of mw_first_kernel: two, so that the launch has B * NC / 2
+// waves (4032 at C2) and every wave is resident from the start -- with one
+// chunk per wave (8064 waves, against about 7 resident per SIMD) the last
+// eight sequences' work-groups started 12 us late, after the first ones
+// ended (36.1 -> 29.4 us at C2).
+constexpr int kMwCPW = 2;
+constexpr int kMwChunksPerWG = (kMwNT / 64) * kMwCPW;
+
+// The first exact pass, with the chunk sums: each wave takes chunks c0 and
+// c0 + 1 (c0 = 2 (4 blockIdx.x + wave)) of job blockIdx.y, lane = tile in the
+// chunk.  With `decide` (cpp rules) every work-group first takes sequence
+// b's decision itself (decide_cpp: the same inputs, so the same job
+// everywhere) and the first one stores it.  Every active job stores its
+// chunk sums of t (the CDF pass of a plain draw, or of the fallback, starts
+// from them); a residual job also stores those of max(0, t - d), finds its
+// chunks' entry values by look-back (both chunks' own sums published first),
+// and writes the sum pass's records (mw_records_chunk).
 __global__ __launch_bounds__(kMwNT) void mw_first_kernel(Args a, int decide) {
   const int b = blockIdx.y, lane = threadIdx.x & 63;
-  const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
+  const int c0 = kMwCPW * (blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6));
   MwJob j;
   if (decide) {
     __shared__ DecideLds L;
@@ -1110,38 +1119,57 @@ __global__ __launch_bounds__(kMwNT) void mw_first_kernel(Args a, int decide) {
     j = a.jobs[b];
   }
   if (j.kind != kResid && j.kind != kPlain) return;
-  if (c >= a.NC) return;
+  if (c0 >= a.NC) return;
+  const bool two = c0 + 1 < a.NC;
   const bool resid = j.kind == kResid;
   const MwElem e = mw_elem(a, b, j, kPassSum);
-  const long long tile = (long long)c * kMwChunkTiles + lane, i0 = tile * kMwTile;
-  float tv[kMwTile], dv[kMwTile], x[kMwTile];
-  mw_load16(a, e.t.p, i0, tv);
-  if (resid) mw_load16(a, e.d.p, i0, dv);
-  float st = 0.0f, sx = 0.0f;
+  float tv[kMwCPW][kMwTile], dv[kMwCPW][kMwTile], x[kMwCPW][kMwTile];
+  // both chunks' loads before any use
 #pragma unroll
-  for (int k = 0; k < kMwTile; ++k) {
-    x[k] = 0.0f;
-    if (i0 + k < a.V) {
-      const float tp = e.t.eval(tv[k]);
-      st += tp;
-      if (resid) {
-        x[k] = relu_ref(tp - e.d.eval(dv[k]));
-        sx += x[k];
+  for (int h = 0; h < kMwCPW; ++h) {
+    const long long i0 = ((long long)(c0 + (two ? h : 0)) * kMwChunkTiles + lane) * kMwTile;
+    mw_load16(a, e.t.p, i0, tv[h]);
+    if (resid) mw_load16(a, e.d.p, i0, dv[h]);
+  }
+  float sx[kMwCPW];
+#pragma unroll
+  for (int h = 0; h < kMwCPW; ++h) {
+    const long long i0 = ((long long)(c0 + h) * kMwChunkTiles + lane) * kMwTile;
+    float st = 0.0f, sxh = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMwTile; ++k) {
+      x[h][k] = 0.0f;
+      if (i0 + k < a.V) {
+        const float tp = e.t.eval(tv[h][k]);
+        st += tp;
+        if (resid) {
+          x[h][k] = relu_ref(tp - e.d.eval(dv[h][k]));
+          sxh += x[h][k];
+        }
       }
     }
-  }
-  st = wave_sum_f32(st);
-  sx = wave_sum_f32(sx);
-  if (lane == 0) {
-    a.csum_t[(long long)b * a.NC + c] = st;
-    a.csum_x[(long long)b * a.NC + c] = sx;
+    st = wave_sum_f32(st);
+    sx[h] = wave_sum_f32(sxh);
+    if (lane == 0 && (h == 0 || two)) {
+      a.csum_t[(long long)b * a.NC + c0 + h] = st;
+      a.csum_x[(long long)b * a.NC + c0 + h] = sx[h];
+    }
   }
   if (!resid) return;
-  const float E0 = mw_lookback(a, b, c, sx);
-  mw_records_chunk(a, b, c, kPassSum, j, E0, x);
+  unsigned long long *fl = a.flags + (long long)b * a.NC;
+  if (two && lane == 0) lb_store(fl + c0 + 1, kLbAgg | f2u(sx[1]));  // before c0's look-back
+  const float E0 = mw_lookback(a, b, c0, sx[0]);
+  mw_records_chunk(a, b, c0, kPassSum, j, E0, x[0]);
+  if (!two) return;
+  const float E1 = E0 + sx[0];
+  if (lane == 0) lb_store(fl + c0 + 1, kLbIncl | f2u(E1 + sx[1]));
+  mw_records_chunk(a, b, c0 + 1, kPassSum, j, E1, x[1]);
 }
 
 // One wave per chunk: chunk c = 4 * blockIdx.x + wave of job blockIdx.y.
+// (Two chunks per wave, as mw_first_kernel, made this pass slower: 18.4 ->
+// 21.7 us at C2; its waves are short, so the tail of late work-groups costs
+// less than a serial second chunk.)
 __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
   const int b = blockIdx.y;
   const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
@@ -1886,9 +1914,10 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   const int fused_decide = mode == CFA_MODE_CPP ? 1 : 0;
   if (!fused_decide) CFA_LAUNCH("chain_decide", decide_kernel, dim3(B), dim3(64), 0, st, a);
   if (mode != CFA_MODE_GREEDY) {
-    const dim3 cg((a.NC + kMwNT / 64 - 1) / (kMwNT / 64), B);
+    const dim3 cg1((a.NC + kMwChunksPerWG - 1) / kMwChunksPerWG, B);   // two chunks per wave
+    const dim3 cg((a.NC + kMwNT / 64 - 1) / (kMwNT / 64), B);              // one chunk per wave
     if (mode == CFA_MODE_PYTHON) CFA_LAUNCH("chain_plan", plan_kernel, dim3(1), dim3(256), 0, st, a);
-    CFA_LAUNCH("chain_mw_first", mw_first_kernel, cg, dim3(kMwNT), 0, st, a, fused_decide);
+    CFA_LAUNCH("chain_mw_first", mw_first_kernel, cg1, dim3(kMwNT), 0, st, a, fused_decide);
     CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassSum);
     CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassCdf);
     CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassCdf);
