@@ -298,8 +298,20 @@ def tree_attention_leg(dev, reps=20):
         run()
     ms = _time_launches(run, reps, ("tree_attn", "tree_attn_merge"))
     t = (ms["tree_attn"] + ms["tree_attn_merge"]) * 1e-3
+    # the whole call on its stream, back to back (adds the dispatch gap
+    # between the two kernels and between calls)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t_call = e0.elapsed_time(e1) / reps * 1e-3
     return {"config": "B=16,N=63 binary tree,Hq=32,Hkv=8,d=128,ctx=4096,page=16 (BASELINE configs[2])",
             "us": round(t * 1e6, 2), "kernels_us": {k: round(v * 1e3, 2) for k, v in ms.items()},
+            "call_us": round(t_call * 1e6, 2),
             "flop": flops, "tflops": round(flops / t / 1e12, 1),
             "mfma_frac": round(flops / t / MFMA_BF16_PEAK, 4),
             "bytes": nbytes, "gbs": round(nbytes / t / 1e9, 1),
