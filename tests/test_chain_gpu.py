@@ -122,7 +122,7 @@ def _softmax64(x, T):
 
 @pytest.mark.parametrize("mode", ["cpp", "python", "greedy"])
 @pytest.mark.parametrize("B,K,V", [(64, 8, 128256), (5, 3, 1001), (3, 0, 257), (2, 2, 1),
-                                   (7, 1, 4096)])
+                                   (7, 1, 4096), (9, 5, 5001)])
 def test_logits_path_matches_oracle(device, mode, B, K, V):
     T = 0.7
     tl, dl, tok, U = c2_inputs(seed=B * 1000 + K * 10 + V % 97, B=B, K=K, V=V, temperature=T)
