@@ -1171,8 +1171,11 @@ __global__ __launch_bounds__(kMwNT) void mw_first_kernel(Args a, int decide) {
 // 21.7 us at C2; its waves are short, so the tail of late work-groups costs
 // less than a serial second chunk.)
 __global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
-  const int b = blockIdx.y;
-  const int c = blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6);
+  // sequences vary fastest: the work-groups that start last, once the first
+  // ones end, hold the chunks nearest the row's end, which lie past the CDF
+  // hit (skipped at once) for most sequences
+  const int b = blockIdx.x;
+  const int c = blockIdx.y * (kMwNT / 64) + (threadIdx.x >> 6);
   const MwJob j = a.jobs[b];
   if (!mw_active(j, pass)) return;
   if (c >= a.NC) return;
@@ -1915,7 +1918,7 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   if (!fused_decide) CFA_LAUNCH("chain_decide", decide_kernel, dim3(B), dim3(64), 0, st, a);
   if (mode != CFA_MODE_GREEDY) {
     const dim3 cg1((a.NC + kMwChunksPerWG - 1) / kMwChunksPerWG, B);   // two chunks per wave
-    const dim3 cg((a.NC + kMwNT / 64 - 1) / (kMwNT / 64), B);              // one chunk per wave
+    const dim3 cg(B, (a.NC + kMwNT / 64 - 1) / (kMwNT / 64));              // one chunk per wave
     if (mode == CFA_MODE_PYTHON) CFA_LAUNCH("chain_plan", plan_kernel, dim3(1), dim3(256), 0, st, a);
     CFA_LAUNCH("chain_mw_first", mw_first_kernel, cg1, dim3(kMwNT), 0, st, a, fused_decide);
     CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassSum);
