@@ -139,3 +139,42 @@ def test_skinny_gemm_workspace_size():
     assert lib.cfa_gemm_bf16_skinny_workspace_size(8, 3072, 2048, 4) == 65536 + 48 * 4 * 4096
     assert lib.cfa_gemm_bf16_skinny_workspace_size(100, 2048, 8192, 8) == 65536 + 32 * 8 * 32 * 1024
     assert lib.cfa_gemm_bf16_skinny_workspace_size(129, 64, 128, 1) == 0
+
+
+def test_w4a16_split_counts():
+    """Split-K counts of the fused W4A16 GEMM (one work-group per CU; the
+    host without a GPU assumes 256 CUs): the verify step's target shapes at
+    M = 504, and 0 for shapes the kernel does not take."""
+    lib = _lib.load()
+    assert lib.cfa_w4a16_gemm_zp_splits(504, 28672, 4096) == 1     # gate/up: 224 tiles
+    assert lib.cfa_w4a16_gemm_zp_splits(504, 6144, 4096) == 5      # QKV: 48 tiles
+    assert lib.cfa_w4a16_gemm_zp_splits(504, 4096, 4096) == 8      # O
+    assert lib.cfa_w4a16_gemm_zp_splits(504, 4096, 14336) == 8     # down
+    assert lib.cfa_w4a16_gemm_zp_splits(1, 256, 128) == 1
+    assert lib.cfa_w4a16_gemm_zp_splits(504, 4100, 4096) == 0
+    assert lib.cfa_w4a16_gemm_zp_splits(0, 256, 128) == 0
+    # the workspace of the reducing entry point is the same partials
+    assert lib.cfa_w4a16_gemm_zp_workspace_size(504, 4096, 4096) == 8 * 504 * 4096 * 4
+
+
+def test_fused_layer_argument_errors():
+    """The partial-summing and SiLU-gated entry points validate before any
+    device work (dummy pointers)."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    rc = lib.cfa_w4a16_gemm_zp_partials(p, p, p, None, 504, 4100, 4096, 128, p, 1 << 30, None)
+    assert rc == _lib.CFA_ERR_ARG and "multiple of 256" in _lib.last_error()
+    rc = lib.cfa_w4a16_gemm_zp_partials(p, p, p, None, 504, 4096, 4096, 128, p, 1024, None)
+    assert rc == _lib.CFA_ERR_ARG and "part too small" in _lib.last_error()
+    rc = lib.cfa_w4a16_gemm_zp_silu(p, p, p, None, 504, 4096, 4000, 128, p, p, 1 << 30, None)
+    assert rc == _lib.CFA_ERR_ARG and "multiple of 32" in _lib.last_error()
+    rc = lib.cfa_rmsnorm_partials(p, p, 0, p, p, 504, 4096, 1e-5, None)
+    assert rc == _lib.CFA_ERR_ARG and "splits" in _lib.last_error()
+    rc = lib.cfa_rmsnorm_partials(p, None, 8, p, p, 504, 4096, 1e-5, None)
+    assert rc == _lib.CFA_ERR_ARG and "null" in _lib.last_error()
+    rc = lib.cfa_rope_kv_paged_partials(None, 5, p, 8, 63, 32, 8, 128, 5e5, p, p, p, 0, 32, 16,
+                                        p, 200, p, None)
+    assert rc == _lib.CFA_ERR_ARG and "null" in _lib.last_error()
+    rc = lib.cfa_rope_kv_paged_partials(p, 0, p, 8, 63, 32, 8, 128, 5e5, p, p, p, 0, 32, 16,
+                                        p, 200, p, None)
+    assert rc == _lib.CFA_ERR_ARG and "splits" in _lib.last_error()
