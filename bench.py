@@ -356,6 +356,7 @@ def tree_accept_commit_leg(dev, reps=10):
     for _ in range(2):
         run()
     torch.cuda.synchronize()
+    res["tv"].check_status()  # a failed walk's paths are not valid (RuntimeError)
     plen = res["tv"].path_len.cpu().numpy()
     path = res["tv"].path.cpu().numpy()
     emitted = int(res["tv"].num_emitted.sum())
@@ -364,6 +365,7 @@ def tree_accept_commit_leg(dev, reps=10):
     moved = int(sum(sum(1 for j in range(int(plen[b])) if path[b, j] != j) for b in range(Bt)))
     alg_commit = moved * 2 * (L * Hkv * D * 2 * 2)  # read + write of K and V rows
     ms = _time_launches(run, reps, ("tree_verify", "kv_commit"))
+    res["tv"].check_status()
     t_acc, t_com = ms["tree_verify"] * 1e-3, ms["kv_commit"] * 1e-3
     return {"config": "B=32,63-node binary tree,V=128256,T=0.7; commit 32L x 8H x 128 bf16 "
                       "(BASELINE configs[3])",

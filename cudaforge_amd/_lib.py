@@ -100,6 +100,9 @@ class KVPageCopyC(ctypes.Structure):
                 ("n_slots", ctypes.c_int32)]
 
 
+# The ABI these signatures describe (CFA_ABI_VERSION of include/cudaforge_amd.h).
+ABI_VERSION = 200
+
 # name -> (restype, argtypes); every symbol the header declares.
 SIGNATURES: dict[str, tuple] = {
     "cfa_last_error": (ctypes.c_char_p, []),
@@ -197,6 +200,10 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
+            if lib.cfa_version() // 100 != ABI_VERSION // 100:
+                raise RuntimeError(
+                    f"{LIB_PATH} has ABI version {lib.cfa_version()}, these bindings need "
+                    f"{ABI_VERSION}: rebuild with `python -m cudaforge_amd._build`")
             _lib = lib
     return _lib
 

@@ -52,7 +52,7 @@ int device_cu_count() {
 
 extern "C" const char *cfa_last_error(void) { return cfa::abi::g_last_error.c_str(); }
 
-extern "C" int cfa_version(void) { return 100; }
+extern "C" int cfa_version(void) { return CFA_ABI_VERSION; }
 
 // ---------------------------------------------------------------------------
 // Host uniform stream (speculative.cpp:8-9, 13-14, 64, 72).

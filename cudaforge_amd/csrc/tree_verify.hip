@@ -30,6 +30,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 
@@ -560,19 +561,20 @@ inline Plan plan(int B, int cus, int per_cu) {
 using namespace cfa;
 
 namespace {
-// Work-groups of the tree kernel one CU holds, per device (queried once).
+// Work-groups of the tree kernel one CU holds, per device (queried once;
+// threads that race on the first query store the same value).
 int kernel_per_cu() {
-  static int cache[64];
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)treev::tree_verify_kernel,
                                                      treev::kNT, 0) != hipSuccess || n < 1)
       n = 1;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 constexpr size_t kErrBytes = 256;
 

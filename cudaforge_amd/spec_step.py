@@ -42,8 +42,8 @@ from . import _lib
 from . import tree as T
 from .kv_cache import KVCacheConfig, PagedKVCache
 from .sampling import expand_tree_level
-from .verify import (_stream_ptr, kv_commit, tree_attention, tree_attention_workspace_bytes,
-                     tree_verify)
+from .verify import (_stream_ptr, check_status, kv_commit, tree_attention,
+                     tree_attention_workspace_bytes, tree_verify)
 from .w4a16 import W4A16Linear
 
 __all__ = ["LlamaShape", "TARGET_8B", "DRAFT_1B", "TargetModel", "DraftModel", "TreeSpeculator",
@@ -432,6 +432,9 @@ class TreeSpeculator:
         self.N = 2 ** (depth + 1) - 1
         if self.N > 64:
             raise ValueError("a tree has at most 64 nodes")
+        # uniforms per sequence and step: the walk draws one per tested child
+        # (at most 2 per level) and one final draw, 2 * depth + 1 in all
+        self.n_uniforms = 2 * 2 * depth + 2
         self.parents_np = T.binary_tree_parents(self.N)
         self.parents = torch.from_numpy(self.parents_np).to(dev)
         self.depths = torch.from_numpy(T.depths(self.parents_np)).to(dev)
@@ -535,11 +538,18 @@ class TreeSpeculator:
         logits = self.t.forward_tree(tokens, pos, self.kv, desc.block_tables, base, self.masks,
                                      max_keys)
         mark()
-        n_u = 2 * 2 * self.depth + 2
-        u = 1.0 - torch.rand(B, n_u, device=dev, generator=self.gen)
+        u = 1.0 - torch.rand(B, self.n_uniforms, device=dev, generator=self.gen)
         res = tree_verify(logits, self.draft_rows, self.parents, tokens, u, input_kind="logits",
                           temperature=self.T, mode=self.mode)
         mark()
+        try:
+            check_status(res.status)
+        except RuntimeError:
+            # nothing is committed: the appended tree slots are released and
+            # the context, root and both caches stay as they were
+            for b in range(B):
+                self.kv.truncate_sequence(b, self.ctx[b])
+            raise
         new_lens = self.kv.commit_tree_paths(list(range(B)), desc, base, res.path, res.path_len)
         plen = [n - c for n, c in zip(new_lens, self.ctx)]
         self.d.commit(base, res.path, res.path_len)

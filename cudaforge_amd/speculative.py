@@ -31,7 +31,11 @@ Reference behaviour kept: ``num_accepted`` counts the resampled or bonus token
 (:184, :195) and ``acceptance_rate = num_accepted / K`` can exceed 1; a
 rejection at the last draft position (i = K-1) brings num_accepted to K, so
 the ``num_accepted == self.k`` branch (:188) appends a bonus token as well
-(K+1 tokens, rate (K+1)/K); K = 0 raises ``ZeroDivisionError`` (:202).
+(K+1 tokens, rate (K+1)/K).  K = 0 fails where the reference fails: the
+``torch.cat`` of the empty draft list (:128) raises ``ValueError`` before the
+target runs, and the lifetime totals are left unchanged.  An empty batch
+accepts all K drafts and the bonus, as the reference's ``.all()`` over no
+rows does (:166): ``accepted_tokens`` is [0, K+1].
 
 ``verify_mode="python"`` (default) keeps the reference's batch lock-step rule
 (one accept count n for the whole batch, :166).  ``verify_mode="cpp"`` applies
@@ -102,6 +106,10 @@ class SpeculativeEngine:
     def _rand(self, *shape: int, device: torch.device) -> torch.Tensor:
         return torch.rand(*shape, device=device, dtype=torch.float32, generator=self.generator)
 
+    def _draw_draft(self, probs: torch.Tensor) -> torch.Tensor:
+        """One draft token per row from the draft softmax (speculative.py:119)."""
+        return torch.multinomial(probs, num_samples=1, generator=self.generator)
+
     @torch.no_grad()
     def _sample_next_token(
         self,
@@ -117,6 +125,8 @@ class SpeculativeEngine:
         if logits.dim() != 2:
             raise ValueError("logits must be [B, V]")
         B = logits.shape[0]
+        if B == 0:
+            return torch.empty(0, 1, dtype=torch.long, device=logits.device)
         x = logits.float().contiguous().unsqueeze(1)
         u = self._rand(B, 2, device=logits.device)
         tok = torch.empty(B, 0, dtype=torch.int32, device=logits.device)
@@ -145,18 +155,16 @@ class SpeculativeEngine:
             draft_logits = self.draft_runner.forward(draft_input_ids, kv_cache_handles)
             next_logits = draft_logits[:, -1, :].float()
             probs = F.softmax(next_logits / self.temperature, dim=-1)
-            next_token = torch.multinomial(probs, num_samples=1, generator=self.generator)
+            next_token = self._draw_draft(probs)
             draft_tokens_list.append(next_token)
             draft_logits_list.append(next_logits)
             draft_input_ids = torch.cat([draft_input_ids, next_token], dim=-1)
         _sync(device)
         t_draft_ms = (time.perf_counter() - t0) * 1000.0
 
-        if K > 0:
-            draft_tokens = torch.cat(draft_tokens_list, dim=-1)
-            draft_logits = torch.stack(draft_logits_list, dim=1)  # [B, K, V]
-        else:
-            draft_tokens = input_ids.new_empty(batch_size, 0)
+        # With K = 0 this raises ValueError, as speculative.py:128 does.
+        draft_tokens = torch.cat(draft_tokens_list, dim=-1)
+        draft_logits = torch.stack(draft_logits_list, dim=1)  # [B, K, V]
 
         # Phase 2: target forward (speculative.py:136-147).
         t1 = time.perf_counter()
@@ -168,25 +176,29 @@ class SpeculativeEngine:
         _sync(device)
         t_target_ms = (time.perf_counter() - t1) * 1000.0
 
-        if K == 0:
-            draft_logits = window[:, :0]
-
         # Phase 3: fused softmax + rejection sampling + resample/bonus.
         python = self.verify_mode == "python"
         uniforms = self._rand(batch_size, K + (2 if python else 1), device=device)
-        res = chain_verify(
-            window, draft_logits, draft_tokens.to(torch.int32), uniforms,
-            input_kind="logits", temperature=self.temperature, top_p=self.top_p,
-            mode=self.verify_mode)
-
-        # one host sync: the emitted count (equal on every row in python mode)
-        width = int(res.num_emitted.max().item())
-        accepted_tokens = res.tokens[:, :width].long()
+        if batch_size == 0:
+            # No row rejects: python mode accepts all K drafts and appends the
+            # bonus (speculative.py:166, :188); a cpp-mode row emits at least
+            # its final token.
+            width = K + 1 if python else 1
+            accepted_tokens = torch.empty(0, width, dtype=torch.long, device=device)
+            per_row = None if python else torch.empty(0, dtype=torch.int32, device=device)
+        else:
+            res = chain_verify(
+                window, draft_logits, draft_tokens.to(torch.int32), uniforms,
+                input_kind="logits", temperature=self.temperature, top_p=self.top_p,
+                mode=self.verify_mode)
+            # one host sync: the emitted count (equal on every row in python mode)
+            width = int(res.num_emitted.max().item())
+            accepted_tokens = res.tokens[:, :width].long()
+            per_row = None if python else res.num_emitted
         num_accepted = width
-        per_row = None if python else res.num_emitted
         self.total_draft_tokens += K
         self.total_accepted_tokens += num_accepted
-        acceptance_rate = num_accepted / K  # K = 0 raises, as speculative.py:202 does
+        acceptance_rate = num_accepted / K
 
         return SpeculativeBatchResult(
             accepted_tokens=accepted_tokens,

@@ -292,9 +292,36 @@ class TreeVerifyOutput:
     num_emitted: torch.Tensor  # [B]
     final: torch.Tensor        # [B]
     eos: torch.Tensor          # [B]
-    status: torch.Tensor       # [B] 1 when the uniform stream ran out
+    status: torch.Tensor       # [B] 0 ok, 1 uniforms ran out, 2 a team wait timed out
     target_probs: Optional[torch.Tensor] = None
     draft_probs: Optional[torch.Tensor] = None
+
+    def check_status(self) -> None:
+        """Raise RuntimeError unless every sequence's status is 0 (one host sync)."""
+        check_status(self.status)
+
+
+TREE_STATUS = {1: "the uniform stream ran out",
+               2: "a wait between the work-groups of its team timed out (kernels of other "
+                  "streams held a member back); run the call again"}
+
+
+def check_status(status: torch.Tensor) -> None:
+    """Raise RuntimeError when a tree verification reported a failure.
+
+    status [B] int32 (``TreeVerifyOutput.status``): 0 ok, 1 the uniform
+    stream ran out, 2 a team wait timed out.  The paths and tokens of a
+    failed call are not valid and must not be committed; the reference raises
+    rather than return unusable results (speculative.cpp:58-62).  Reads the
+    status to the host: one synchronisation with its stream."""
+    st = status.detach().to("cpu", torch.int32).reshape(-1)
+    bad = torch.nonzero(st).reshape(-1).tolist()
+    if not bad:
+        return
+    codes = sorted({int(st[b]) for b in bad})
+    what = "; ".join(f"{TREE_STATUS.get(c, f'status {c}')} (sequences "
+                     f"{[b for b in bad if int(st[b]) == c][:8]})" for c in codes)
+    raise RuntimeError(f"cfa_tree_verify failed: {what}")
 
 
 def tree_verify(target: torch.Tensor, draft: Optional[torch.Tensor], parents: torch.Tensor,
@@ -310,8 +337,9 @@ def tree_verify(target: torch.Tensor, draft: Optional[torch.Tensor], parents: to
     workspace: optional uint8 device tensor of tree_verify_workspace_bytes(B).
     status: 0 ok, 1 the uniform stream ran out, 2 a wait between the
     work-groups of a sequence timed out -- kernels of other streams held one
-    of them back; run the call again (raised as RuntimeError by
-    check_status).
+    of them back; run the call again.  ``check_status`` (or the output's
+    ``check_status()``) raises RuntimeError on either; the call itself does
+    not synchronise.
     """
     if mode not in ("cpp", "greedy"):
         raise ValueError("mode must be 'cpp' or 'greedy'")

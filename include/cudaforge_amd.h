@@ -53,7 +53,12 @@ extern "C" {
 /* Message of this thread's last failed call ("" if none). */
 const char *cfa_last_error(void);
 
-/* Library ABI version (major * 100 + minor). */
+/* Library ABI version (major * 100 + minor); equals CFA_ABI_VERSION for a
+ * library built from this header.  Major 2 changed two contracts of major 1:
+ * cfa_tree_verify takes (workspace, workspace_bytes) before its stream, and
+ * python-mode cfa_chain_verify reads uniforms [B, K+2] (row stride K+2), not
+ * [B, K+1].  Binding code checks the major before its first call. */
+#define CFA_ABI_VERSION 200
 int cfa_version(void);
 
 /* ---------------------------------------------------------------------------

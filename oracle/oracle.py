@@ -77,6 +77,10 @@ def lib() -> ctypes.CDLL:
         L.orc_py_sample_adjusted.restype = ctypes.c_int32
         L.orc_py_sample_adjusted.argtypes = [c_f32p, c_f32p, ctypes.c_int64, ctypes.c_float,
                                              ctypes.POINTER(ctypes.c_int)]
+        L.orc_py_residual_weights.restype = ctypes.c_int
+        L.orc_py_residual_weights.argtypes = [c_f32p, c_f32p, ctypes.c_int64, c_f32p]
+        L.orc_py_bonus_weights.restype = None
+        L.orc_py_bonus_weights.argtypes = [c_f32p, ctypes.c_int64, ctypes.c_float, c_f32p]
         L.orc_topp_keep.restype = None
         L.orc_topp_keep.argtypes = [c_f32p, ctypes.c_int64, ctypes.c_float, c_u8p]
         L.orc_sample_weights.restype = ctypes.c_int32
@@ -223,6 +227,24 @@ def py_sample_adjusted(target_p, draft_q, u: float) -> tuple[int, bool]:
     tok = lib().orc_py_sample_adjusted(_p(t, c_f32p), _p(d, c_f32p), t.size, np.float32(u),
                                        ctypes.byref(fb))
     return int(tok), bool(fb.value)
+
+
+def py_residual_weights(target_p, draft_q) -> tuple[np.ndarray, bool]:
+    """The normalised weights the python-mode resample draws from
+    (speculative.py:171-182) and whether the sum <= 1e-6 fallback applied."""
+    t, d = _f32(target_p), _f32(draft_q)
+    out = np.empty(t.size, np.float32)
+    fb = lib().orc_py_residual_weights(_p(t, c_f32p), _p(d, c_f32p), t.size, _p(out, c_f32p))
+    return out, bool(fb)
+
+
+def py_bonus_weights(pk, top_p: float) -> np.ndarray:
+    """The normalised weights the python-mode bonus draws from
+    (speculative.py:57-84, :188-195)."""
+    a = _f32(pk)
+    out = np.empty(a.size, np.float32)
+    lib().orc_py_bonus_weights(_p(a, c_f32p), a.size, np.float32(top_p), _p(out, c_f32p))
+    return out
 
 
 def topp_keep(p, top_p: float) -> np.ndarray:

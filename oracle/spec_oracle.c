@@ -263,31 +263,53 @@ int32_t orc_sample_weights(const float *w, int64_t V, float u) {
   return t;
 }
 
-/* speculative.py:171-182: residual clamp(t - d, 0), target row when its sum
- * is <= 1e-6 (the sum formed sequentially in fp32, as speculative.cpp:30-37
- * does), then a python-mode draw from the normalised weights. */
-int32_t orc_py_sample_adjusted(const float *target_p, const float *draft_q,
-                               int64_t V, float u, int *fallback) {
-  float *adjusted = (float *)malloc((size_t)V * sizeof(float));
+/* speculative.py:171-182: the weights the resample draws from.  The residual
+ * clamp(t - d, 0) divided by its sum (formed sequentially in fp32, as
+ * speculative.cpp:30-37 does), or the target row itself when that sum is
+ * <= 1e-6.  Returns whether the fallback applied. */
+int orc_py_residual_weights(const float *target_p, const float *draft_q,
+                            int64_t V, float *out) {
   float sum = 0.0f;
   for (int64_t i = 0; i < V; ++i) {
-    adjusted[i] = relu_std_max(target_p[i] - draft_q[i]);
-    sum += adjusted[i];
+    out[i] = relu_std_max(target_p[i] - draft_q[i]);
+    sum += out[i];
   }
-  int32_t tok;
   if (sum <= 1e-6f) {
-    if (fallback) *fallback = 1;
-    tok = py_inverse_cdf(target_p, V, u);
-  } else {
-    if (fallback) *fallback = 0;
-    for (int64_t i = 0; i < V; ++i) adjusted[i] /= sum;
-    tok = py_inverse_cdf(adjusted, V, u);
+    for (int64_t i = 0; i < V; ++i) out[i] = target_p[i];
+    return 1;
   }
-  free(adjusted);
+  for (int64_t i = 0; i < V; ++i) out[i] /= sum;
+  return 0;
+}
+
+/* The python-mode resample: a python-mode inverse-CDF draw from the weights
+ * of orc_py_residual_weights. */
+int32_t orc_py_sample_adjusted(const float *target_p, const float *draft_q,
+                               int64_t V, float u, int *fallback) {
+  float *w = (float *)malloc((size_t)V * sizeof(float));
+  int fb = orc_py_residual_weights(target_p, draft_q, V, w);
+  if (fallback) *fallback = fb;
+  int32_t tok = py_inverse_cdf(w, V, u);
+  free(w);
   return tok;
 }
 
-/* speculative.py:188-195: the top-p filtered bonus draw from target row K. */
+/* speculative.py:57-84 as the bonus draw sees it: the top-p keep set of the
+ * target row, the kept probabilities divided by their sequential fp32 sum
+ * (the renormalisation that the softmax over -inf-masked logits performs). */
+void orc_py_bonus_weights(const float *pk, int64_t V, float top_p, float *out) {
+  uint8_t *keep = (uint8_t *)malloc((size_t)V);
+  orc_topp_keep(pk, V, top_p, keep);
+  for (int64_t i = 0; i < V; ++i) out[i] = keep[i] ? pk[i] : 0.0f;
+  free(keep);
+  float sum = orc_seq_sum(out, V);
+  if (sum > 0.0f)
+    for (int64_t i = 0; i < V; ++i) out[i] /= sum;
+}
+
+/* speculative.py:188-195: the top-p filtered bonus draw from target row K.
+ * The draw normalises the kept weights by their sequential fp32 sum, exactly
+ * as orc_py_bonus_weights does. */
 static int32_t py_bonus(const float *pk, int64_t V, float top_p, float u,
                         uint8_t *keep, float *w) {
   orc_topp_keep(pk, V, top_p, keep);

@@ -94,9 +94,15 @@ int orc_verify_python(int B, int K, int64_t V, int64_t ld, int64_t tsb,
                       int32_t *out_n, int32_t *out_num_emitted,
                       int32_t *out_tokens);
 
-/* The python-mode residual draw (speculative.py:171-182): max(0, t - d),
- * sequential fp32 sum, the target row when the sum is <= 1e-6, otherwise the
- * normalised residual; drawn with the python-mode inverse CDF below. */
+/* The normalised weights the python-mode resample draws from (the residual,
+ * or the target row on the sum <= 1e-6 fallback; returns 1 on fallback). */
+int orc_py_residual_weights(const float *target_p, const float *draft_q,
+                            int64_t V, float *out);
+/* The normalised weights the python-mode bonus draws from (top-p kept
+ * target probabilities over their sequential fp32 sum). */
+void orc_py_bonus_weights(const float *pk, int64_t V, float top_p, float *out);
+/* The python-mode residual draw (speculative.py:171-182): the weights of
+ * orc_py_residual_weights drawn with the python-mode inverse CDF. */
 int32_t orc_py_sample_adjusted(const float *target_p, const float *draft_q,
                                int64_t V, float u, int *fallback);
 

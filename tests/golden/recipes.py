@@ -90,3 +90,79 @@ def c2_inputs(seed: int, B: int = 64, K: int = 8, V: int = 128256, sigma: float 
             tok[b, i] = _draw(dp[b, i], u[b, i])
     U = rng.random((B, K + 1)).astype(np.float32)
     return tl, dl, tok, U
+
+
+# ---- python-engine step cases (cudaforge/speculative.py:86-211) ----------
+
+def python_step_case(seed: int, B: int, K: int, V: int, steps: int, sigma: float = 2.0,
+                     noise: float = 0.5):
+    """Logit tables and uniforms for `steps` successive steps of the python engine.
+
+    Returns draft [S,B,K,V] fp32 (the last-row logits of each of the K draft
+    forwards), target [S,B,K+1,V] fp32 (the target's last K+1 rows) and
+    uniforms: draft draws [S,B,K], acceptance draws [S,B,K], final draws
+    [S,B,2] (the resample or bonus, then the bonus after a rejection at the
+    last position), all fp32 in [0, 1).  target = sigma * N(0,1);
+    draft = target[:K] + noise * N(0,1)."""
+    rng = np.random.default_rng(seed)
+    tl = (sigma * rng.standard_normal((steps, B, K + 1, V))).astype(np.float32)
+    dl = (tl[:, :, :K] + noise * rng.standard_normal((steps, B, K, V))).astype(np.float32)
+    ud = rng.random((steps, B, K)).astype(np.float32)
+    ua = rng.random((steps, B, K)).astype(np.float32)
+    uf = rng.random((steps, B, 2)).astype(np.float32)
+    return dl, tl, ud, ua, uf
+
+
+def fed_inverse_cdf(w: np.ndarray, u: np.ndarray):
+    """Stand-in for torch.multinomial(w, 1) driven by fed uniforms: per row, the
+    first index whose fp64 prefix sum of w / sum(w) exceeds u (a zero-weight
+    index is never returned).  Also returns each draw's distance from u to the
+    nearest prefix-sum boundary of its interval, so that a comparison with a
+    draw computed in another precision can leave out draws within rounding of
+    a boundary."""
+    w = np.asarray(w, np.float64)
+    ids = np.zeros(w.shape[0], np.int64)
+    margin = np.zeros(w.shape[0], np.float64)
+    for r in range(w.shape[0]):
+        c = np.cumsum(w[r] / w[r].sum())
+        i = int(np.searchsorted(c, float(u[r]), side="right"))
+        if i >= c.size:  # u past the last prefix sum: the last positive weight
+            i = int(np.flatnonzero(w[r] > 0)[-1])
+        lo = c[i - 1] if i > 0 else 0.0
+        ids[r] = i
+        margin[r] = min(abs(float(u[r]) - lo), abs(c[i] - float(u[r])))
+    return ids, margin
+
+
+class TableRunner:
+    """A runner with the protocol of speculative.py:115,139 (``forward(input_ids,
+    kv_cache_handles) -> logits [B, T, V]``) that replays logit tables.
+
+    table [S, B, R, V].  As the draft runner (``per_step`` = K forwards per
+    step), forward call j of step s returns logits whose last row is
+    table[s, :, j]; as the target runner (one forward per step) the last R
+    rows are table[s].  Other rows are zero: the engine never reads them."""
+
+    def __init__(self, table, draft: bool, device="cpu"):
+        import torch
+
+        self.table = torch.as_tensor(np.ascontiguousarray(table)).to(device)
+        self.draft = draft
+        self.calls = 0
+        self.inputs = []
+
+    def forward(self, input_ids, kv_cache_handles=None):
+        import torch
+
+        S, B, R, V = self.table.shape
+        self.inputs.append(input_ids.detach().cpu().clone())
+        T = input_ids.shape[1]
+        out = torch.zeros(input_ids.shape[0], T, V, dtype=self.table.dtype,
+                          device=self.table.device)
+        if self.draft:
+            s, j = divmod(self.calls, R)
+            out[:, -1] = self.table[s, :, j]
+        else:
+            out[:, T - R:] = self.table[self.calls]
+        self.calls += 1
+        return out

@@ -178,3 +178,22 @@ def test_fused_layer_argument_errors():
     rc = lib.cfa_rope_kv_paged_partials(p, 0, p, 8, 63, 32, 8, 128, 5e5, p, p, p, 0, 32, 16,
                                         p, 200, p, None)
     assert rc == _lib.CFA_ERR_ARG and "splits" in _lib.last_error()
+
+
+def test_abi_version_matches_bindings():
+    """The library reports the ABI of its header, which the bindings require."""
+    with open(os.path.join(HEADER_DIR, "cudaforge_amd.h")) as f:
+        hdr = int(re.search(r"#define CFA_ABI_VERSION (\d+)", f.read()).group(1))
+    assert _lib.load().cfa_version() == hdr == _lib.ABI_VERSION
+
+
+def test_tree_status_check_raises_on_failures():
+    """check_status: 0 passes; 1 (uniforms ran out) and 2 (a team wait timed
+    out) raise RuntimeError naming the sequences."""
+    from cudaforge_amd.verify import check_status
+
+    check_status(torch.zeros(4, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match=r"ran out .*\[2\]"):
+        check_status(torch.tensor([0, 0, 1, 0], dtype=torch.int32))
+    with pytest.raises(RuntimeError, match=r"timed out .*\[0, 3\]"):
+        check_status(torch.tensor([2, 0, 0, 2], dtype=torch.int32))

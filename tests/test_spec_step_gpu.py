@@ -293,3 +293,54 @@ def test_draft_level_graphs_match_eager(device):
             torch.cuda.synchronize()
             assert torch.equal(graph, eager), (rep, lvl, (graph - eager).abs().max().item())
             assert torch.equal(dm.k_pool, k1) and torch.equal(dm.v_pool, v1)
+
+
+@pytest.mark.parametrize("status", [1, 2])
+def test_failed_tree_verification_raises_and_commits_nothing(device, monkeypatch, status):
+    """A tree verification that reports a failure (1: the uniform stream ran
+    out, driven for real by a one-uniform stream; 2: a team wait timed out,
+    forced on the host by setting the status the kernel returned) raises
+    RuntimeError before anything is committed: context, root, page tables,
+    committed K/V of both caches unchanged; the next step runs normally.  The
+    reference raises rather than return unusable results
+    (speculative.cpp:58-62)."""
+    import cudaforge_amd.spec_step as S
+
+    B, ctx0 = 3, 40
+    tm = TargetModel(SMALL_T, device, seed=15)
+    dm = DraftModel(SMALL_D, device, B, max_slots=ctx0 + 64 + 8 * 8)
+    sp = TreeSpeculator(tm, dm, B, ctx0, depth=3, temperature=0.8, mode="cpp", max_steps=8,
+                        seed=16)
+    sp.step()
+    torch.cuda.synchronize()
+    ctx, root = list(sp.ctx), sp.root.clone()
+    tables = [list(sp.kv.get_block_table(b)) for b in range(B)]
+    kt = [_slots(sp.kv.key_pool, torch.tensor(tables[b], device=device), ctx[b]).clone()
+          for b in range(B)]
+    dk = [_slots(dm.k_pool, dm.block_tables[b], ctx[b]).clone() for b in range(B)]
+    if status == 1:
+        sp.n_uniforms = 1
+    else:
+        real = S.tree_verify
+
+        def timed_out(*a, **k):
+            out = real(*a, **k)
+            out.status[1] = 2
+            return out
+
+        monkeypatch.setattr(S, "tree_verify", timed_out)
+    with pytest.raises(RuntimeError, match="ran out" if status == 1 else "timed out"):
+        sp.step()
+    torch.cuda.synchronize()
+    assert sp.ctx == ctx and torch.equal(sp.root, root)
+    for b in range(B):
+        assert sp.kv.context_length(b) == ctx[b]
+        assert list(sp.kv.get_block_table(b)) == tables[b]
+        assert torch.equal(_slots(sp.kv.key_pool, torch.tensor(tables[b], device=device),
+                                  ctx[b]), kt[b])
+        assert torch.equal(_slots(dm.k_pool, dm.block_tables[b], ctx[b]), dk[b])
+    sp.n_uniforms = 2 * 2 * sp.depth + 2
+    monkeypatch.undo()
+    r = sp.step()
+    for b in range(B):
+        assert sp.ctx[b] == ctx[b] + r.path_len[b] and sp.kv.context_length(b) == sp.ctx[b]

@@ -9,8 +9,9 @@ what the runners returned; the probabilities the kernel used are checked
 against a float64 softmax (1e-6), and the accept count, the emitted ids and
 the telemetry against the oracle fed those probabilities and the uniforms
 the step drew.  Stub runners force the reference's quirks: a rejection at the
-last position appends a bonus (K + 1 tokens), K = 0 raises
-ZeroDivisionError.
+last position appends a bonus (K + 1 tokens), K = 0 raises the reference's
+ValueError before the target runs.  tests/test_python_golden_gpu.py replays
+the reference's own recorded steps.
 """
 import numpy as np
 import pytest
@@ -168,14 +169,18 @@ def test_rejection_at_last_position_emits_bonus(device):
     assert res.accepted_tokens.tolist() == [[7, 3]] * 2 and res.num_accepted == 2
 
 
-def test_k_zero_raises_zero_division(device):
+def test_k_zero_raises_before_the_target_runs(device):
+    """speculative.py:128: torch.cat of the empty draft list raises ValueError;
+    the target never runs and the totals stay 0 (the reference's own run,
+    tests/golden/python_engine.json cases k0_b1 / k0_b4)."""
     V = 32
-    r = PeakRunner(lambda t: 5, V, device)
-    eng = SpeculativeEngine(r, r, num_speculative_tokens=0)
-    with pytest.raises(ZeroDivisionError):
+    draft = Recorder(PeakRunner(lambda t: 5, V, device))
+    target = Recorder(PeakRunner(lambda t: 5, V, device))
+    eng = SpeculativeEngine(draft, target, num_speculative_tokens=0)
+    with pytest.raises(ValueError, match="expected a non-empty list of Tensors"):
         eng.step(torch.zeros(1, 3, dtype=torch.long, device=device))
-    # the totals were updated before the division, as in the reference
-    assert eng.total_draft_tokens == 0 and eng.total_accepted_tokens == 1
+    assert not draft.calls and not target.calls
+    assert eng.total_draft_tokens == 0 and eng.total_accepted_tokens == 0
     assert eng.get_aggregate_acceptance_rate() == 0.0
 
 
