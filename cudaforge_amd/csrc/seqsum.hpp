@@ -341,14 +341,13 @@ __device__ long long walk(int count, float &s, bool cdf, float r, const Item &it
   return -1;
 }
 
-// Serial replay of wave w's 64 tiles (all lanes redundantly; the 16-byte
-// LDS reads are broadcasts, eight of them in flight ahead of the adds).
-template <int NT>
-__device__ long long serial_wave(const Shared<NT> &sh, int w, float &s, bool cdf, float r,
-                                 long long blk0) {
-  constexpr int kElems = 64 * Shared<NT>::kTile;
-  const float4 *x4 = reinterpret_cast<const float4 *>(sh.x + w * kElems);
-  const long long i0 = blk0 + (long long)w * kElems;
+// Serial replay of the 1024 values xs[0 .. 1023] of elements i0 .. (all
+// lanes redundantly; the 16-byte LDS reads are broadcasts, eight of them in
+// flight ahead of the adds).
+__device__ __forceinline__ long long serial_run1024(const float *xs, long long i0, float &s,
+                                                    bool cdf, float r) {
+  constexpr int kElems = 1024;
+  const float4 *x4 = reinterpret_cast<const float4 *>(xs);
   float acc = s;
   for (int c = 0; c < kElems / 4; c += 8) {
     float4 v[8];
@@ -382,6 +381,15 @@ __device__ long long serial_wave(const Shared<NT> &sh, int w, float &s, bool cdf
   }
   s = acc;
   return -1;
+}
+
+// Serial replay of wave w's 64 tiles of the staged block.
+template <int NT>
+__device__ long long serial_wave(const Shared<NT> &sh, int w, float &s, bool cdf, float r,
+                                 long long blk0) {
+  constexpr int kElems = 64 * Shared<NT>::kTile;
+  static_assert(kElems == 1024, "a wave's span is 1024 elements");
+  return serial_run1024(sh.x + w * kElems, blk0 + (long long)w * kElems, s, cdf, r);
 }
 
 // Walk one staged block (wave 0 executes); updates sh.s / sh.found.

@@ -33,6 +33,7 @@ namespace cfa {
 namespace team {
 
 constexpr int kMaxG = 8;
+constexpr int kRecWords = 20;  // run-1 function (2), its region, break tile, 16 break values
 constexpr long kSpinLimit = 1l << 22;   // about 0.2-0.5 s of polling
 
 // One team's global state (part of the caller's workspace, zero before the
@@ -43,6 +44,10 @@ struct alignas(256) State {
   // exchanged per-member values: four words (tag << 32 | value) per member,
   // in the buffer of the exchange tag's parity
   unsigned long long xw[kMaxG][2][4];
+  // per member, a segment function's second run and break tile (tag << 32 |
+  // value): written before an exact pass's second exchange, read after it,
+  // and rewritten only after the next pass's first exchange
+  unsigned long long rec[kMaxG][kRecWords];
 };
 
 // LDS a team member needs besides seq::Shared.
@@ -170,23 +175,15 @@ __device__ void get_hand(Team &t, Lds &l, int k, unsigned tag, float &s, long lo
   found = (long long)(uint32_t)(w >> 32) - 1;
 }
 
-// The tile and wave functions of the staged block sh.x (as seq::run) from
-// the entry value guess E.  Ends with a work-group barrier.
-template <int NT>
-__device__ void block_functions(seq::Shared<NT> &sh, float E) {
+// The tile and wave functions of a block whose thread t holds the values
+// v of its tile (elements 16 t .. 16 t + 15), from the entry value guess E.
+// SH provides the function tables (tI, treg, wI, wreg, wserial) and wscan.
+// Ends with a work-group barrier.
+template <int NT, class SH>
+__device__ void block_functions_v(SH &sh, const float (&v)[seq::Shared<NT>::kTile], float E) {
   using namespace seq;
   constexpr int TILE = Shared<NT>::kTile;
   const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float v[TILE];
-  const float4 *x4 = reinterpret_cast<const float4 *>(sh.x + tid * TILE);
-#pragma unroll
-  for (int k = 0; k < TILE / 4; ++k) {
-    const float4 q = x4[k];
-    v[4 * k] = q.x;
-    v[4 * k + 1] = q.y;
-    v[4 * k + 2] = q.z;
-    v[4 * k + 3] = q.w;
-  }
   float A = 0.0f;
 #pragma unroll
   for (int k = 0; k < TILE; ++k) A += v[k];
@@ -228,6 +225,24 @@ __device__ void block_functions(seq::Shared<NT> &sh, float E) {
     sh.wserial[wave] = crossings >= kSerialCrossings ? 1 : 0;
   }
   __syncthreads();
+}
+
+// The tile and wave functions of the staged block sh.x (as seq::run) from
+// the entry value guess E.  Ends with a work-group barrier.
+template <int NT>
+__device__ void block_functions(seq::Shared<NT> &sh, float E) {
+  constexpr int TILE = seq::Shared<NT>::kTile;
+  float v[TILE];
+  const float4 *x4 = reinterpret_cast<const float4 *>(sh.x + threadIdx.x * TILE);
+#pragma unroll
+  for (int k = 0; k < TILE / 4; ++k) {
+    const float4 q = x4[k];
+    v[4 * k] = q.x;
+    v[4 * k + 1] = q.y;
+    v[4 * k + 2] = q.z;
+    v[4 * k + 3] = q.w;
+  }
+  block_functions_v<NT>(sh, v, E);
 }
 
 // Stage elements [b0, min(b1, b0 + BLK)) of xf into sh.x (zero past the end).

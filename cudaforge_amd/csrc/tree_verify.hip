@@ -36,6 +36,7 @@
 
 #include "abi_internal.hpp"
 #include "dist.hpp"
+#include "lds_dma.hpp"
 #include "seqsum.hpp"
 #include "team.hpp"
 
@@ -157,6 +158,7 @@ struct __align__(16) Smem {
   unsigned long long kids;
   float2 raw[kMaxN];  // (target, draft) raw values of the current node's rows at each child's token
   float uni[kMaxU];   // the sequence's uniforms (the first kMaxU)
+  Args args;          // the launch arguments (stage_args)
 };
 
 __device__ __forceinline__ const float *trow(const Args &a, int b, int n) {
@@ -183,12 +185,40 @@ __device__ __forceinline__ void ms_merge(float &m1, float &s1, float m2, float s
   m1 = M;
 }
 
+// Block-wide (max, sum exp2) of two rows from every thread's partials, in a
+// fixed order (lanes, then waves): (m_t, s_t, m_d, s_d).  Ends with a barrier.
+__device__ float4 block_ms2(float mt, float st, float md, float sd, float (&red)[4][kNT / 64],
+                            float c) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 32; k >= 1; k >>= 1) {
+    const float m2 = __shfl_xor(mt, k, 64), s2 = __shfl_xor(st, k, 64);
+    const float m3 = __shfl_xor(md, k, 64), s3 = __shfl_xor(sd, k, 64);
+    ms_merge(mt, st, m2, s2, c);
+    ms_merge(md, sd, m3, s3, c);
+  }
+  if (lane == 0) {
+    red[0][wave] = mt;
+    red[1][wave] = st;
+    red[2][wave] = md;
+    red[3][wave] = sd;
+  }
+  __syncthreads();
+  float4 r = make_float4(red[0][0], red[1][0], red[2][0], red[3][0]);
+  for (int w = 1; w < kNT / 64; ++w) {
+    ms_merge(r.x, r.y, red[0][w], red[1][w], c);
+    ms_merge(r.z, r.w, red[2][w], red[3][w], c);
+  }
+  __syncthreads();
+  return r;
+}
+
 // (max, sum exp2((x - max) c)) of t[lo, hi) and of d[lo, hi) (d may be
 // NULL), block-wide, in a fixed order: (m_t, s_t, m_d, s_d).  Both rows'
 // loads are issued together.
 __device__ __attribute__((noinline)) float4 slice_ms2(const Args &a, const float *t, const float *d, long long lo,
                             long long hi, Smem &sm) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const float c = a.c;
   float mt = -INFINITY, st = 0.0f, md = -INFINITY, sd = 0.0f;
   auto update = [c](float &m, float &s, float v0, float v1, float v2, float v3) {
@@ -243,36 +273,13 @@ __device__ __attribute__((noinline)) float4 slice_ms2(const Args &a, const float
       if (d) upd1(md, sd, d[i]);
     }
   }
-#pragma unroll
-  for (int k = 32; k >= 1; k >>= 1) {
-    const float m2 = __shfl_xor(mt, k, 64), s2 = __shfl_xor(st, k, 64);
-    const float m3 = __shfl_xor(md, k, 64), s3 = __shfl_xor(sd, k, 64);
-    ms_merge(mt, st, m2, s2, c);
-    ms_merge(md, sd, m3, s3, c);
-  }
-  if (lane == 0) {
-    sm.red[0][wave] = mt;
-    sm.red[1][wave] = st;
-    sm.red[2][wave] = md;
-    sm.red[3][wave] = sd;
-  }
-  __syncthreads();
-  float4 r = make_float4(sm.red[0][0], sm.red[1][0], sm.red[2][0], sm.red[3][0]);
-  for (int w = 1; w < kNT / 64; ++w) {
-    ms_merge(r.x, r.y, sm.red[0][w], sm.red[1][w], c);
-    ms_merge(r.z, r.w, sm.red[2][w], sm.red[3][w], c);
-  }
-  __syncthreads();
-  return r;
+  return block_ms2(mt, st, md, sd, sm.red, c);
 }
 
-// Softmax statistics of the target row (and the draft row when `d` is set),
-// reduced over the team in member order: sm.stat = (M_t, 1/S_t, M_d, 1/S_d).
-__device__ void team_stats(const Args &a, team::Team &tm, Smem &sm, const float *t,
-                           const float *d) {
-  long long lo, hi;
-  slice(a, tm, lo, hi);
-  const float4 p = slice_ms2(a, t, d, lo, hi, sm);
+// The members' (max, sum) partials p combined in member order:
+// sm.stat = (M_t, 1/S_t, M_d, 1/S_d).  Ends with a barrier.
+template <class SM>
+__device__ void team_combine_stats(const Args &a, team::Team &tm, SM &sm, float4 p) {
   team::exchange(tm, sm.tl, team::f4u(p));
   if (threadIdx.x == 0) {
     float4 acc = team::u4f(sm.tl.got[0][0]);
@@ -284,6 +291,16 @@ __device__ void team_stats(const Args &a, team::Team &tm, Smem &sm, const float 
     sm.stat = make_float4(acc.x, 1.0f / acc.y, acc.z, 1.0f / acc.w);
   }
   __syncthreads();
+}
+
+// Softmax statistics of the target row (and the draft row when `d` is set),
+// reduced over the team in member order: sm.stat = (M_t, 1/S_t, M_d, 1/S_d).
+__device__ void team_stats(const Args &a, team::Team &tm, Smem &sm, const float *t,
+                           const float *d) {
+  long long lo, hi;
+  slice(a, tm, lo, hi);
+  const float4 p = slice_ms2(a, t, d, lo, hi, sm);
+  team_combine_stats(a, tm, sm, p);
 }
 
 __device__ Dist row_dist(const Args &a, const float *row, float M, float invS) {
@@ -304,15 +321,16 @@ __device__ void write_probs(const Args &a, const team::Team &tm, const Dist &d, 
   for (long long i = lo + threadIdx.x; i < hi; i += kNT) dst[i] = d(i);
 }
 
-// First index of the largest probability (std::max_element) over the team.
-__device__ int team_argmax(const Args &a, team::Team &tm, Smem &sm, const Dist &d) {
+// First index of the largest probability (std::max_element) over the team:
+// this member scans [lo, hi), val(i) the probability of index i.
+template <class SM, class Val>
+__device__ int team_argmax(const Args &a, team::Team &tm, SM &sm, long long lo, long long hi,
+                           const Val &val) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  long long lo, hi;
-  slice(a, tm, lo, hi);
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (long long i = lo + tid; i < hi; i += kNT) {
-    const float v = d(i);
+    const float v = val(i);
     if (v > bv) {  // strided: indices increase, so ">" keeps the first max
       bv = v;
       bi = (int)i;
@@ -365,8 +383,515 @@ __device__ int team_argmax(const Args &a, team::Team &tm, Smem &sm, const Dist &
   return sm.amax;
 }
 
+// ---------------------------------------------------------------------------
+// Resident rows.  When a member's share of a row fits in kLCap elements, the
+// node's rows are read from HBM once, by the statistics pass, into LDS as
+// probabilities (P: target, Q: draft), and every exact pass evaluates its
+// elements there: the residual terms max(0, P - Q) or the inverse CDF of P.
+// After a residual sum S > 1e-6 is applied, P becomes max(0, P - Q) / S in
+// place -- the fp32 operations of Resid::eval (and of the oracle's residual
+// update), in the same order -- so an exact pass never divides per element
+// and never reads HBM.
+// ---------------------------------------------------------------------------
+constexpr int kRTile = seq::Shared<kNT>::kTile;  // 16 consecutive elements per thread
+constexpr int kLCap = kNT * kRTile;               // elements of a row per member (16384)
+
+struct __align__(16) SmemR {
+  float P[kLCap];  // this member's share of the residual r^(k) (target probabilities at k = 0)
+  float Q[kLCap];  // ... of the draft probabilities
+  seq::Inc tI[kNT];
+  int16_t treg[kNT];
+  seq::Inc wI[kNT / 64];
+  int16_t wreg[kNT / 64];
+  uint8_t wserial[kNT / 64];
+  float wscan[kNT / 64];
+  float s;
+  long long found;
+  alignas(16) float xs[1024];  // one wave's values, for its serial replay
+  int ctl[4];                  // share-function analysis: first real tile, break, ...
+  seq::Inc w0[kNT / 64], w1[kNT / 64];  // per-wave compositions of runs 0 and 1
+  uint32_t rec[team::kMaxG][team::kRecWords];  // the members' run-1 records
+  team::Lds tl;
+  float red[4][kNT / 64];
+  float Slist[kMaxN];
+  int par[kMaxN];
+  int tk[kMaxN];
+  int path[kMaxN];
+  float4 stat;
+  int amax;
+  unsigned long long kids;
+  float2 raw[kMaxN];
+  float uni[kMaxU];
+  Args args;
+};
+
+// Share layout: element e of a share sits in tile e / 16, and the tile's
+// four 16-byte chunks are XOR-swizzled by the tile index, so that 16
+// consecutive tiles' chunk c (one thread each: a ds_read_b128 of 16 lanes),
+// and the 16 elements of one tile (a serial replay), both fall in distinct
+// LDS banks.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int chunk_off(int tile, int c) {
+  return tile * kRTile + ((c ^ (((tile >> 1) ^ (tile >> 3)) & 3)) << 2);
+}
+__device__ __forceinline__ int phys(int e) { return chunk_off(e >> 4, (e >> 2) & 3) + (e & 3); }
+__device__ __forceinline__ CFA_LDS f32x4 *lds4(float *p) { return (CFA_LDS f32x4 *)p; }
+__device__ __forceinline__ const CFA_LDS f32x4 *lds4(const float *p) {
+  return (const CFA_LDS f32x4 *)p;
+}
+__device__ __forceinline__ float lds1(const float *p) { return *(const CFA_LDS float *)p; }
+
+// This member's share [lo, lo + n) of a row in resident mode (shares are a
+// multiple of the tile long; the host checks that they fit kLCap).
+__device__ __forceinline__ void rslice(const Args &a, const team::Team &tm, long long &lo, int &n) {
+  const long long L = ((a.V + tm.G - 1) / tm.G + kRTile - 1) / kRTile * kRTile;
+  lo = min((long long)a.V, (long long)tm.m * L);
+  n = (int)(min((long long)a.V, lo + L) - lo);
+}
+
+// Loads this member's share of row t (and of row d when set) into sm.P
+// (sm.Q), zero past its end, as raw values.  With logits, the rows' softmax
+// statistics are reduced over the team into sm.stat; convert_share turns the
+// share into probabilities when a pass first needs them.  Ends with a
+// barrier.
+__device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team &tm, SmemR &sm,
+                                                     const float *t, const float *d) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int tid = threadIdx.x;
+  long long lo;
+  int n;
+  rslice(a, tm, lo, n);
+  const float c = a.c;
+  const bool lg = a.logits != 0;
+  float mt = -INFINITY, st = 0.0f, md = -INFINITY, sd = 0.0f;
+  auto upd = [c](float &m, float &s, float v) {
+    if (v > m) {
+      s *= __builtin_amdgcn_exp2f((m - v) * c);
+      m = v;
+    }
+    const float ms = (m == -INFINITY) ? 0.0f : m;
+    s += __builtin_amdgcn_exp2f((v - ms) * c);
+  };
+  // four values at once: one maximum, at most one rescale, four independent
+  // exponentials
+  auto upd4 = [c](float &m, float &s, f32x4 v) {
+    const float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+    if (mx > m) {
+      s *= __builtin_amdgcn_exp2f((m - mx) * c);
+      m = mx;
+    }
+    const float ms = (m == -INFINITY) ? 0.0f : m;
+    s += (__builtin_amdgcn_exp2f((v[0] - ms) * c) + __builtin_amdgcn_exp2f((v[1] - ms) * c)) +
+         (__builtin_amdgcn_exp2f((v[2] - ms) * c) + __builtin_amdgcn_exp2f((v[3] - ms) * c));
+  };
+  constexpr int U = kLCap / (4 * kNT);  // 16-byte vectors per thread and row
+  if (a.vec) {
+    // n % 4 == 0 (V % 4 == 0 and lo % 16 == 0); every load issued before
+    // the first use
+    const int n4 = n / 4;
+    const f32x4 *t4 = reinterpret_cast<const f32x4 *>(t + lo);
+    const f32x4 *d4 = d ? reinterpret_cast<const f32x4 *>(d + lo) : t4;
+    f32x4 vt[U], vd[U];
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = tid + u * kNT;
+      vt[u] = i < n4 ? t4[i] : zero;
+      vd[u] = (d && i < n4) ? d4[i] : zero;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = tid + u * kNT;  // vector i: chunk i % 4 of tile i / 4
+      *lds4(sm.P + chunk_off(i >> 2, i & 3)) = vt[u];
+      if (d) *lds4(sm.Q + chunk_off(i >> 2, i & 3)) = vd[u];
+      if (lg && i < n4) {  // the two rows' chains interleave
+        upd4(mt, st, vt[u]);
+        if (d) upd4(md, sd, vd[u]);
+      }
+    }
+  } else {
+    for (int e = tid; e < kLCap; e += kNT) {
+      const float x = e < n ? t[lo + e] : 0.0f;
+      sm.P[phys(e)] = x;
+      if (lg && e < n) upd(mt, st, x);
+      if (d) {
+        const float y = e < n ? d[lo + e] : 0.0f;
+        sm.Q[phys(e)] = y;
+        if (lg && e < n) upd(md, sd, y);
+      }
+    }
+  }
+  if (lg) team_combine_stats(a, tm, sm, block_ms2(mt, st, md, sd, sm.red, c));
+  __syncthreads();
+}
+
+// The loaded share as probabilities, exp2((x - M) c) * (1 / S) as
+// Dist::eval rounds it (logits input; probabilities are loaded as they
+// are).  Ends with a barrier.
+__device__ __attribute__((noinline)) void convert_share(const Args &a, const team::Team &tm,
+                                                       SmemR &sm, bool with_d) {
+  if (!a.logits) return;
+  long long lo;
+  int n;
+  rslice(a, tm, lo, n);
+  const float4 S = sm.stat;
+  const float c = a.c;
+  // this thread's tile; elements past n stay zero
+  const int tile = threadIdx.x, j0 = tile * kRTile;
+  f32x4 pv[kRTile / 4], qv[kRTile / 4];
+#pragma unroll
+  for (int k = 0; k < kRTile / 4; ++k) {
+    pv[k] = *lds4(sm.P + chunk_off(tile, k));
+    if (with_d) qv[k] = *lds4(sm.Q + chunk_off(tile, k));
+  }
+  auto cv = [c, n](float x, float M, float invS, int j) {
+    return j < n ? __builtin_amdgcn_exp2f((x - M) * c) * invS : 0.0f;
+  };
+#pragma unroll
+  for (int k = 0; k < kRTile / 4; ++k) {
+    f32x4 p, q;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      p[w] = cv(pv[k][w], S.x, S.y, j0 + 4 * k + w);
+      if (with_d) q[w] = cv(qv[k][w], S.z, S.w, j0 + 4 * k + w);
+    }
+    *lds4(sm.P + chunk_off(tile, k)) = p;
+    if (with_d) *lds4(sm.Q + chunk_off(tile, k)) = q;
+  }
+  __syncthreads();
+}
+
+// The values of tile `tile` (elements 16 tile .. 16 tile + 15) of this
+// member's share for an exact pass: max(0, P - Q) (the residual terms of
+// speculative.cpp:33) or P.
+__device__ __forceinline__ void share_vals(const SmemR &sm, bool resid, int tile, float (&v)[kRTile]) {
+#pragma unroll
+  for (int k = 0; k < kRTile / 4; ++k) {
+    const f32x4 p = *lds4(sm.P + chunk_off(tile, k));
+    if (resid) {
+      const f32x4 q = *lds4(sm.Q + chunk_off(tile, k));
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v[4 * k + w] = relu_ref(p[w] - q[w]);
+    } else {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v[4 * k + w] = p[w];
+    }
+  }
+}
+
+// Serial replay of tile `tile` of the share (wave-uniform): lane k < 16
+// evaluates element k, the adds take the values lane by lane.
+__device__ long long serial_tile_r(const SmemR &sm, bool resid, int tile, float &s, bool cdf,
+                                   float r, long long blk0) {
+  const int j = phys(tile * kRTile + (seq::lane_id() & (kRTile - 1)));
+  const float x = resid ? relu_ref(lds1(sm.P + j) - lds1(sm.Q + j)) : lds1(sm.P + j);
+  long long hit = -1;
+#pragma unroll
+  for (int k = 0; k < kRTile; ++k) {
+    const float xk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
+    const float t = s + xk;
+    if (hit < 0) {
+      s = t;
+      if (cdf && r <= s) hit = blk0 + (long long)tile * kRTile + k;
+    }
+  }
+  return hit;
+}
+
+// Orders one wave's LDS accesses (a wave's LDS operations complete in issue
+// order, so this only keeps the compiler from moving accesses across it).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Serial replay of wave w's 1024 elements: every lane evaluates its tile
+// into sm.xs, then the values are added in element order.
+__device__ long long serial_wave_r(SmemR &sm, bool resid, int w, float &s, bool cdf, float r,
+                                   long long blk0) {
+  const int lane = seq::lane_id();
+  float v[kRTile];
+  share_vals(sm, resid, w * 64 + lane, v);
+  float4 *x4 = reinterpret_cast<float4 *>(sm.xs + lane * kRTile);
+#pragma unroll
+  for (int k = 0; k < kRTile / 4; ++k)
+    x4[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+  wave_lds_sync();
+  const long long hit = seq::serial_run1024(sm.xs, blk0 + (long long)w * 1024, s, cdf, r);
+  wave_lds_sync();  // sm.xs is rewritten by the next replay
+  return hit;
+}
+
+// Walk this member's share exactly from sm.s (wave 0 executes, as
+// seq::sweep_block over the functions block_functions_v wrote); updates sm.s
+// and sm.found.
+__device__ void sweep_share(SmemR &sm, bool resid, long long blk0, bool cdf, float r) {
+  using namespace seq;
+  float s = sm.s;
+  auto tile_desc = [&](int w) {
+    return [&sm, w, resid, cdf, r, blk0](int i, float &ss) -> long long {
+      return serial_tile_r(sm, resid, w * 64 + i, ss, cdf, r, blk0);
+    };
+  };
+  auto wave_item = [&sm](int i, int &reg) -> Inc {
+    reg = sm.wreg[i];
+    return sm.wI[i];
+  };
+  auto wave_desc = [&](int w, float &ss) -> long long {
+    if (sm.wserial[w]) return serial_wave_r(sm, resid, w, ss, cdf, r, blk0);
+    auto tile_item = [&sm, w](int i, int &reg) -> Inc {
+      reg = sm.treg[w * 64 + i];
+      return sm.tI[w * 64 + i];
+    };
+    return walk(64, ss, cdf, r, tile_item, tile_desc(w));
+  };
+  const long long found = walk(kNT / 64, s, cdf, r, wave_item, wave_desc);
+  if (lane_id() == 0) {
+    sm.s = s;
+    if (found >= 0) sm.found = found;
+  }
+}
+
+// team::team_seq over the resident shares: the exact left-to-right fp32
+// accumulation of max(0, P - Q) (resid; sum mode) or of P (CDF mode: *idx =
+// the first index i with r <= s_i, or -1), with the same early exit.  Every
+// thread of every member calls it with the same arguments.
+template <class Early = team::NoEarlyExit>
+__device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team &tm, SmemR &sm,
+                                                      bool resid, bool cdf, float r,
+                                                      long long *idx,
+                                                      const Early &early = Early()) {
+  using namespace seq;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const unsigned tag = ++tm.pass;  // the workspace starts at zero: 0 is never a tag
+  long long lo;
+  int n;
+  rslice(a, tm, lo, n);
+
+  // A: the share's approximate sum (thread tiles, wave scans, waves in order)
+  float T = 0.0f;
+  {
+    float v[kRTile];
+    share_vals(sm, resid, tid, v);
+    float A = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRTile; ++k) A += v[k];
+    const float incl = wave_incl_scan_f32(A);
+    if (lane == 63) sm.wscan[wave] = incl;
+    __syncthreads();
+    for (int q = 0; q < kNT / 64; ++q) T += sm.wscan[q];
+    __syncthreads();
+  }
+  team::exchange(tm, sm.tl, make_uint4(f2u(T), 0u, 0u, 0u));
+  float E = 0.0f;
+  for (int j = 0; j < tm.m; ++j) E += u2f(sm.tl.got[j][0].x);
+  if (!cdf) {
+    float tot = 0.0f;
+    for (int j = 0; j < tm.G; ++j) tot += u2f(sm.tl.got[j][0].x);
+    // per member: 16 sequential adds per thread, a 6-level wave scan and 16
+    // waves; then the G members
+    if (early(tot, (kRTile + 6 + kNT / 64 + 1) + tm.G)) {
+      if (idx) *idx = -1;
+      __syncthreads();
+      return -1.0f;
+    }
+  }
+
+  // B: tile / wave functions from the guess E, and the share as a function
+  // of its entry value: kind 1, one run of tiles in region r0; kind 2, run 0
+  // in region r0, a break tile (straddling a region boundary, or the first
+  // tile of another region) replayed serially from its published values,
+  // and run 1 in region r1; kind 0, neither (the owner sweeps the share).
+  {
+    float v[kRTile];
+    share_vals(sm, resid, tid, v);
+    team::block_functions_v<kNT>(sm, v, E);
+  }
+  {
+    // the first tile of the share (in tile order) meeting a condition: one
+    // LDS atomic per wave, from its first lane that meets it
+    auto first_of = [&](bool c, int slot) {
+      const unsigned long long m = __ballot(c);
+      if (m && lane == (int)__builtin_ctzll(m)) atomicMin(&sm.ctl[slot], tid);
+    };
+    const Inc f = sm.tI[tid];
+    const int reg = sm.treg[tid];
+    const bool bad = f.e == kBad;
+    if (tid < 4) sm.ctl[tid] = tid < 3 ? kNT : 0;
+    __syncthreads();
+    first_of(bad || reg != kAnyRegion, 0);  // the first real tile
+    __syncthreads();
+    const int fr = sm.ctl[0];
+    const int r0 = fr < kNT ? sm.treg[fr] : kAnyRegion;
+    first_of(bad || (reg != kAnyRegion && reg != r0), 1);  // the break
+    __syncthreads();
+    const int brk = sm.ctl[1];
+    first_of(tid > brk && (bad || reg != kAnyRegion), 2);  // the first real tile after it
+    __syncthreads();
+    const int fa = sm.ctl[2];
+    const int r1 = fa < kNT ? sm.treg[fa] : kAnyRegion;
+    if (__ballot(tid > brk && (bad || (reg != kAnyRegion && reg != r1))) && lane == 0)
+      sm.ctl[3] = 1;  // not two runs
+    const Inc w0 = wave_incl_compose(tid < brk ? f : inc_identity());
+    const Inc w1 = wave_incl_compose((tid > brk && !bad) ? f : inc_identity());
+    if (lane == 63) {
+      sm.w0[wave] = w0;
+      sm.w1[wave] = w1;
+    }
+    __syncthreads();
+    const int kind = brk >= kNT ? 1 : (sm.ctl[3] ? 0 : 2);
+    Inc F0 = inc_identity(), F1 = inc_identity();
+    if (tid == 0) {
+      for (int w = 0; w < kNT / 64; ++w) {
+        F0 = compose(F0, sm.w0[w]);
+        F1 = compose(F1, sm.w1[w]);
+      }
+      sm.tl.got[0][1] = make_uint4(F0.e, F0.o, (uint32_t)r0, (uint32_t)kind);  // scratch
+      sm.w0[0] = F1;
+    }
+    __syncthreads();
+    if (kind == 2 && tid < team::kRecWords) {
+      // the record: run 1's function and region, the break tile, its values
+      uint32_t w;
+      if (tid == 0) w = sm.w0[0].e;
+      else if (tid == 1) w = sm.w0[0].o;
+      else if (tid == 2) w = (uint32_t)r1;
+      else if (tid == 3) w = (uint32_t)brk;
+      else {
+        const int j = phys(brk * kRTile + (tid - 4));
+        w = f2u(resid ? relu_ref(lds1(sm.P + j) - lds1(sm.Q + j)) : lds1(sm.P + j));
+      }
+      team::st64(&tm.st->rec[tm.m][tid], ((unsigned long long)tag << 32) | w);
+    }
+  }
+  team::exchange(tm, sm.tl, sm.tl.got[0][1]);
+  // the records of the shares that published two runs (bounded waits on
+  // their tags)
+  if (tid < team::kMaxG * team::kRecWords) {
+    const int j = tid / team::kRecWords, w = tid % team::kRecWords;
+    if (j < tm.G && sm.tl.got[j][0].w == 2u) {
+      unsigned long long x = 0;
+      long spins = 0;
+      for (;;) {
+        x = team::ld64(&tm.st->rec[j][w]);
+        if ((unsigned)(x >> 32) == tag) break;
+        if (sm.tl.failed || ++spins > team::kSpinLimit || team::error_set(tm.err)) {
+          sm.tl.failed = 1;
+          team::set_error(tm.err);
+          x = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      sm.rec[j][w] = (uint32_t)x;
+    }
+  }
+  __syncthreads();
+  const long long L = ((a.V + tm.G - 1) / tm.G + kRTile - 1) / kRTile * kRTile;
+
+  // C: walk the shares from the exact running value
+  float s = 0.0f;
+  long long found = -1;
+  // one run of region reg from the exact value v (false: it does not apply)
+  auto run = [](Inc F, int reg, float &v) -> bool {
+    if (reg == kAnyRegion) return true;
+    const int rs = region_of(v);
+    if (rs != reg) return false;
+    const uint32_t au = units_of(v, rs);
+    const uint32_t inc = inc_at(F, au);
+    if (au + inc > kUnitsTop) return false;
+    v = value_of(au + inc, rs);
+    return true;
+  };
+  for (int j = 0; j < tm.G; ++j) {
+    const uint4 fj = sm.tl.got[j][0];
+    bool applies = false;
+    float snext = s;
+    if (fj.w == 1u) {
+      applies = run(Inc{fj.x, fj.y}, (int)fj.z, snext) && !(cdf && r <= snext);
+    } else if (fj.w == 2u && run(Inc{fj.x, fj.y}, (int)fj.z, snext) && !(cdf && r <= snext)) {
+      // run 0 applied; the break tile serially, then run 1
+      const int brk = (int)sm.rec[j][3];
+      long long hit = -1;
+#pragma unroll
+      for (int k = 0; k < kRTile; ++k) {
+        const float t = snext + u2f(sm.rec[j][4 + k]);
+        if (hit < 0) {
+          snext = t;
+          if (cdf && r <= snext) hit = (long long)j * L + (long long)brk * kRTile + k;
+        }
+      }
+      if (hit >= 0) {  // the draw lands in the break tile
+        s = snext;
+        found = hit;
+        break;
+      }
+      applies = run(Inc{sm.rec[j][0], sm.rec[j][1]}, (int)sm.rec[j][2], snext) &&
+                !(cdf && r <= snext);
+    }
+    if (applies) {
+      s = snext;
+      continue;
+    }
+    if (j == tm.m) {  // sweep this share exactly from s
+      if (tid == 0) {
+        sm.s = s;
+        sm.found = -1;
+      }
+      __syncthreads();
+      if (wave == 0) sweep_share(sm, resid, lo, cdf, r);
+      __syncthreads();
+      s = sm.s;
+      found = sm.found;
+      team::put_hand(tm, j + 1, tag, s, found);
+      __syncthreads();
+    } else {
+      team::get_hand(tm, sm.tl, j + 1, tag, s, found);
+    }
+    if (cdf && found >= 0) break;
+  }
+  (void)n;
+  if (idx) *idx = found;
+  __syncthreads();
+  return s;
+}
+
+// r^(k+1) = max(0, r^(k) - q) / S in place over this member's share (the
+// order of operations of Resid::eval).  Ends with a barrier.
+__device__ __attribute__((noinline)) void normalize_share(SmemR &sm, float S) {
+  // element-wise at every position (P and Q share the layout)
+  f32x4 pv[kRTile / 4], qv[kRTile / 4];
+#pragma unroll
+  for (int k = 0; k < kRTile / 4; ++k) {
+    pv[k] = *lds4(sm.P + 4 * (threadIdx.x + k * kNT));
+    qv[k] = *lds4(sm.Q + 4 * (threadIdx.x + k * kNT));
+  }
+#pragma unroll
+  for (int k = 0; k < kRTile / 4; ++k) {
+    f32x4 r;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) r[w] = relu_ref(pv[k][w] - qv[k][w]) / S;
+    *lds4(sm.P + 4 * (threadIdx.x + k * kNT)) = r;
+  }
+  __syncthreads();
+}
+
+// This member's share of P or Q (the probabilities of a visited row) to dst.
+__device__ __attribute__((noinline)) void write_share(const Args &a, const team::Team &tm,
+                                                     const float *src, float *dst) {
+  if (!dst) return;
+  long long lo;
+  int n;
+  rslice(a, tm, lo, n);
+  for (int e = threadIdx.x; e < n; e += kNT) dst[lo + e] = lds1(src + phys(e));
+}
+
 // One sequence's walk; every member of the team runs it with the same data.
-__device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
+// RES: the node's rows are resident in LDS (SmemR), else re-read from HBM
+// by every exact pass (Smem).
+template <bool RES, class SM>
+__device__ void walk_sequence(const Args &a, team::Team &tm, SM &sm, int b) {
   const int tid = threadIdx.x;
   const int N = a.N, V = a.V;
   if (tid < N) {
@@ -402,29 +927,70 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
       const int xs = (x >= 0 && x < V) ? x : 0;
       sm.raw[tid] = make_float2(tr[xs], dr[xs]);
     }
-    if (a.logits) team_stats(a, tm, sm, tr, dr);
-    else __syncthreads();
+    // resident rows: whether the share holds probabilities yet (the first
+    // pass that reads them converts it; a node whose first child is
+    // accepted never does)
+    bool conv = false;
+    auto ensure_probs = [&]() {
+      if constexpr (RES) {
+        if (!conv) convert_share(a, tm, sm, dr != nullptr);
+        conv = true;
+      }
+    };
+    if constexpr (RES) {
+      load_rows_r(a, tm, sm, tr, dr);
+    } else {
+      if (a.logits) team_stats(a, tm, sm, tr, dr);
+      else __syncthreads();
+    }
     const float4 st = sm.stat;
     const Dist t = row_dist(a, tr, st.x, st.y);
-    if (a.probs_t) write_probs(a, tm, t, a.probs_t + ((long long)b * N + node) * V);
+    float *const pt_out = a.probs_t ? a.probs_t + ((long long)b * N + node) * V : nullptr;
+    if constexpr (RES) {
+      if (pt_out || a.probs_d) {
+        ensure_probs();
+        write_share(a, tm, sm.P, pt_out);
+      }
+    } else if (pt_out) {
+      write_probs(a, tm, t, pt_out);
+    }
+    // the first index of the largest target probability, over the team
+    auto argmax_t = [&]() -> int {
+      long long lo, hi;
+      if constexpr (RES) {
+        ensure_probs();
+        int n;
+        rslice(a, tm, lo, n);
+        return team_argmax(a, tm, sm, lo, lo + n,
+                           [&sm, lo](long long i) { return lds1(sm.P + phys((int)(i - lo))); });
+      } else {
+        slice(a, tm, lo, hi);
+        return team_argmax(a, tm, sm, lo, hi, t);
+      }
+    };
     if (leaf) {  // the bonus token
       if (a.greedy) {
-        fin = team_argmax(a, tm, sm, t);
+        fin = argmax_t();
       } else {
         if (draws >= a.n_u) {
           status = 1;
           break;
         }
         long long idx = -1;
-        team::team_seq<kNT>(tm, sm.tl, Resid{t, t, sm.Slist, 0}, V, true, U_at(draws++), sm.seq,
-                            &idx);
+        if constexpr (RES) {
+          ensure_probs();
+          team_seq_r(a, tm, sm, false, true, U_at(draws++), &idx);
+        } else {
+          team::team_seq<kNT>(tm, sm.tl, Resid{t, t, sm.Slist, 0}, V, true, U_at(draws++),
+                              sm.seq, &idx);
+        }
         fin = (idx < 0) ? V - 1 : (int)idx;
       }
       break;
     }
     int accepted = -1;
     if (a.greedy) {
-      const int am = team_argmax(a, tm, sm, t);
+      const int am = argmax_t();
       for (unsigned long long m = kids; m; m &= m - 1) {
         const int c = __builtin_ctzll(m);
         if (sm.tk[c] == am) {
@@ -438,7 +1004,9 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
       }
     } else {
       const Dist d = row_dist(a, dr, st.z, st.w);
-      if (a.probs_d) write_probs(a, tm, d, a.probs_d + ((long long)b * N + node) * V);
+      float *const pd_out = a.probs_d ? a.probs_d + ((long long)b * N + node) * V : nullptr;
+      if constexpr (RES) write_share(a, tm, sm.Q, pd_out);
+      else if (pd_out) write_probs(a, tm, d, pd_out);
       int k = 0;  // applied normalisations of the residual
       for (unsigned long long m = kids; m; m &= m - 1) {
         const int c = __builtin_ctzll(m);
@@ -466,19 +1034,28 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
         if (rest && draws < a.n_u && sm.tk[__builtin_ctzll(rest)] >= 0 &&
             sm.tk[__builtin_ctzll(rest)] < V) {
           const SiblingAccepts early{r, sm.raw[__builtin_ctzll(rest)], U_at(draws), (long long)V};
-          S = team::team_seq<kNT>(tm, sm.tl, ResidX{r}, V, false, 0.0f, sm.seq, nullptr, early);
+          if constexpr (RES) {
+            ensure_probs();
+            S = team_seq_r(a, tm, sm, true, false, 0.0f, nullptr, early);
+          } else
+            S = team::team_seq<kNT>(tm, sm.tl, ResidX{r}, V, false, 0.0f, sm.seq, nullptr, early);
           if (S < 0.0f) {  // the sibling is accepted for every S in the bounds
             accepted = __builtin_ctzll(rest);
             ++draws;
             break;
           }
         } else {
-          S = team::team_seq<kNT>(tm, sm.tl, ResidX{r}, V, false, 0.0f, sm.seq, nullptr);
+          if constexpr (RES) {
+            ensure_probs();
+            S = team_seq_r(a, tm, sm, true, false, 0.0f, nullptr);
+          } else
+            S = team::team_seq<kNT>(tm, sm.tl, ResidX{r}, V, false, 0.0f, sm.seq, nullptr);
         }
         if (S > 1e-6f) {  // else the residual stays (speculative.cpp:37-40)
           if (tid == 0) sm.Slist[k] = S;
           __syncthreads();
           ++k;
+          if constexpr (RES) normalize_share(sm, S);
         }
       }
       if (status) break;
@@ -488,8 +1065,13 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
           break;
         }
         long long idx = -1;
-        team::team_seq<kNT>(tm, sm.tl, Resid{t, d, sm.Slist, k}, V, true, U_at(draws++), sm.seq,
-                            &idx);
+        if constexpr (RES) {
+          ensure_probs();
+          team_seq_r(a, tm, sm, false, true, U_at(draws++), &idx);
+        } else {
+          team::team_seq<kNT>(tm, sm.tl, Resid{t, d, sm.Slist, k}, V, true, U_at(draws++),
+                              sm.seq, &idx);
+        }
         fin = (idx < 0) ? V - 1 : (int)idx;
         break;
       }
@@ -524,17 +1106,46 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, Smem &sm, int b) {
   }
 }
 
-__global__ __launch_bounds__(kNT) void tree_verify_kernel(Args a) {
-  __shared__ Smem sm;
+// The launch arguments, copied once from the kernarg segment into the
+// work-group's LDS.  The walk passes them by reference to out-of-line
+// functions; a reference to the by-value kernel parameter would make every
+// lane keep its own copy in scratch memory.
+template <class SM>
+__device__ __forceinline__ const Args &stage_args(SM &sm) {
+  static_assert(sizeof(Args) % 4 == 0 && sizeof(Args) / 4 <= kNT, "Args copy");
+  typedef const uint32_t __attribute__((address_space(4))) kword;
+  kword *src = (kword *)__builtin_amdgcn_kernarg_segment_ptr();
+  if (threadIdx.x < sizeof(Args) / 4)
+    reinterpret_cast<uint32_t *>(&sm.args)[threadIdx.x] = src[threadIdx.x];
+  __syncthreads();
+  return sm.args;
+}
+
+template <bool RES, class SM>
+__device__ __forceinline__ void tree_verify_body(SM &sm) {
+  const Args &a = stage_args(sm);
   const int team_id = (int)blockIdx.x / a.G;
   if (threadIdx.x == 0) sm.tl.failed = 0;
   __syncthreads();
   if (team_id >= a.T) return;
   team::Team tm{a.teams + team_id, a.err, (int)blockIdx.x % a.G, a.G, 0u, 0u};
   for (int b = team_id; b < a.B; b += a.T) {
-    walk_sequence(a, tm, sm, b);
+    walk_sequence<RES>(a, tm, sm, b);
     __syncthreads();
   }
+}
+
+// Every exact pass re-reads its elements from HBM (any V).
+__global__ __launch_bounds__(kNT) void tree_verify_kernel(Args) {
+  __shared__ Smem sm;
+  tree_verify_body<false>(sm);
+}
+
+// The visited rows stay resident in LDS (a member's share of a row at most
+// kLCap elements).
+__global__ __launch_bounds__(kNT) void tree_verify_res_kernel(Args) {
+  __shared__ SmemR sm;
+  tree_verify_body<true>(sm);
 }
 
 // Zero the teams' state before the launch.
@@ -561,20 +1172,32 @@ inline Plan plan(int B, int cus, int per_cu) {
 using namespace cfa;
 
 namespace {
-// Work-groups of the tree kernel one CU holds, per device (queried once;
-// threads that race on the first query store the same value).
-int kernel_per_cu() {
-  static std::atomic<int> cache[64];
+// Work-groups of a tree kernel (0: rows re-read, 1: rows resident) one CU
+// holds, per device (queried once; threads that race on the first query
+// store the same value).
+int kernel_per_cu(int which) {
+  static std::atomic<int> cache[2][64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
-  int n = cache[dev].load(std::memory_order_relaxed);
+  int n = cache[which][dev].load(std::memory_order_relaxed);
   if (n == 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)treev::tree_verify_kernel,
-                                                     treev::kNT, 0) != hipSuccess || n < 1)
+    const void *k = which ? (const void *)treev::tree_verify_res_kernel
+                          : (const void *)treev::tree_verify_kernel;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, treev::kNT, 0) != hipSuccess || n < 1)
       n = 1;
-    cache[dev].store(n, std::memory_order_relaxed);
+    cache[which][dev].store(n, std::memory_order_relaxed);
   }
   return n;
+}
+
+// CFA_TREE_RESIDENT=0 keeps every vocabulary on the kernel that re-reads
+// rows from HBM (the path for shares larger than the LDS holds).
+bool resident_allowed() {
+  static const bool on = [] {
+    const char *v = std::getenv("CFA_TREE_RESIDENT");
+    return !(v != nullptr && v[0] == '0');
+  }();
+  return on;
 }
 constexpr size_t kErrBytes = 256;
 
@@ -622,7 +1245,12 @@ extern "C" int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t 
     return fail_arg("draft strides overlap rows");
   if (B > 2147483647 / 2) return fail_arg("B too large");
   const int cus = device_cu_count();
-  const treev::Plan pl = treev::plan(B, cus, kernel_per_cu());
+  // rows resident in LDS when a member's share of a row fits there
+  treev::Plan pl = treev::plan(B, cus, kernel_per_cu(1));
+  const long long share = ((long long)(V + pl.G - 1) / pl.G + treev::kRTile - 1) /
+                          treev::kRTile * treev::kRTile;
+  const bool resident = resident_allowed() && share <= treev::kLCap;
+  if (!resident) pl = treev::plan(B, cus, kernel_per_cu(0));
   const size_t need = kErrBytes + (size_t)pl.T * sizeof(team::State);
   if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255))
     return fail_arg("workspace missing, too small or not 256-byte aligned "
@@ -682,10 +1310,13 @@ extern "C" int cfa_tree_verify(const float *target, int64_t t_stride_b, int64_t 
   if (cooperative_launch()) {
     void *tok = prof::enabled() ? prof::begin("tree_verify", st) : nullptr;
     void *args[] = {&a};
-    const hipError_t e = hipLaunchCooperativeKernel((const void *)treev::tree_verify_kernel, grid,
-                                                    dim3(treev::kNT), args, 0, st);
+    const void *k = resident ? (const void *)treev::tree_verify_res_kernel
+                             : (const void *)treev::tree_verify_kernel;
+    const hipError_t e = hipLaunchCooperativeKernel(k, grid, dim3(treev::kNT), args, 0, st);
     if (tok) prof::end(tok, st);
     if (e != hipSuccess) return fail_hip(e, "tree_verify (cooperative launch)");
+  } else if (resident) {
+    CFA_LAUNCH("tree_verify", treev::tree_verify_res_kernel, grid, dim3(treev::kNT), 0, st, a);
   } else {
     CFA_LAUNCH("tree_verify", treev::tree_verify_kernel, grid, dim3(treev::kNT), 0, st, a);
   }

@@ -172,3 +172,27 @@ def test_uniform_stream_exhaustion_is_reported(device):
     out = tree_verify(t_d, t_d.clone() * 2, p_d, tok_d, U_d, input_kind="probs", mode="cpp")
     torch.cuda.synchronize()
     assert out.status.cpu().tolist() == [1, 1]
+
+
+@pytest.mark.parametrize("kind", ["probs", "logits"])
+def test_large_vocab_rereads_rows(device, kind):
+    """V = 140000: with 8 work-groups per sequence a share exceeds what the
+    LDS holds, so the kernel that re-reads rows from HBM runs.  Decisions vs
+    the oracle (fed the kernel's probabilities for logits input)."""
+    parents = T.binary_tree_parents(15)
+    B, V = 2, 140000
+    tl, dl, tok, U = tree_case(51, B, parents, V)
+    if kind == "probs":
+        tp = _softmax64(tl.astype(np.float64) / 0.7).astype(np.float32)
+        dp = _softmax64(dl.astype(np.float64) / 0.7).astype(np.float32)
+        t_d, d_d, tok_d, U_d, p_d = _dev(device, tp, dp, tok, U, parents)
+        out = tree_verify(t_d, d_d, p_d, tok_d, U_d, input_kind="probs", mode="cpp")
+    else:
+        t_d, d_d, tok_d, U_d, p_d = _dev(device, tl, dl, tok, U, parents)
+        out = tree_verify(t_d, d_d, p_d, tok_d, U_d, input_kind="logits", temperature=0.7,
+                          mode="cpp", return_probs=True)
+    torch.cuda.synchronize()
+    assert out.status.cpu().tolist() == [0] * B
+    if kind == "logits":
+        tp, dp = out.target_probs.cpu().numpy(), out.draft_probs.cpu().numpy()
+    _check(_cpu(out), parents, tp, dp, tok, U, -1, False)
