@@ -93,7 +93,10 @@ __device__ __forceinline__ void set_error(int *err) {
 // counter and a separate read of published values took two.  A buffer is
 // written again two exchanges later: by then every member has published the
 // exchange in between, which it does only after reading this one.
-__device__ void exchange(Team &t, Lds &l, uint4 v) {
+// The exchange in two halves: a member may publish its value, do work that
+// needs nothing from the others, and collect theirs later.  It has to have
+// collected an exchange before it publishes the next one.
+__device__ void exchange_publish(Team &t, uint4 v) {
   const unsigned tag = ++t.nb;  // the workspace starts at zero: 0 is never a tag
   __syncthreads();              // every thread is done with the previous exchange's l.got
   if (threadIdx.x == 0) {
@@ -104,6 +107,10 @@ __device__ void exchange(Team &t, Lds &l, uint4 v) {
     st64(mine + 2, hi | v.z);
     st64(mine + 3, hi | v.w);
   }
+}
+
+__device__ void exchange_collect(Team &t, Lds &l) {
+  const unsigned tag = t.nb;
   if (threadIdx.x < t.G) {
     unsigned long long *p = &t.st->xw[threadIdx.x][tag & 1u][0];
     unsigned long long w0 = 0, w1 = 0, w2 = 0, w3 = 0;
@@ -127,6 +134,11 @@ __device__ void exchange(Team &t, Lds &l, uint4 v) {
     l.got[threadIdx.x][0] = make_uint4((uint32_t)w0, (uint32_t)w1, (uint32_t)w2, (uint32_t)w3);
   }
   __syncthreads();
+}
+
+__device__ void exchange(Team &t, Lds &l, uint4 v) {
+  exchange_publish(t, v);
+  exchange_collect(t, l);
 }
 __device__ __forceinline__ uint4 f4u(float4 v) {
   return make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),

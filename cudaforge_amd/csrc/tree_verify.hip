@@ -708,7 +708,28 @@ __device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team 
     share_vals(sm, resid, tid, v);
     team::block_functions_v<kNT>(sm, v, E);
   }
-  {
+  // Share 0 enters at exactly 0 and crosses a binade every doubling of the
+  // running value: its owner publishes kind 0, sweeps it at once (it needs
+  // nothing from the others) and hands the exit value on, and collects the
+  // other members' functions afterwards.
+  float s = 0.0f;
+  long long found = -1;
+  int j0 = 0;
+  if (tm.m == 0) {
+    team::exchange_publish(tm, make_uint4(0u, 0u, (uint32_t)kAnyRegion, 0u));
+    if (tid == 0) {
+      sm.s = 0.0f;
+      sm.found = -1;
+    }
+    __syncthreads();
+    if (wave == 0) sweep_share(sm, resid, lo, cdf, r);
+    __syncthreads();
+    s = sm.s;
+    found = sm.found;
+    team::put_hand(tm, 1, tag, s, found);
+    team::exchange_collect(tm, sm.tl);
+    j0 = 1;
+  } else {
     // the first tile of the share (in tile order) meeting a condition: one
     // LDS atomic per wave, from its first lane that meets it
     auto first_of = [&](bool c, int slot) {
@@ -764,8 +785,8 @@ __device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team 
       }
       team::st64(&tm.st->rec[tm.m][tid], ((unsigned long long)tag << 32) | w);
     }
+    team::exchange(tm, sm.tl, sm.tl.got[0][1]);
   }
-  team::exchange(tm, sm.tl, sm.tl.got[0][1]);
   // the records of the shares that published two runs (bounded waits on
   // their tags)
   if (tid < team::kMaxG * team::kRecWords) {
@@ -791,8 +812,6 @@ __device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team 
   const long long L = ((a.V + tm.G - 1) / tm.G + kRTile - 1) / kRTile * kRTile;
 
   // C: walk the shares from the exact running value
-  float s = 0.0f;
-  long long found = -1;
   // one run of region reg from the exact value v (false: it does not apply)
   auto run = [](Inc F, int reg, float &v) -> bool {
     if (reg == kAnyRegion) return true;
@@ -804,7 +823,7 @@ __device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team 
     v = value_of(au + inc, rs);
     return true;
   };
-  for (int j = 0; j < tm.G; ++j) {
+  for (int j = j0; j < tm.G && !(cdf && found >= 0); ++j) {
     const uint4 fj = sm.tl.got[j][0];
     bool applies = false;
     float snext = s;
