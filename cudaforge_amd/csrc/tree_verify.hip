@@ -407,7 +407,6 @@ struct __align__(16) SmemR {
   float wscan[kNT / 64];
   float s;
   long long found;
-  alignas(16) float xs[1024];  // one wave's values, for its serial replay
   int ctl[4];                  // share-function analysis: first real tile, break, ...
   seq::Inc w0[kNT / 64], w1[kNT / 64];  // per-wave compositions of runs 0 and 1
   uint32_t rec[team::kMaxG][team::kRecWords];  // the members' run-1 records
@@ -598,31 +597,6 @@ __device__ long long serial_tile_r(const SmemR &sm, bool resid, int tile, float 
   return hit;
 }
 
-// Orders one wave's LDS accesses (a wave's LDS operations complete in issue
-// order, so this only keeps the compiler from moving accesses across it).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Serial replay of wave w's 1024 elements: every lane evaluates its tile
-// into sm.xs, then the values are added in element order.
-__device__ long long serial_wave_r(SmemR &sm, bool resid, int w, float &s, bool cdf, float r,
-                                   long long blk0) {
-  const int lane = seq::lane_id();
-  float v[kRTile];
-  share_vals(sm, resid, w * 64 + lane, v);
-  float4 *x4 = reinterpret_cast<float4 *>(sm.xs + lane * kRTile);
-#pragma unroll
-  for (int k = 0; k < kRTile / 4; ++k)
-    x4[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
-  wave_lds_sync();
-  const long long hit = seq::serial_run1024(sm.xs, blk0 + (long long)w * 1024, s, cdf, r);
-  wave_lds_sync();  // sm.xs is rewritten by the next replay
-  return hit;
-}
-
 // Walk this member's share exactly from sm.s (wave 0 executes, as
 // seq::sweep_block over the functions block_functions_v wrote); updates sm.s
 // and sm.found.
@@ -638,8 +612,9 @@ __device__ void sweep_share(SmemR &sm, bool resid, long long blk0, bool cdf, flo
     reg = sm.wreg[i];
     return sm.wI[i];
   };
+  // (a wave crossing several binades is walked tile by tile as well: from
+  // LDS a crossing tile's serial replay is cheaper than the wave's)
   auto wave_desc = [&](int w, float &ss) -> long long {
-    if (sm.wserial[w]) return serial_wave_r(sm, resid, w, ss, cdf, r, blk0);
     auto tile_item = [&sm, w](int i, int &reg) -> Inc {
       reg = sm.treg[w * 64 + i];
       return sm.tI[w * 64 + i];
