@@ -306,8 +306,17 @@ __device__ __forceinline__ float2 slice_partial(const Args &a, int r, int slice)
 // (max, sum exp2) over the slice.
 __device__ void mw_reset_share(const Args &a, long long wg, long long nwg);
 
+// Threads of a statistics work-group (512 and 1024 measured 1% and 10%
+// slower per C2 step).  A slice's partial depends on the fold order, which
+// depends on the slice bounds (a function of the shape) and on the
+// work-group size (which thread folds which vectors, the order of the block
+// reduction): every statistics kernel uses kStatsNT threads, so the head,
+// tail and one-pass statistics of a row combine identical partials.
+constexpr int kStatsNT = 256;
+
 template <int NT, int W>
 __global__ __launch_bounds__(NT) void stats_kernel(Args a, int set) {
+  static_assert(NT == kStatsNT, "every statistics pass folds a slice the same way");
   if (a.mw_reset && set != kRowsTail)
     mw_reset_share(a, (long long)blockIdx.y * gridDim.x + blockIdx.x, (long long)gridDim.x * gridDim.y);
   const int r = set_row(a, set, (int)blockIdx.x);
@@ -328,9 +337,6 @@ __global__ __launch_bounds__(NT) void stats_kernel(Args a, int set) {
   }
 }
 
-// Threads of a statistics work-group (512 and 1024 measured 1% and 10%
-// slower per C2 step).
-constexpr int kStatsNT = 256;
 // Row groups the balanced tail pass can list in LDS.
 constexpr int kTailMaxGroups = 4096;
 
@@ -344,6 +350,7 @@ constexpr int kTailMaxGroups = 4096;
 // item's partial is the one stats_kernel computes for that (row, slice).
 template <int NT>
 __global__ __launch_bounds__(NT) void stats_tail_kernel(Args a) {
+  static_assert(NT == kStatsNT, "every statistics pass folds a slice the same way");
   __shared__ int list[kTailMaxGroups];
   __shared__ int wcnt[NT / 64];
   __shared__ int base;
