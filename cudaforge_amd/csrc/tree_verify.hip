@@ -176,41 +176,59 @@ __device__ __forceinline__ void slice(const Args &a, const team::Team &tm, long 
   hi = min((long long)a.V, lo + L);
 }
 
-__device__ __forceinline__ void ms_merge(float &m1, float &s1, float m2, float s2, float c) {
-  const float M = fmaxf(m1, m2);
-  if (M == -INFINITY) return;
-  const float f1 = (m1 == M) ? 1.0f : __builtin_amdgcn_exp2f((m1 - M) * c);
-  const float f2 = (m2 == M) ? 1.0f : __builtin_amdgcn_exp2f((m2 - M) * c);
-  s1 = s1 * f1 + s2 * f2;
-  m1 = M;
+// A partial sum exp2((x - m) c) over values of maximum m, rescaled to the
+// larger maximum M (0 for an empty partial, m = -inf).
+__device__ __forceinline__ float rescale_sum(float m, float s, float M, float c) {
+  return (m == -INFINITY) ? 0.0f : s * __builtin_amdgcn_exp2f((m - M) * c);
 }
 
-// Block-wide (max, sum exp2) of two rows from every thread's partials, in a
-// fixed order (lanes, then waves): (m_t, s_t, m_d, s_d).  Ends with a barrier.
+__device__ __forceinline__ float wave_max_f32(float x) {
+#pragma unroll
+  for (int k = 32; k >= 1; k >>= 1) x = fmaxf(x, __shfl_xor(x, k, 64));
+  return x;
+}
+__device__ __forceinline__ float wave_sum_f32(float x) {
+#pragma unroll
+  for (int k = 32; k >= 1; k >>= 1) x += __shfl_xor(x, k, 64);
+  return x;
+}
+
+// Block-wide (max, sum exp2) of two rows from every thread's partials (m, s):
+// the block maximum first (a maximum needs no order), then every thread's sum
+// rescaled to it once and summed over lanes (xor butterfly), then over waves
+// in order: (m_t, s_t, m_d, s_d).  A merge per butterfly step and per wave
+// would cost two exponentials each on one long dependent chain.  Ends with a
+// barrier.
 __device__ float4 block_ms2(float mt, float st, float md, float sd, float (&red)[4][kNT / 64],
                             float c) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int k = 32; k >= 1; k >>= 1) {
-    const float m2 = __shfl_xor(mt, k, 64), s2 = __shfl_xor(st, k, 64);
-    const float m3 = __shfl_xor(md, k, 64), s3 = __shfl_xor(sd, k, 64);
-    ms_merge(mt, st, m2, s2, c);
-    ms_merge(md, sd, m3, s3, c);
-  }
+  const float wmt = wave_max_f32(mt), wmd = wave_max_f32(md);
   if (lane == 0) {
-    red[0][wave] = mt;
-    red[1][wave] = st;
-    red[2][wave] = md;
-    red[3][wave] = sd;
+    red[0][wave] = wmt;
+    red[2][wave] = wmd;
   }
   __syncthreads();
-  float4 r = make_float4(red[0][0], red[1][0], red[2][0], red[3][0]);
+  float Mt = red[0][0], Md = red[2][0];
+#pragma unroll
   for (int w = 1; w < kNT / 64; ++w) {
-    ms_merge(r.x, r.y, red[0][w], red[1][w], c);
-    ms_merge(r.z, r.w, red[2][w], red[3][w], c);
+    Mt = fmaxf(Mt, red[0][w]);
+    Md = fmaxf(Md, red[2][w]);
+  }
+  const float wst = wave_sum_f32(rescale_sum(mt, st, Mt, c));
+  const float wsd = wave_sum_f32(rescale_sum(md, sd, Md, c));
+  if (lane == 0) {
+    red[1][wave] = wst;
+    red[3][wave] = wsd;
   }
   __syncthreads();
-  return r;
+  float St = 0.0f, Sd = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kNT / 64; ++w) {
+    St += red[1][w];
+    Sd += red[3][w];
+  }
+  __syncthreads();
+  return make_float4(Mt, St, Md, Sd);
 }
 
 // (max, sum exp2((x - max) c)) of t[lo, hi) and of d[lo, hi) (d may be
@@ -276,19 +294,27 @@ __device__ __attribute__((noinline)) float4 slice_ms2(const Args &a, const float
   return block_ms2(mt, st, md, sd, sm.red, c);
 }
 
-// The members' (max, sum) partials p combined in member order:
-// sm.stat = (M_t, 1/S_t, M_d, 1/S_d).  Ends with a barrier.
+// The members' (max, sum) partials p combined (the team maximum, then the
+// rescaled sums in member order): sm.stat = (M_t, 1/S_t, M_d, 1/S_d).  Ends
+// with a barrier.
 template <class SM>
 __device__ void team_combine_stats(const Args &a, team::Team &tm, SM &sm, float4 p) {
   team::exchange(tm, sm.tl, team::f4u(p));
   if (threadIdx.x == 0) {
-    float4 acc = team::u4f(sm.tl.got[0][0]);
-    for (int j = 1; j < tm.G; ++j) {
+    // the team maximum, then each member's sum rescaled to it, in member order
+    float Mt = -INFINITY, Md = -INFINITY;
+    for (int j = 0; j < tm.G; ++j) {
       const float4 v = team::u4f(sm.tl.got[j][0]);
-      ms_merge(acc.x, acc.y, v.x, v.y, a.c);
-      ms_merge(acc.z, acc.w, v.z, v.w, a.c);
+      Mt = fmaxf(Mt, v.x);
+      Md = fmaxf(Md, v.z);
     }
-    sm.stat = make_float4(acc.x, 1.0f / acc.y, acc.z, 1.0f / acc.w);
+    float St = 0.0f, Sd = 0.0f;
+    for (int j = 0; j < tm.G; ++j) {
+      const float4 v = team::u4f(sm.tl.got[j][0]);
+      St += rescale_sum(v.x, v.y, Mt, a.c);
+      Sd += rescale_sum(v.z, v.w, Md, a.c);
+    }
+    sm.stat = make_float4(Mt, 1.0f / St, Md, 1.0f / Sd);
   }
   __syncthreads();
 }
@@ -484,12 +510,17 @@ __device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team 
          (__builtin_amdgcn_exp2f((v[2] - ms) * c) + __builtin_amdgcn_exp2f((v[3] - ms) * c));
   };
   constexpr int U = kLCap / (4 * kNT);  // 16-byte vectors per thread and row
+  // thread c < N: the raw values of the two rows at child c's token (an
+  // invalid token reads index 0), issued behind the share's loads
+  const bool want = d && tid < a.N && ((sm.kids >> tid) & 1ull);
+  float2 raw = make_float2(0.0f, 0.0f);
   if (a.vec) {
     // n % 4 == 0 (V % 4 == 0 and lo % 16 == 0); every load issued before
     // the first use
+    typedef const f32x4 __attribute__((address_space(1))) gf32x4;
     const int n4 = n / 4;
-    const f32x4 *t4 = reinterpret_cast<const f32x4 *>(t + lo);
-    const f32x4 *d4 = d ? reinterpret_cast<const f32x4 *>(d + lo) : t4;
+    gf32x4 *t4 = (gf32x4 *)(t + lo);
+    gf32x4 *d4 = d ? (gf32x4 *)(d + lo) : t4;
     f32x4 vt[U], vd[U];
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -497,6 +528,12 @@ __device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team 
       const int i = tid + u * kNT;
       vt[u] = i < n4 ? t4[i] : zero;
       vd[u] = (d && i < n4) ? d4[i] : zero;
+    }
+    if (want) {
+      const int x = sm.tk[tid];
+      const int xs = (x >= 0 && x < a.V) ? x : 0;
+      raw = make_float2(((const float __attribute__((address_space(1))) *)t)[xs],
+                        ((const float __attribute__((address_space(1))) *)d)[xs]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -509,6 +546,11 @@ __device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team 
       }
     }
   } else {
+    if (want) {
+      const int x = sm.tk[tid];
+      const int xs = (x >= 0 && x < a.V) ? x : 0;
+      raw = make_float2(t[xs], d[xs]);
+    }
     for (int e = tid; e < kLCap; e += kNT) {
       const float x = e < n ? t[lo + e] : 0.0f;
       sm.P[phys(e)] = x;
@@ -520,6 +562,7 @@ __device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team 
       }
     }
   }
+  if (want) sm.raw[tid] = raw;
   if (lg) team_combine_stats(a, tm, sm, block_ms2(mt, st, md, sd, sm.red, c));
   __syncthreads();
 }
@@ -915,8 +958,9 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, SM &sm, int b) {
     const float *tr = trow(a, b, node);
     const float *dr = (leaf || a.greedy) ? nullptr : drow(a, b, node);
     // the rows' raw values at the children's tokens, loaded ahead of the
-    // statistics pass (thread c: child c; an invalid token reads index 0)
-    if (dr && tid < N && ((kids >> tid) & 1ull)) {
+    // statistics pass (thread c: child c; an invalid token reads index 0);
+    // load_rows_r gathers them behind its own loads
+    if (!RES && dr && tid < N && ((kids >> tid) & 1ull)) {
       const int x = sm.tk[tid];
       const int xs = (x >= 0 && x < V) ? x : 0;
       sm.raw[tid] = make_float2(tr[xs], dr[xs]);
