@@ -96,7 +96,7 @@ __device__ __forceinline__ void set_error(int *err) {
 // The exchange in two halves: a member may publish its value, do work that
 // needs nothing from the others, and collect theirs later.  It has to have
 // collected an exchange before it publishes the next one.
-__device__ void exchange_publish(Team &t, uint4 v) {
+__device__ __forceinline__ void exchange_publish(Team &t, uint4 v) {
   const unsigned tag = ++t.nb;  // the workspace starts at zero: 0 is never a tag
   __syncthreads();              // every thread is done with the previous exchange's l.got
   if (threadIdx.x == 0) {
@@ -109,7 +109,7 @@ __device__ void exchange_publish(Team &t, uint4 v) {
   }
 }
 
-__device__ void exchange_collect(Team &t, Lds &l) {
+__device__ __forceinline__ void exchange_collect(Team &t, Lds &l) {
   const unsigned tag = t.nb;
   if (threadIdx.x < t.G) {
     unsigned long long *p = &t.st->xw[threadIdx.x][tag & 1u][0];
@@ -136,7 +136,7 @@ __device__ void exchange_collect(Team &t, Lds &l) {
   __syncthreads();
 }
 
-__device__ void exchange(Team &t, Lds &l, uint4 v) {
+__device__ __forceinline__ void exchange(Team &t, Lds &l, uint4 v) {
   exchange_publish(t, v);
   exchange_collect(t, l);
 }
@@ -159,7 +159,7 @@ __device__ __forceinline__ void put_hand(Team &t, int k, unsigned tag, float s, 
 }
 
 // Waits (bounded) for handoff k of pass `tag`; every thread gets it.
-__device__ void get_hand(Team &t, Lds &l, int k, unsigned tag, float &s, long long &found) {
+__device__ __forceinline__ void get_hand(Team &t, Lds &l, int k, unsigned tag, float &s, long long &found) {
   if (threadIdx.x == 0) {
     unsigned long long v = 0, h = 0;  // failure: value 0, no hit
     if (!l.failed) {
@@ -314,11 +314,14 @@ struct NoEarlyExit {
 // only needs a decision valid for every sum within the rounding bounds of
 // both summation orders can skip the exact walk.
 template <int NT, class XF, class Early = NoEarlyExit>
-__device__ __attribute__((noinline)) float team_seq(Team &tm, Lds &tl, const XF &xf, long long n, bool cdf, float r,
+__device__ __attribute__((noinline)) float team_seq(Team &team_ref, Lds &tl, const XF &xf, long long n, bool cdf, float r,
                           seq::Shared<NT> &sh, long long *idx, const Early &early = Early()) {
   using namespace seq;
   constexpr int TILE = Shared<NT>::kTile;
   constexpr int BLK = Shared<NT>::kBlock;
+  // a copy in registers: the caller's object is in its stack, which every
+  // store through a generic pointer could alias (each use would reload it)
+  Team tm = team_ref;
   const int tid = (int)threadIdx.x, wave = tid >> 6;
   const unsigned tag = ++tm.pass;  // the workspace starts at zero: 0 is never a tag
   const long long L = ((n + tm.G - 1) / tm.G + TILE - 1) / TILE * TILE;
@@ -353,6 +356,8 @@ __device__ __attribute__((noinline)) float team_seq(Team &tm, Lds &tl, const XF 
     if (early(tot, depth)) {
       if (idx) *idx = -1;
       __syncthreads();
+      team_ref.nb = tm.nb;
+      team_ref.pass = tm.pass;
       return -1.0f;
     }
   }
@@ -434,6 +439,8 @@ __device__ __attribute__((noinline)) float team_seq(Team &tm, Lds &tl, const XF 
   }
   if (idx) *idx = found;
   __syncthreads();
+  team_ref.nb = tm.nb;
+  team_ref.pass = tm.pass;
   return s;
 }
 

@@ -479,8 +479,9 @@ __device__ __forceinline__ void rslice(const Args &a, const team::Team &tm, long
 // statistics are reduced over the team into sm.stat; convert_share turns the
 // share into probabilities when a pass first needs them.  Ends with a
 // barrier.
-__device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team &tm, SmemR &sm,
+__device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team &team_ref, SmemR &sm,
                                                      const float *t, const float *d) {
+  team::Team tm = team_ref;  // a register copy (see team_seq_r)
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int tid = threadIdx.x;
   long long lo;
@@ -564,6 +565,7 @@ __device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team 
   }
   if (want) sm.raw[tid] = raw;
   if (lg) team_combine_stats(a, tm, sm, block_ms2(mt, st, md, sd, sm.red, c));
+  team_ref.nb = tm.nb;
   __syncthreads();
 }
 
@@ -676,11 +678,14 @@ __device__ void sweep_share(SmemR &sm, bool resid, long long blk0, bool cdf, flo
 // the first index i with r <= s_i, or -1), with the same early exit.  Every
 // thread of every member calls it with the same arguments.
 template <class Early = team::NoEarlyExit>
-__device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team &tm, SmemR &sm,
+__device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team &team_ref, SmemR &sm,
                                                       bool resid, bool cdf, float r,
                                                       long long *idx,
                                                       const Early &early = Early()) {
   using namespace seq;
+  // a copy in registers: the caller's object is in its stack, which every
+  // store through a generic pointer could alias (each use would reload it)
+  team::Team tm = team_ref;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const unsigned tag = ++tm.pass;  // the workspace starts at zero: 0 is never a tag
   long long lo;
@@ -711,6 +716,8 @@ __device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team 
     // waves; then the G members
     if (early(tot, (kRTile + 6 + kNT / 64 + 1) + tm.G)) {
       if (idx) *idx = -1;
+      team_ref.nb = tm.nb;
+      team_ref.pass = tm.pass;
       __syncthreads();
       return -1.0f;
     }
@@ -890,6 +897,8 @@ __device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team 
   }
   (void)n;
   if (idx) *idx = found;
+  team_ref.nb = tm.nb;
+  team_ref.pass = tm.pass;
   __syncthreads();
   return s;
 }
