@@ -498,18 +498,6 @@ __device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team 
     const float ms = (m == -INFINITY) ? 0.0f : m;
     s += __builtin_amdgcn_exp2f((v - ms) * c);
   };
-  // four values at once: one maximum, at most one rescale, four independent
-  // exponentials
-  auto upd4 = [c](float &m, float &s, f32x4 v) {
-    const float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
-    if (mx > m) {
-      s *= __builtin_amdgcn_exp2f((m - mx) * c);
-      m = mx;
-    }
-    const float ms = (m == -INFINITY) ? 0.0f : m;
-    s += (__builtin_amdgcn_exp2f((v[0] - ms) * c) + __builtin_amdgcn_exp2f((v[1] - ms) * c)) +
-         (__builtin_amdgcn_exp2f((v[2] - ms) * c) + __builtin_amdgcn_exp2f((v[3] - ms) * c));
-  };
   constexpr int U = kLCap / (4 * kNT);  // 16-byte vectors per thread and row
   // thread c < N: the raw values of the two rows at child c's token (an
   // invalid token reads index 0), issued behind the share's loads
@@ -536,14 +524,31 @@ __device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team 
       raw = make_float2(((const float __attribute__((address_space(1))) *)t)[xs],
                         ((const float __attribute__((address_space(1))) *)d)[xs]);
     }
+    // the thread's maxima first, then its sums of exponentials against them
+    // (no rescaling on the way)
+    auto max4 = [](f32x4 v) { return fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])); };
+    auto ex4 = [c](f32x4 v, float m) {
+      return (__builtin_amdgcn_exp2f((v[0] - m) * c) + __builtin_amdgcn_exp2f((v[1] - m) * c)) +
+             (__builtin_amdgcn_exp2f((v[2] - m) * c) + __builtin_amdgcn_exp2f((v[3] - m) * c));
+    };
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int i = tid + u * kNT;  // vector i: chunk i % 4 of tile i / 4
       *lds4(sm.P + chunk_off(i >> 2, i & 3)) = vt[u];
       if (d) *lds4(sm.Q + chunk_off(i >> 2, i & 3)) = vd[u];
-      if (lg && i < n4) {  // the two rows' chains interleave
-        upd4(mt, st, vt[u]);
-        if (d) upd4(md, sd, vd[u]);
+      if (i < n4) {
+        mt = fmaxf(mt, max4(vt[u]));
+        if (d) md = fmaxf(md, max4(vd[u]));
+      }
+    }
+    if (lg) {
+      const float bt = (mt == -INFINITY) ? 0.0f : mt, bd = (md == -INFINITY) ? 0.0f : md;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (tid + u * kNT < n4) {  // the two rows' sums interleave
+          st += ex4(vt[u], bt);
+          if (d) sd += ex4(vd[u], bd);
+        }
       }
     }
   } else {
