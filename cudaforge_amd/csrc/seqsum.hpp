@@ -258,6 +258,36 @@ __device__ __forceinline__ int trailing_ones(unsigned long long m) {
   return inv ? (int)__builtin_ctzll(inv) : 64;
 }
 
+// The reference's sequential fp32 adds of 16 values x >= 0 to s and, in CDF
+// mode, the first k with r <= the running value after x[k] (-1: none).  The
+// adds form one dependent chain with nothing else on it; the running value
+// never decreases, so the hit is searched only when the last partial sum
+// reaches r (static indices: a dynamically indexed array would live in
+// scratch).
+__device__ __forceinline__ int replay16(const float (&x)[16], float &s, bool cdf, float r) {
+  float ps[16];
+  float acc = s;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    acc = acc + x[k];
+    ps[k] = acc;
+  }
+  if (cdf && r <= acc) {
+    int k = 15;
+    float sk = ps[15];
+#pragma unroll
+    for (int q = 14; q >= 0; --q) {
+      const bool h = r <= ps[q];
+      k = h ? q : k;
+      sk = h ? ps[q] : sk;
+    }
+    s = sk;
+    return k;
+  }
+  s = acc;
+  return -1;
+}
+
 // Serial replay of one 16-element tile (all lanes redundantly; the four
 // 16-byte LDS reads are broadcasts and are issued before the dependent adds).
 template <int NT>
@@ -273,16 +303,8 @@ __device__ long long serial_tile(const Shared<NT> &sh, int tile, float &s, bool 
     x[4 * k + 2] = q.z;
     x[4 * k + 3] = q.w;
   }
-  long long hit = -1;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const float t = s + x[k];
-    if (hit < 0) {
-      s = t;
-      if (cdf && r <= s) hit = blk0 + (long long)tile * Shared<NT>::kTile + k;
-    }
-  }
-  return hit;
+  const int k = replay16(x, s, cdf, r);
+  return k < 0 ? -1 : blk0 + (long long)tile * Shared<NT>::kTile + k;
 }
 
 // Walk `count` items (tiles of one wave, or the waves of a block) from the

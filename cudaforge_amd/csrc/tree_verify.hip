@@ -633,18 +633,13 @@ __device__ __forceinline__ void share_vals(const SmemR &sm, bool resid, int tile
 __device__ long long serial_tile_r(const SmemR &sm, bool resid, int tile, float &s, bool cdf,
                                    float r, long long blk0) {
   const int j = phys(tile * kRTile + (seq::lane_id() & (kRTile - 1)));
-  const float x = resid ? relu_ref(lds1(sm.P + j) - lds1(sm.Q + j)) : lds1(sm.P + j);
-  long long hit = -1;
+  const float v = resid ? relu_ref(lds1(sm.P + j) - lds1(sm.Q + j)) : lds1(sm.P + j);
+  float x[kRTile];
 #pragma unroll
-  for (int k = 0; k < kRTile; ++k) {
-    const float xk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
-    const float t = s + xk;
-    if (hit < 0) {
-      s = t;
-      if (cdf && r <= s) hit = blk0 + (long long)tile * kRTile + k;
-    }
-  }
-  return hit;
+  for (int k = 0; k < kRTile; ++k)
+    x[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), k));
+  const int k = seq::replay16(x, s, cdf, r);
+  return k < 0 ? -1 : blk0 + (long long)tile * kRTile + k;
 }
 
 // Walk this member's share exactly from sm.s (wave 0 executes, as
@@ -862,18 +857,13 @@ __device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team 
     } else if (fj.w == 2u && run(Inc{fj.x, fj.y}, (int)fj.z, snext) && !(cdf && r <= snext)) {
       // run 0 applied; the break tile serially, then run 1
       const int brk = (int)sm.rec[j][3];
-      long long hit = -1;
+      float x[kRTile];
 #pragma unroll
-      for (int k = 0; k < kRTile; ++k) {
-        const float t = snext + u2f(sm.rec[j][4 + k]);
-        if (hit < 0) {
-          snext = t;
-          if (cdf && r <= snext) hit = (long long)j * L + (long long)brk * kRTile + k;
-        }
-      }
-      if (hit >= 0) {  // the draw lands in the break tile
+      for (int k = 0; k < kRTile; ++k) x[k] = u2f(sm.rec[j][4 + k]);
+      const int k = seq::replay16(x, snext, cdf, r);
+      if (k >= 0) {  // the draw lands in the break tile
         s = snext;
-        found = hit;
+        found = (long long)j * L + (long long)brk * kRTile + k;
         break;
       }
       applies = run(Inc{sm.rec[j][0], sm.rec[j][1]}, (int)sm.rec[j][2], snext) &&
