@@ -315,7 +315,7 @@ struct NoEarlyExit {
 // both summation orders can skip the exact walk.
 template <int NT, class XF, class Early = NoEarlyExit>
 __device__ __attribute__((noinline)) float team_seq(Team &team_ref, Lds &tl, const XF &xf, long long n, bool cdf, float r,
-                          seq::Shared<NT> &sh, long long *idx, const Early &early = Early()) {
+                          seq::Shared<NT> &sh, long long *idx, Early early = Early()) {
   using namespace seq;
   constexpr int TILE = Shared<NT>::kTile;
   constexpr int BLK = Shared<NT>::kBlock;

@@ -125,11 +125,15 @@ __device__ __forceinline__ float f32_up(double v) {
 // r^(k+1)(x) = max(0, r^(k)(x) - q(x)) / S, does not increase with S, so if
 // its uniform passes at the largest S (and the <= 1e-6 fallback is excluded)
 // it is accepted whatever the exact S is: the exact walk is skipped.
+// (A handful of scalars, passed by value: a larger functor would be passed
+// through scratch memory.)
 struct SiblingAccepts {
-  Resid r;  // r^(k)
-  float2 raw;  // the sibling token's raw (target, draft) values
+  float p;  // r^(k) at the sibling's token
+  float q;  // the draft probability there
   float u;  // its uniform
   long long n;
+  __device__ SiblingAccepts(const Resid &r, float2 raw, float u_, long long n_)
+      : p(r.eval(raw)), q(r.d.eval(raw.y)), u(u_), n(n_) {}
   __device__ bool operator()(float Sb, int depth) const {
     const double u24 = 5.9604644775390625e-08;
     const double gn = (double)n * u24 / (1.0 - (double)n * u24);
@@ -138,8 +142,6 @@ struct SiblingAccepts {
     const float lo = f32_down((double)Sb * (1.0 - gn) / (1.0 + gd));
     const float hi = f32_up((double)Sb * (1.0 + gn) / (1.0 - gd));
     if (!(lo > 1e-6f) || !(hi < INFINITY)) return false;
-    const float p = r.eval(raw);
-    const float q = r.d.eval(raw.y);
     const float ratio = ratio_cpp(relu_ref(p - q) / hi, q);
     return u <= ratio;
   }
@@ -155,10 +157,11 @@ struct __align__(16) Smem {
   int path[kMaxN];
   float4 stat;  // (max, 1/sum) of the target and the draft row
   int amax;
-  unsigned long long kids;
+  unsigned long long kidm[kMaxN];  // children of each node (bit c: node c)
   float2 raw[kMaxN];  // (target, draft) raw values of the current node's rows at each child's token
   float uni[kMaxU];   // the sequence's uniforms (the first kMaxU)
   Args args;          // the launch arguments (stage_args)
+  team::Team team;    // this member's team (in LDS, so that no call site keeps it in scratch)
 };
 
 __device__ __forceinline__ const float *trow(const Args &a, int b, int n) {
@@ -298,7 +301,8 @@ __device__ __attribute__((noinline)) float4 slice_ms2(const Args &a, const float
 // rescaled sums in member order): sm.stat = (M_t, 1/S_t, M_d, 1/S_d).  Ends
 // with a barrier.
 template <class SM>
-__device__ void team_combine_stats(const Args &a, team::Team &tm, SM &sm, float4 p) {
+__device__ void team_combine_stats(const Args &a, team::Team &team_ref, SM &sm, float4 p) {
+  team::Team tm = team_ref;  // a register copy (see team_seq_r)
   team::exchange(tm, sm.tl, team::f4u(p));
   if (threadIdx.x == 0) {
     // the team maximum, then each member's sum rescaled to it, in member order
@@ -316,6 +320,7 @@ __device__ void team_combine_stats(const Args &a, team::Team &tm, SM &sm, float4
     }
     sm.stat = make_float4(Mt, 1.0f / St, Md, 1.0f / Sd);
   }
+  team_ref.nb = tm.nb;
   __syncthreads();
 }
 
@@ -350,8 +355,9 @@ __device__ void write_probs(const Args &a, const team::Team &tm, const Dist &d, 
 // First index of the largest probability (std::max_element) over the team:
 // this member scans [lo, hi), val(i) the probability of index i.
 template <class SM, class Val>
-__device__ int team_argmax(const Args &a, team::Team &tm, SM &sm, long long lo, long long hi,
+__device__ int team_argmax(const Args &a, team::Team &team_ref, SM &sm, long long lo, long long hi,
                            const Val &val) {
+  team::Team tm = team_ref;  // a register copy (see team_seq_r)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
@@ -405,6 +411,7 @@ __device__ int team_argmax(const Args &a, team::Team &tm, SM &sm, long long lo, 
     }
     sm.amax = (ix == 0x7fffffff) ? 0 : ix;
   }
+  team_ref.nb = tm.nb;
   __syncthreads();
   return sm.amax;
 }
@@ -444,10 +451,11 @@ struct __align__(16) SmemR {
   int path[kMaxN];
   float4 stat;
   int amax;
-  unsigned long long kids;
+  unsigned long long kidm[kMaxN];  // children of each node (bit c: node c)
   float2 raw[kMaxN];
   float uni[kMaxU];
   Args args;
+  team::Team team;
 };
 
 // Share layout: element e of a share sits in tile e / 16, and the tile's
@@ -480,7 +488,8 @@ __device__ __forceinline__ void rslice(const Args &a, const team::Team &tm, long
 // share into probabilities when a pass first needs them.  Ends with a
 // barrier.
 __device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team &team_ref, SmemR &sm,
-                                                     const float *t, const float *d) {
+                                                     const float *t, const float *d,
+                                                     unsigned long long kids) {
   team::Team tm = team_ref;  // a register copy (see team_seq_r)
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int tid = threadIdx.x;
@@ -501,7 +510,7 @@ __device__ __attribute__((noinline)) void load_rows_r(const Args &a, team::Team 
   constexpr int U = kLCap / (4 * kNT);  // 16-byte vectors per thread and row
   // thread c < N: the raw values of the two rows at child c's token (an
   // invalid token reads index 0), issued behind the share's loads
-  const bool want = d && tid < a.N && ((sm.kids >> tid) & 1ull);
+  const bool want = d && tid < a.N && ((kids >> tid) & 1ull);
   float2 raw = make_float2(0.0f, 0.0f);
   if (a.vec) {
     // n % 4 == 0 (V % 4 == 0 and lo % 16 == 0); every load issued before
@@ -681,7 +690,7 @@ template <class Early = team::NoEarlyExit>
 __device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team &team_ref, SmemR &sm,
                                                       bool resid, bool cdf, float r,
                                                       long long *idx,
-                                                      const Early &early = Early()) {
+                                                      Early early = Early()) {
   using namespace seq;
   // a copy in registers: the caller's object is in its stack, which every
   // store through a generic pointer could alias (each use would reload it)
@@ -892,6 +901,8 @@ __device__ __attribute__((noinline)) float team_seq_r(const Args &a, team::Team 
   }
   (void)n;
   if (idx) *idx = found;
+  __syncthreads();  // every thread has read sm.found above
+  if (tid == 0) sm.found = found;  // the CDF hit, for callers that read it from LDS
   team_ref.nb = tm.nb;
   team_ref.pass = tm.pass;
   __syncthreads();
@@ -944,20 +955,21 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, SM &sm, int b) {
   if (Ug)
     for (int i = tid; i < min(a.n_u, kMaxU); i += kNT) sm.uni[i] = Ug[i];
   __syncthreads();
+  // children of every node (bit c of kidm[n]: parent[c] = n with n < c)
+  if (tid < N) sm.kidm[tid] = 0ull;
+  __syncthreads();
+  if (tid > 0 && tid < N) {
+    const int pc = sm.par[tid];
+    if (pc >= 0 && pc < tid) atomicOr(&sm.kidm[pc], 1ull << tid);
+  }
+  __syncthreads();
   // draw i: from LDS when staged
   auto U_at = [&](int i) -> float { return i < kMaxU ? sm.uni[i] : Ug[i]; };
   int node = 0, len = 1, draws = 0, fin = -1, eos_acc = 0, status = 0;
   for (;;) {
     // children of `node`, in increasing index order
-    unsigned long long kids = 0;
-    {
-      const bool is_kid = (tid < N) && (tid > node) && sm.par[tid] == node;
-      const unsigned long long m = __ballot(is_kid);  // wave 0 holds every node (N <= 64)
-      if (tid == 0) sm.kids = m;
-      __syncthreads();
-      kids = sm.kids;
-      __syncthreads();
-    }
+    const unsigned long long kids = sm.kidm[node];
+    __syncthreads();  // every wave is done with the previous node's sm.raw and sm.stat
     const bool leaf = kids == 0;
     const float *tr = trow(a, b, node);
     const float *dr = (leaf || a.greedy) ? nullptr : drow(a, b, node);
@@ -980,7 +992,7 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, SM &sm, int b) {
       }
     };
     if constexpr (RES) {
-      load_rows_r(a, tm, sm, tr, dr);
+      load_rows_r(a, tm, sm, tr, dr, kids);
     } else {
       if (a.logits) team_stats(a, tm, sm, tr, dr);
       else __syncthreads();
@@ -1021,7 +1033,8 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, SM &sm, int b) {
         long long idx = -1;
         if constexpr (RES) {
           ensure_probs();
-          team_seq_r(a, tm, sm, false, true, U_at(draws++), &idx);
+          team_seq_r(a, tm, sm, false, true, U_at(draws++), nullptr);
+          idx = sm.found;  // the hit, as team_seq_r left it in LDS
         } else {
           team::team_seq<kNT>(tm, sm.tl, Resid{t, t, sm.Slist, 0}, V, true, U_at(draws++),
                               sm.seq, &idx);
@@ -1109,7 +1122,8 @@ __device__ void walk_sequence(const Args &a, team::Team &tm, SM &sm, int b) {
         long long idx = -1;
         if constexpr (RES) {
           ensure_probs();
-          team_seq_r(a, tm, sm, false, true, U_at(draws++), &idx);
+          team_seq_r(a, tm, sm, false, true, U_at(draws++), nullptr);
+          idx = sm.found;  // the hit, as team_seq_r left it in LDS
         } else {
           team::team_seq<kNT>(tm, sm.tl, Resid{t, d, sm.Slist, k}, V, true, U_at(draws++),
                               sm.seq, &idx);
@@ -1167,10 +1181,15 @@ template <bool RES, class SM>
 __device__ __forceinline__ void tree_verify_body(SM &sm) {
   const Args &a = stage_args(sm);
   const int team_id = (int)blockIdx.x / a.G;
-  if (threadIdx.x == 0) sm.tl.failed = 0;
+  if (threadIdx.x == 0) {
+    sm.tl.failed = 0;
+    sm.team = team::Team{a.teams + team_id, a.err, (int)blockIdx.x % a.G, a.G, 0u, 0u};
+  }
   __syncthreads();
   if (team_id >= a.T) return;
-  team::Team tm{a.teams + team_id, a.err, (int)blockIdx.x % a.G, a.G, 0u, 0u};
+  // Functions that exchange work on a register copy and store the
+  // exchange and pass counts back before their last barrier.
+  team::Team &tm = sm.team;
   for (int b = team_id; b < a.B; b += a.T) {
     walk_sequence<RES>(a, tm, sm, b);
     __syncthreads();
