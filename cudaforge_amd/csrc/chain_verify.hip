@@ -135,8 +135,35 @@ __device__ __forceinline__ const float *row_ptr(const Args &a, int b, int j) {
 }
 
 // (max, 1/S) of row r from its slices' partials, combined in slice order
-// (the same for whichever pass computed the row).
+// (the same for whichever pass computed the row).  Up to kFastS slices
+// (every row at C2 has 2) the partials load in one round before any use;
+// the arithmetic is the same, in the same order, either way.
+constexpr int kFastS = 4;
+struct RowParts {
+  float2 p[kFastS];
+};
+__device__ __forceinline__ void row_parts_load(const Args &a, int r, RowParts &q) {
+#pragma unroll
+  for (int w = 0; w < kFastS; ++w)
+    if (w < a.S) q.p[w] = a.part[(long long)r * a.S + w];
+}
+__device__ __forceinline__ float2 row_parts_stat(const Args &a, const RowParts &q) {
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kFastS; ++w)
+    if (w < a.S) M = fmaxf(M, q.p[w].x);
+  float S = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kFastS; ++w)
+    if (w < a.S) S += (q.p[w].x == M) ? q.p[w].y : q.p[w].y * __builtin_amdgcn_exp2f((q.p[w].x - M) * a.c);
+  return make_float2(M, 1.0f / S);
+}
 __device__ float2 row_stat(const Args &a, int r) {
+  if (a.S <= kFastS) {
+    RowParts q;
+    row_parts_load(a, r, q);
+    return row_parts_stat(a, q);
+  }
   const float2 *p = a.part + (long long)r * a.S;
   float M = -INFINITY;
   for (int w = 0; w < a.S; ++w) M = fmaxf(M, p[w].x);
@@ -237,6 +264,46 @@ __device__ __forceinline__ bool head_accepts(const Args &a, int ub, int i) {
   const float qd = __builtin_amdgcn_exp2f((a.rawtok[rd] - sd.x) * a.c) * sd.y;
   const bool valid = traw >= 0 && traw < a.V;
   return valid && u <= ratio_cpp(pt, qd) && traw != a.eos;
+}
+
+// Whether row group ub accepted every head position (head_accepts for each,
+// the same operations in the same order): with P <= kFastP and S <= kFastS
+// every load of the test is issued before the first use, one round of
+// loads instead of a round trip per position and slice.
+constexpr int kFastP = 3;
+__device__ bool head_all_accept(const Args &a, int ub) {
+  if (a.P > kFastP || a.S > kFastS) {
+    bool ok = true;
+    for (int i = 0; i < a.P; ++i) ok &= head_accepts(a, ub, i);
+    return ok;
+  }
+  RowParts qt[kFastP], qd[kFastP];
+  float rt[kFastP], rd[kFastP], u[kFastP];
+  int tk[kFastP];
+#pragma unroll
+  for (int i = 0; i < kFastP; ++i) {
+    if (i < a.P) {
+      const int r_t = ub * a.rpb + i, r_d = ub * a.rpb + a.K + 1 + i;
+      row_parts_load(a, r_t, qt[i]);
+      row_parts_load(a, r_d, qd[i]);
+      rt[i] = a.rawtok[r_t];
+      rd[i] = a.rawtok[r_d];
+      tk[i] = a.tokens[(long long)ub * a.K + i];
+      u[i] = a.U[(long long)ub * a.ustride + i];
+    }
+  }
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < kFastP; ++i) {
+    if (i < a.P) {
+      const float2 st = row_parts_stat(a, qt[i]), sd = row_parts_stat(a, qd[i]);
+      const float pt = __builtin_amdgcn_exp2f((rt[i] - st.x) * a.c) * st.y;
+      const float q = __builtin_amdgcn_exp2f((rd[i] - sd.x) * a.c) * sd.y;
+      const bool valid = tk[i] >= 0 && tk[i] < a.V;
+      ok &= valid && u[i] <= ratio_cpp(pt, q) && tk[i] != a.eos;
+    }
+  }
+  return ok;
 }
 
 // Whether row group ub accepted every head position, i.e. needs its tail
@@ -361,11 +428,7 @@ __global__ __launch_bounds__(NT) void stats_tail_kernel(Args a) {
   for (int g0 = 0; g0 < groups; g0 += NT) {
     const int ub = g0 + (int)threadIdx.x;
     bool need = ub < groups;
-    if (need) {
-      bool ok = true;  // every position's loads issued together
-      for (int i = 0; i < a.P; ++i) ok &= head_accepts(a, ub, i);
-      need = ok;
-    }
+    if (need) need = head_all_accept(a, ub);
     const unsigned long long m = __ballot(need);
     if (lane == 0) wcnt[wave] = (int)__popcll(m);
     __syncthreads();

@@ -276,3 +276,47 @@ def test_two_pass_statistics_match_one_pass(device, case):
         assert (one.eos.cpu().numpy()[::2] == 1).all()
     if case == "c2":  # both outcomes present: sequences stopped in the head and ones that went on
         assert (n < 3).any() and (n >= 3).any()
+
+
+def test_workspace_reuse_and_graph_replays(device):
+    """The pipeline keeps state between its kernels in the workspace (the
+    look-back words and cache counters, zeroed by the first statistics pass,
+    the records, the jobs) and needs none of it to survive a call.  A call
+    captured in a graph and replayed with new inputs copied in between, with
+    eager calls on the same workspace interleaved, equals an eager call on a
+    fresh workspace each time, and the outcomes differ between the input
+    sets (so a replay that reused stale state would show)."""
+    T, B, K, V = 0.7, 64, 8, 128256
+    sets = [c2_inputs(seed=s, B=B, K=K, V=V, temperature=T) for s in (201, 202)]
+    sets.append(sets[0][:1] + (sets[0][0][:, :-1].copy(),) + sets[0][2:])  # draft = target: all accept
+    kw = dict(input_kind="logits", temperature=T, mode="cpp", eos_token_id=-1)
+    t_d, d_d, tok_d, U_d = _to_dev(device, *sets[0])
+    from cudaforge_amd.verify import chain_workspace_bytes
+    ws = torch.empty(chain_workspace_bytes(B, K, V, "logits", "cpp"), dtype=torch.uint8, device=device)
+    ws.fill_(0xA5)  # foreign contents
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):  # warm-up outside the capture, as torch requires
+        chain_verify(t_d, d_d, tok_d, U_d, workspace=ws, **kw)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = chain_verify(t_d, d_d, tok_d, U_d, workspace=ws, **kw)
+    seen = []
+    for rep in range(7):
+        src = sets[rep % 3]
+        for dst, a in zip((t_d, d_d, tok_d, U_d), src):
+            dst.copy_(torch.from_numpy(np.ascontiguousarray(a)))
+        g.replay()
+        torch.cuda.synchronize()
+        got = _chain_outputs(out)
+        ref = _chain_outputs(chain_verify(t_d, d_d, tok_d, U_d, **kw))
+        for a, b in zip(got, ref):
+            np.testing.assert_array_equal(a, b, err_msg=f"replay {rep}")
+        if rep % 2:  # an eager call on the graph's workspace between replays
+            eager = _chain_outputs(chain_verify(t_d, d_d, tok_d, U_d, workspace=ws, **kw))
+            for a, b in zip(eager, ref):
+                np.testing.assert_array_equal(a, b, err_msg=f"eager after replay {rep}")
+        seen.append(got[0].copy())
+    assert not np.array_equal(seen[0], seen[1]) and (seen[2] == K).all()
