@@ -570,9 +570,9 @@ def main() -> int:
 
     kern = {}
     for name in ("chain_stats_head", "chain_stats_tail", "chain_decide", "chain_plan",
-                 "chain_mw_first", "chain_mw_records", "chain_mw_walk", "chain_finish"):
+                 "chain_mw_first", "chain_mw_tail", "chain_finish"):
         n, ms = _lib.profile_query(name)
-        kern[name] = ms / args.steps  # per step (records and walk run twice)
+        kern[name] = ms / args.steps  # per step
     _lib.profile_reset()
     # the statistics passes: the logits of their rows, each read once
     stats_bytes = sum(rows[i % NSETS] for i in range(args.steps)) / args.steps * V * 4

@@ -119,6 +119,7 @@ struct Args {
   MwBad *bad;             // [2, B, kMwMaxBad]
   float *x0;              // [2, B, kMwChunk] chunk 0's element values per pass
   unsigned long long *flags;  // [B, NC] look-back words of the first exact pass
+  unsigned long long *tsync;  // [B, 2] mw_tail_kernel: S published, CDF shares done
   int mw_reset;           // the first statistics pass zeroes flags and badcnt
   float *rawtok;          // [R] head pass: a row's raw logit at its position's draft token
   int32_t *out_accept_len, *out_tokens, *out_num_emitted, *out_final, *out_eos;
@@ -810,26 +811,25 @@ __global__ __launch_bounds__(256) void plan_kernel(Args a) {
 // ---------------------------------------------------------------------------
 // Exact draw over all work-groups ("mw").  A row is cut into chunks of 1024
 // elements (64 tiles of 16, one wave per chunk).  For each drawing sequence:
-//   sums    (grid NC/4 x B)  approximate fp32 chunk sums of the residual and
-//                            of the target row, used only to guess regions;
-//   records (grid NC/4 x B)  per pass: every tile quantised in its guessed
-//                            region (seqsum.hpp); per chunk, the composed
-//                            function of the tiles before its first break
-//                            (a tile straddling a region boundary, or a
-//                            region change), the break, and the function of
-//                            the tiles after it; tiles that will need a
-//                            serial replay are cached;
-//   walk    (grid B, 1 wave) per pass: chunk 0, where the running value is
-//                            small and crosses a binade every doubling, is
-//                            walked tile by tile from its records (mw_records
-//                            also stores all its values, so the straddling
-//                            tiles replay from LDS); later chunks apply their
-//                            functions from the exact running value, and a
-//                            chunk with a break costs a check, the break
-//                            tile's serial replay and a second check.  Any
-//                            check that fails (a wrong guess, a second
-//                            break, a CDF hit inside a run) falls back to the
-//                            tile-level walk of seq::walk.
+//   sums     approximate fp32 chunk sums of the residual and of the target
+//            row, used only to guess regions;
+//   records  per pass: every tile quantised in its guessed region
+//            (seqsum.hpp); per chunk, the composed function of the tiles
+//            before its first break (a tile straddling a region boundary, or
+//            a region change), the break, and the function of the tiles
+//            after it; tiles that will need a serial replay are cached;
+//   walk     per pass, one wave: chunk 0, where the running value is small
+//            and crosses a binade every doubling, is walked tile by tile
+//            from its records (the records also store all its values, so the
+//            straddling tiles replay from LDS); later chunks apply their
+//            functions from the exact running value, and a chunk with a
+//            break costs a check, the break tile's serial replay and a second
+//            check.  Any check that fails (a wrong guess, a second break, a
+//            CDF hit inside a run) falls back to the tile-level walk of
+//            seq::walk.
+// Two launches: mw_first_kernel (the decision, the sums and the sum pass's
+// records) and mw_tail_kernel (the sum pass's walk, the CDF pass's records
+// and walk, job by job).
 // Pass 0 sums max(0, t - d) (speculative.cpp:30-35); pass 1 searches the
 // inverse CDF of max(0, t - d) / S, or of t for a bonus draw or the
 // sum <= 1e-6 fallback (speculative.cpp:11-24, 37-45, 97).
@@ -1074,13 +1074,16 @@ __device__ __forceinline__ void mw_records_chunk(const Args &a, int b, int c, in
 }
 
 // Zeroes this work-group's share (work-group wg of nwg) of the first exact
-// pass's look-back words and of both passes' cache counters.  The first
-// kernel of every call that draws exactly runs this, so nothing in the
-// workspace has to start at zero.
+// pass's look-back words, of both passes' cache counters and of the tail
+// kernel's synchronisation words.  The first kernel of every call that draws
+// exactly runs this, so nothing in the workspace has to start at zero.
 __device__ void mw_reset_share(const Args &a, long long wg, long long nwg) {
   const long long nt = blockDim.x, i0 = wg * nt + threadIdx.x, step = nwg * nt;
   for (long long i = i0; i < (long long)a.B * a.NC; i += step) a.flags[i] = 0ull;
-  for (long long i = i0; i < 2LL * a.B; i += step) a.badcnt[i] = 0;
+  for (long long i = i0; i < 2LL * a.B; i += step) {
+    a.badcnt[i] = 0;
+    a.tsync[i] = 0ull;
+  }
 }
 
 __global__ __launch_bounds__(256) void mw_reset_kernel(Args a) {
@@ -1236,32 +1239,6 @@ __global__ __launch_bounds__(kMwNT) void mw_first_kernel(Args a, int decide) {
   mw_records_chunk(a, b, c0 + 1, kPassSum, j, E1, x[1]);
 }
 
-// One wave per chunk: chunk c = 4 * blockIdx.x + wave of job blockIdx.y.
-// (Two chunks per wave, as mw_first_kernel, made this pass slower: 18.4 ->
-// 21.7 us at C2; its waves are short, so the tail of late work-groups costs
-// less than a serial second chunk.)
-__global__ __launch_bounds__(kMwNT) void mw_records_kernel(Args a, int pass) {
-  // sequences vary fastest: the work-groups that start last, once the first
-  // ones end, hold the chunks nearest the row's end, which lie past the CDF
-  // hit (skipped at once) for most sequences
-  const int b = blockIdx.x;
-  const int c = blockIdx.y * (kMwNT / 64) + (threadIdx.x >> 6);
-  const MwJob j = a.jobs[b];
-  if (!mw_active(j, pass)) return;
-  if (c >= a.NC) return;
-  const MwElem e = mw_elem(a, b, j, pass);
-  const float *csum = (e.fn == 2 ? a.csum_t : a.csum_x) + (long long)b * a.NC;
-  float E0 = mw_entry_prefix(csum, c);
-  if (e.fn == 1) E0 = E0 / e.S;
-  if (mw_skip(pass, j, E0)) {
-    mw_write_skipped(a, (long long)pass * a.B + b, c);
-    return;
-  }
-  float x[kMwTile];
-  mw_tile_values(a, e, (long long)c * kMwChunkTiles + (threadIdx.x & 63), x);
-  mw_records_chunk(a, b, c, pass, j, E0, x);
-}
-
 constexpr int kMwWin = 256;  // chunk records staged in LDS at a time
 
 __device__ __forceinline__ void finish_one(const Args &a, int b, const MwJob &j, int idx,
@@ -1302,9 +1279,11 @@ __device__ __forceinline__ void wave_sync() {
 // synchronises only itself, so the other waves of its work-group can wait at
 // a barrier meanwhile.  Writes the pass's result (sum pass: S and the
 // fallback flag; CDF pass: the drawn index, and the outputs in cpp mode) and
-// returns the final running value.
+// returns the final running value.  use_cache = false ignores the cached
+// serial tiles (another work-group may still be filling a slot); the walk
+// then reads those tiles' values from the row.
 __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const MwJob &j,
-                                         const MwElem &e, MwWalkLds &L) {
+                                         const MwElem &e, MwWalkLds &L, bool use_cache = true) {
   using namespace seq;
   MwChunk *cr = L.cr;
   MwRec *tr = L.tr;
@@ -1318,7 +1297,7 @@ __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const M
 
   // One round of loads before the first wait: chunk 0's values and tile
   // records, the first window of chunk records, every cache slot (all
-  // written by mw_records for active jobs; in-bounds, unused otherwise) and
+  // written by the records for active jobs; in-bounds, unused otherwise) and
   // the cache count.
   {
     const float4 *src = reinterpret_cast<const float4 *>(a.x0 + rowrec * kMwChunk + lane * kMwTile);
@@ -1330,12 +1309,12 @@ __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const M
   for (int c = 1 + lane; c < min(a.NC, 1 + kMwWin); c += 64) cr[c - 1] = crec[c];
   static_assert(kMwMaxBad <= 64, "one cache slot per lane");
   bad[lane] = a.bad[rowrec * kMwMaxBad + lane];
-  const int nbad = min(a.badcnt[rowrec], kMwMaxBad);
+  const int nbad = use_cache ? min(a.badcnt[rowrec], kMwMaxBad) : 0;
   wave_sync();
   const bool cdf = (pass == kPassCdf);
   const float r = j.u;
 
-  // The first kMwPf chunks of the first window that the records kernel
+  // The first kMwPf chunks of the first window that the records
   // flagged `near`: lane p < npf holds the p-th one's index.  Their tile
   // records travel straight to LDS during the chunk-0 walk (which touches
   // no global memory), so a tile-level walk there costs no round trip.
@@ -1385,7 +1364,7 @@ __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const M
     s = acc;
     return -1;
   };
-  // values of tile `tile`: the cache when the records kernel stored them
+  // values of tile `tile`: the cache when the records stored them
   auto serial = [&](long long tile, float &s) -> long long {
     const int q = lane < nbad ? lane : 0;
     const unsigned long long m = __ballot(lane < nbad && bad[q].tile == (int)tile);
@@ -1548,16 +1527,153 @@ __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const M
   return s;
 }
 
-// One wave per job: the exact walk of one pass.
-__global__ __launch_bounds__(64) void mw_walk_kernel(Args a, int pass) {
+// Everything after the first exact pass, kMwTailWGs work-groups ("parts")
+// of kMwTailNT threads per job:
+//   1. part 0's wave 0 walks the sum pass (residual draws) and publishes S;
+//   2. every part writes its share of the CDF pass's records (chunk c goes
+//      to part (c / 16) % kMwTailWGs, wave c % 16), from entry values that
+//      one wave per part scans from the stored chunk sums once;
+//   3. the other parts report their shares done, and part 0's wave 0 walks
+//      the CDF pass.
+// A job's stages follow each other directly instead of in three launches
+// (walk, records, walk), each of which waited for the slowest job of the
+// previous one.
+//
+// S and the share counts cross work-groups (and XCDs) through agent-scope
+// atomics on a.tsync, zeroed by the first kernel of the call: polled with
+// relaxed loads, one release fence before each publication and one acquire
+// fence after each wait (an acquire per poll would invalidate the cache on
+// every poll).  The parts of a job take linear indices 8 apart, so that they
+// share an XCD when work-groups go to the 8 XCDs round-robin.  Every wait is
+// bounded, and none can cost correctness: a part that never sees S writes
+// nothing, and a walker that does not see every share done writes the
+// missing records itself -- the same values (the entry values come from the
+// stored chunk sums, not from timing), so a late part's writes change
+// nothing -- and then walks without the serial-tile cache, where a late part
+// could still be filling a slot.
+constexpr int kMwTailNT = 1024;
+constexpr int kMwTailWaves = kMwTailNT / 64;
+constexpr int kMwTailWGs = 4;
+constexpr long kMwTailSpins = 1l << 15;  // s_sleep(2) polls: about 2 ms
+constexpr unsigned long long kTsyncSet = 1ull << 63;  // a.tsync[2 b]: S is there
+
+__device__ __forceinline__ unsigned long long ts_load(unsigned long long *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Job b and part of linear work-group index L: groups of 8 jobs take
+// 8 * kMwTailWGs consecutive indices, the parts of one job 8 apart.
+__device__ __forceinline__ void mw_tail_ids(int L, int &b, int &part) {
+  const int grp = L / (8 * kMwTailWGs), w = L % (8 * kMwTailWGs);
+  b = grp * 8 + (w % 8);
+  part = w / 8;
+}
+
+__global__ __launch_bounds__(kMwTailNT) void mw_tail_kernel(Args a) {
   __shared__ MwWalkLds L;
-  const int b = blockIdx.x;
+  __shared__ float Es[kMwMaxNC];  // approximate chunk entry values (before the 1 / S)
+  __shared__ float sS;
+  __shared__ int sok;
+  int b, part;
+  mw_tail_ids(blockIdx.x, b, part);
+  if (b >= a.B) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const MwJob j = a.jobs[b];
-  if (!mw_active(j, pass)) {
-    if (pass == kPassCdf && a.mode == CFA_MODE_CPP && threadIdx.x == 0) finish_one(a, b, j, -1);
+  if (!mw_active(j, kPassCdf)) {
+    if (part == 0 && a.mode == CFA_MODE_CPP && threadIdx.x == 0) finish_one(a, b, j, -1);
     return;
   }
-  mw_walk(a, b, pass, j, mw_elem(a, b, j, pass), L);
+  const bool resid = j.kind == kResid;
+  // a wave that does not walk scans the chunk sums of the CDF pass's row
+  if (wave == 1) {
+    const float *csum = (resid ? a.csum_x : a.csum_t) + (long long)b * a.NC;
+    float carry = 0.0f;
+    for (int base = 0; base < a.NC; base += 64) {
+      const float v = (base + lane < a.NC) ? csum[base + lane] : 0.0f;
+      const float incl = seq::wave_incl_scan_f32(v);
+      if (base + lane < a.NC) Es[base + lane] = carry + (incl - v);
+      carry += __shfl(incl, 63, 64);
+    }
+  }
+  unsigned long long *ts = a.tsync + 2LL * b;
+  MwRes r{0.0f, 0, -1, -1};
+  if (resid) {
+    if (part == 0) {
+      if (wave == 0) {
+        const float S = mw_walk(a, b, kPassSum, j, mw_elem(a, b, j, kPassSum), L);
+        if (lane == 0) {
+          sS = S;
+          __hip_atomic_store(ts, kTsyncSet | f2u(S), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    } else if (threadIdx.x == 0) {
+      unsigned long long w = 0;
+      for (long n = 0; n < kMwTailSpins; ++n) {
+        w = ts_load(ts);
+        if (w & kTsyncSet) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      sok = (w & kTsyncSet) ? 1 : 0;
+      sS = u2f((uint32_t)w);
+    }
+    __syncthreads();
+    if (part != 0 && !sok) return;  // the walker writes this part's share
+    r.S = sS;
+    r.fallback = (r.S <= 1e-6f) ? 1 : 0;  // speculative.cpp:37, as the walk stores it
+  } else {
+    __syncthreads();  // Es
+  }
+  const MwElem e = mw_elem_r(a, b, j, kPassCdf, r);
+  // approximate entry value of chunk c on the CDF pass's scale (a residual
+  // job whose sum fell to the fallback draws from t: t's own chunk sums)
+  auto entry = [&](int c) -> float {
+    if (resid && e.fn == 2) return mw_entry_prefix(a.csum_t + (long long)b * a.NC, c);
+    return (e.fn == 1) ? Es[c] / e.S : Es[c];
+  };
+  // part p's share: chunks 16 p + wave, then every 16 kMwTailWGs further; a
+  // chunk surely past u gets a "skipped" record and no loads
+  auto share = [&](int p) {
+    for (int c = p * kMwTailWaves + wave; c < a.NC; c += kMwTailWGs * kMwTailWaves) {
+      const float E0 = entry(c);
+      if (mw_skip(kPassCdf, j, E0)) {
+        mw_write_skipped(a, (long long)kPassCdf * a.B + b, c);
+        continue;
+      }
+      float x[kMwTile];
+      mw_tile_values(a, e, (long long)c * kMwChunkTiles + lane, x);
+      mw_records_chunk(a, b, c, kPassCdf, j, E0, x);
+    }
+  };
+  share(part);
+  if (part != 0) {
+    // every wave's record stores complete, then one release for the part
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __hip_atomic_fetch_add(ts + 1, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long n = 0;
+    for (long k = 0; k < kMwTailSpins; ++k) {
+      n = ts_load(ts + 1);
+      if (n >= (unsigned long long)(kMwTailWGs - 1)) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    sok = (n >= (unsigned long long)(kMwTailWGs - 1)) ? 1 : 0;
+  }
+  __syncthreads();
+  const bool all_in = sok != 0;
+  if (!all_in) {
+    for (int p = 1; p < kMwTailWGs; ++p) share(p);
+    __syncthreads();
+  }
+  if (wave == 0) mw_walk(a, b, kPassCdf, j, e, L, all_in);
 }
 
 // ---------------------------------------------------------------------------
@@ -1797,7 +1913,7 @@ constexpr int kHeadPositions = 3;
 // Workspace layout (each region 256-byte aligned).
 struct WsLayout {
   size_t part, apart, rawtok, dec, ufin, jobs, res, csum_x, csum_t, crec, trec, badcnt, bad, x0, flags,
-      total;
+      tsync, total;
 };
 
 static WsLayout ws_layout(int B, int K, int V, int mode) {
@@ -1828,6 +1944,7 @@ static WsLayout ws_layout(int B, int K, int V, int mode) {
   L.bad = take(mw ? 2 * (size_t)B * kMwMaxBad * sizeof(MwBad) : 0);
   L.x0 = take(mw ? 2 * (size_t)B * kMwChunk * sizeof(float) : 0);
   L.flags = take(mw ? (size_t)B * NC * sizeof(unsigned long long) : 0);
+  L.tsync = take(2 * (size_t)B * sizeof(unsigned long long));
   L.total = o;
   return L;
 }
@@ -1945,8 +2062,10 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   a.bad = (MwBad *)(ws + L.bad);
   a.x0 = (float *)(ws + L.x0);
   a.flags = (unsigned long long *)(ws + L.flags);
-  // the first statistics pass zeroes the look-back words and cache counters;
-  // without one (probabilities input) a small kernel does
+  a.tsync = (unsigned long long *)(ws + L.tsync);
+  // the first statistics pass zeroes the look-back words, cache counters and
+  // tail synchronisation words; without one (probabilities input) a small
+  // kernel does
   a.mw_reset = (mode != CFA_MODE_GREEDY && a.logits) ? 1 : 0;
 
   if (mode != CFA_MODE_GREEDY && !a.logits) {
@@ -1988,12 +2107,10 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   if (!fused_decide) CFA_LAUNCH("chain_decide", decide_kernel, dim3(B), dim3(64), 0, st, a);
   if (mode != CFA_MODE_GREEDY) {
     const dim3 cg1((a.NC + kMwChunksPerWG - 1) / kMwChunksPerWG, B);   // two chunks per wave
-    const dim3 cg(B, (a.NC + kMwNT / 64 - 1) / (kMwNT / 64));              // one chunk per wave
+    const unsigned tail_wgs = (unsigned)(((B + 7) / 8) * 8 * kMwTailWGs);
     if (mode == CFA_MODE_PYTHON) CFA_LAUNCH("chain_plan", plan_kernel, dim3(1), dim3(256), 0, st, a);
     CFA_LAUNCH("chain_mw_first", mw_first_kernel, cg1, dim3(kMwNT), 0, st, a, fused_decide);
-    CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassSum);
-    CFA_LAUNCH("chain_mw_records", mw_records_kernel, cg, dim3(kMwNT), 0, st, a, (int)kPassCdf);
-    CFA_LAUNCH("chain_mw_walk", mw_walk_kernel, dim3(B), dim3(64), 0, st, a, (int)kPassCdf);
+    CFA_LAUNCH("chain_mw_tail", mw_tail_kernel, dim3(tail_wgs), dim3(kMwTailNT), 0, st, a);
     if (mode == CFA_MODE_PYTHON)
       CFA_LAUNCH("chain_pybonus", pybonus_kernel, dim3(B), dim3(kSampleNT), 0, st, a);
     if (mode == CFA_MODE_PYTHON)
