@@ -199,6 +199,57 @@ __device__ __forceinline__ void issue_tile(const Args &a, const long long *gtab,
   }
 }
 
+// One 16-byte-per-lane transfer with a wave-uniform 64-bit base (SGPRs) and
+// a per-lane 32-bit byte offset: no per-transfer address arithmetic on the
+// vector unit.
+__device__ __forceinline__ void dma16_s(const void *sbase, uint32_t voff, CFA_LDS void *lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory");
+}
+
+// Per-lane byte offsets, within their 16-key group, of this lane's K and V
+// transfers (issue_tile's rows and chunks) for a tile that lies wholly below
+// nkeys, where no position is clamped: the same for every such tile.
+template <int D>
+struct DmaOffs {
+  uint32_t k[8 / Geo<D>::kRowsPerLoad], v[8 / Geo<D>::kRowsPerLoad];
+};
+template <int D>
+__device__ __forceinline__ DmaOffs<D> dma_offsets(int wave, int lane) {
+  using Gm = Geo<D>;
+  constexpr int RPL = Gm::kRowsPerLoad;
+  const int sub = lane / Gm::kChunks, pc = lane % Gm::kChunks;
+  DmaOffs<D> o;
+#pragma unroll
+  for (int j = 0; j < 8 / RPL; ++j) {
+    const int R = 8 * wave + RPL * j + sub;
+    const int kin = k_key_of_row(R) - 32 * (wave >> 2) - 16 * (wave & 1);  // key in its group
+    o.k[j] = (uint32_t)((kin * D + (pc ^ k_swz<D>(R)) * 8) * 2);
+    const int key = 8 * wave + RPL * j + sub;
+    const int vin = key - 16 * (wave >> 1);
+    o.v[j] = (uint32_t)((vin * D + (pc ^ v_swz<D>(key)) * 8) * 2);
+  }
+  return o;
+}
+
+// issue_tile for a tile with kbase + 64 <= nkeys, from the precomputed
+// offsets: per transfer only the group's page base, which is uniform.
+template <int D>
+__device__ __forceinline__ void issue_tile_full(const Args &a, const long long *gtab, int g0, int kbase,
+                                                const DmaOffs<D> &off, uint8_t *kdst, uint8_t *vdst,
+                                                int wave) {
+  using Gm = Geo<D>;
+  constexpr int RPL = Gm::kRowsPerLoad;
+  const uint16_t *kb = a.kpool + uniform_i64(gtab[kbase / 16 + 2 * (wave >> 2) + (wave & 1) - g0]);
+  const uint16_t *vb = a.vpool + uniform_i64(gtab[kbase / 16 + (wave >> 1) - g0]);
+#pragma unroll
+  for (int j = 0; j < 8 / RPL; ++j)
+    dma16_s(kb, off.k[j], (CFA_LDS void *)(kdst + (8 * wave + RPL * j) * Gm::kRowBytes));
+#pragma unroll
+  for (int j = 0; j < 8 / RPL; ++j)
+    dma16_s(vb, off.v[j], (CFA_LDS void *)(vdst + (8 * wave + RPL * j) * Gm::kRowBytes));
+}
+
 // Visibility of the 64 keys kbase.. of a tile to a query whose ancestor mask
 // (bits < N) is anc: context positions (< ctx) are all visible, tree position
 // ctx + j is visible iff bit j of anc is set, positions past the tree never.
@@ -461,6 +512,15 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
     ln.vbase = vrow * Gm::kRowBytes + ((col >> 1) & 1) * 16 + (col & 1) * 8;
   }
 
+  // this wave's share of tile u: whole tiles from the fixed offsets, the
+  // last tile of the keys (clamped positions) through issue_tile
+  const DmaOffs<D> doff = dma_offsets<D>(wave, lane);
+  auto issue = [&](int u, uint8_t *kdst, uint8_t *vdst) {
+    if (u * kKT + kKT <= nkeys)
+      issue_tile_full<D>(a, gtab, g0, u * kKT, doff, kdst, vdst, wave);
+    else
+      issue_tile<D>(a, gtab, g0, u * kKT, nkeys, kdst, vdst, wave, lane);
+  };
   // the split's page lookups, once
   {
     const int32_t *btb = a.bt + (long long)b * a.max_blocks;
@@ -486,8 +546,7 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
 
   if (t0 < t1) {
     for (int u = t0; u < min(t0 + 3, t1); ++u)
-      issue_tile<D>(a, gtab, g0, u * kKT, nkeys, kring + ((u - t0) % kKStages) * kTileBytes,
-                 vring + ((u - t0) % kVStages) * kTileBytes, wave, lane);
+      issue(u, kring + ((u - t0) % kKStages) * kTileBytes, vring + ((u - t0) % kVStages) * kTileBytes);
     // tile t0 has landed once at most the other prologue tiles are in flight
     const int later = min(t0 + 3, t1) - 1 - t0;
     if (later >= 2) wait_vmcnt<2 * kLoadsPerTile>();
@@ -519,8 +578,7 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
         block_barrier();
         if (t + 3 < t1) {
           const int u = t + 3 - t0;
-          issue_tile<D>(a, gtab, g0, (t + 3) * kKT, nkeys, kring + (u % kKStages) * kTileBytes,
-                     vring + (u % kVStages) * kTileBytes, wave, lane);
+          issue(t + 3, kring + (u % kKStages) * kTileBytes, vring + (u % kVStages) * kTileBytes);
         }
       } else {
         if (t + 2 < t1) wait_vmcnt<kLoadsPerTile>();
@@ -528,8 +586,7 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
         block_barrier();
         if (t + 3 < t1) {
           const int u = t + 3 - t0;
-          issue_tile<D>(a, gtab, g0, (t + 3) * kKT, nkeys, kring + (u % kKStages) * kTileBytes,
-                     vring + (u % kVStages) * kTileBytes, wave, lane);
+          issue(t + 3, kring + (u % kKStages) * kTileBytes, vring + (u % kVStages) * kTileBytes);
         }
       }
       if (busy) valu_phase(ln, kbase, ctx, S, sm, o, lacc, P);
