@@ -294,7 +294,9 @@ def tree_attention_leg(dev, reps=20):
     def run():
         tree_attention(q, kp, vp, bt, ctx, mt, max_keys=C + N, out=out, workspace=ws)
 
-    for _ in range(3):
+    # steady state: the first few dozen calls of a process over these
+    # freshly allocated pools run up to 10% slower (82 -> 92 us per call)
+    for _ in range(40):
         run()
     ms = _time_launches(run, reps, ("tree_attn", "tree_attn_merge"))
     t = (ms["tree_attn"] + ms["tree_attn_merge"]) * 1e-3
