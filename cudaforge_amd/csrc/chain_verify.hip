@@ -120,6 +120,7 @@ struct Args {
   float *x0;              // [2, B, kMwChunk] chunk 0's element values per pass
   unsigned long long *flags;  // [B, NC] look-back words of the first exact pass
   unsigned long long *tsync;  // [B, 2] mw_tail_kernel: S published, CDF shares done
+  float *s0;              // [B] sum pass: the exact running value after chunk 0
   int mw_reset;           // the first statistics pass zeroes flags and badcnt
   float *rawtok;          // [R] head pass: a row's raw logit at its position's draft token
   int32_t *out_accept_len, *out_tokens, *out_num_emitted, *out_final, *out_eos;
@@ -973,9 +974,12 @@ __device__ __forceinline__ void mw_write_skipped(const Args &a, long long rowrec
 
 // Records of chunk c of job b for one pass, by one wave (lane = tile in the
 // chunk), from the chunk's approximate entry value E0 (on the pass's scale)
-// and the lane's 16 evaluated elements.
+// and the lane's 16 evaluated elements.  For chunk 0, tr_lds / xs_lds (if
+// given) also receive its tile records and values in LDS, for a walk of
+// chunk 0 by the same wave.
 __device__ __forceinline__ void mw_records_chunk(const Args &a, int b, int c, int pass,
-                                                 const MwJob &j, float E0, const float *x) {
+                                                 const MwJob &j, float E0, const float *x,
+                                                 MwRec *tr_lds = nullptr, float *xs_lds = nullptr) {
   using namespace seq;
   const int lane = threadIdx.x & 63;
   const long long rowrec = ((long long)pass * a.B + b);
@@ -1004,11 +1008,18 @@ __device__ __forceinline__ void mw_records_chunk(const Args &a, int b, int c, in
     ok = (f.e <= kUnitsTop) && (f.o <= kUnitsTop);
     if (!ok) f = Inc{kBad, kBad};
   }
-  trec[tile] = MwRec{f.e, f.o, ok ? r_lo : kAnyRegion, ok ? 0 : 1};
+  const MwRec rec_t{f.e, f.o, ok ? r_lo : kAnyRegion, ok ? 0 : 1};
+  trec[tile] = rec_t;
   if (c == 0) {  // chunk 0 is walked tile by tile: all its values go to the walk
     float4 *dst = reinterpret_cast<float4 *>(a.x0 + rowrec * kMwChunk + lane * kMwTile);
 #pragma unroll
     for (int k = 0; k < kMwTile; k += 4) dst[k / 4] = make_float4(x[k], x[k + 1], x[k + 2], x[k + 3]);
+    if (tr_lds != nullptr) {
+      tr_lds[lane] = rec_t;
+      float4 *dl = reinterpret_cast<float4 *>(xs_lds + lane * kMwTile);
+#pragma unroll
+      for (int k = 0; k < kMwTile; k += 4) dl[k / 4] = make_float4(x[k], x[k + 1], x[k + 2], x[k + 3]);
+    }
     return;
   }
   // Cache the values of the tiles the walk will probably replay serially: a
@@ -1153,6 +1164,95 @@ __device__ float mw_lookback(const Args &a, int b, int c, float own) {
   return pre;
 }
 
+// Orders one wave's LDS accesses (a wave's LDS operations complete in issue
+// order, so this only keeps the compiler from moving accesses across it).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Serial replay of a tile's 16 values x from s (CDF: first hit index, the
+// first i with r <= s_i, else -1).  The running value never decreases
+// (x >= 0), so the hit is searched only in a tile whose last partial sum
+// reaches r.
+__device__ __forceinline__ long long mw_replay16(const float *x, long long i0, float &s, bool cdf,
+                                                 float r) {
+  float ps[kMwTile];
+  float acc = s;
+#pragma unroll
+  for (int k = 0; k < kMwTile; ++k) {
+    acc = acc + x[k];
+    ps[k] = acc;
+  }
+  if (cdf && r <= acc) {
+    // static indices only: a dynamically indexed ps[] would live in scratch
+    int k = kMwTile - 1;
+    float sk = ps[kMwTile - 1];
+#pragma unroll
+    for (int q = kMwTile - 2; q >= 0; --q) {
+      const bool h = r <= ps[q];
+      k = h ? q : k;
+      sk = h ? ps[q] : sk;
+    }
+    s = sk;
+    return i0 + k;
+  }
+  s = acc;
+  return -1;
+}
+
+// Chunk 0 of a row, walked by one wave from 0 with its values xs[kMwChunk]
+// and tile records tr[64] in LDS: the first kMwSerialTiles tiles replayed
+// serially (the small running value doubles every few elements there: 1, 2,
+// 4, ... 32 for a flat row), then runs of tiles applied from their records,
+// the tiles straddling a binade replayed serially.  Touches no global
+// memory.  Returns the CDF hit (or -1) and leaves the running value in s.
+__device__ __forceinline__ long long mw_walk_chunk0(const float *xs, const MwRec *tr, bool cdf, float r,
+                                                    float &s) {
+  using namespace seq;
+  s = 0.0f;
+  long long found = -1;
+  {
+    const float4 *h4 = reinterpret_cast<const float4 *>(xs);
+    float xh[kMwSerialTiles * kMwTile];
+#pragma unroll
+    for (int k = 0; k < kMwSerialTiles * kMwTile / 4; ++k) {
+      const float4 q = h4[k];
+      xh[4 * k] = q.x;
+      xh[4 * k + 1] = q.y;
+      xh[4 * k + 2] = q.z;
+      xh[4 * k + 3] = q.w;
+    }
+#pragma unroll
+    for (int t = 0; t < kMwSerialTiles; ++t)
+      if (found < 0) found = mw_replay16(xh + t * kMwTile, (long long)t * kMwTile, s, cdf, r);
+  }
+  if (found < 0) {
+    auto item0 = [&](int i, int &reg) -> Inc {
+      const MwRec q = tr[kMwSerialTiles + i];
+      reg = q.reg;
+      return q.pad ? Inc{kBad, kBad} : Inc{q.e, q.o};
+    };
+    auto desc0 = [&](int i0, float &s2) -> long long {
+      const int i = kMwSerialTiles + i0;
+      const float4 *x4 = reinterpret_cast<const float4 *>(xs + i * kMwTile);
+      float x[kMwTile];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float4 q = x4[k];
+        x[4 * k] = q.x;
+        x[4 * k + 1] = q.y;
+        x[4 * k + 2] = q.z;
+        x[4 * k + 3] = q.w;
+      }
+      return mw_replay16(x, (long long)i * kMwTile, s2, cdf, r);
+    };
+    found = walk(kMwChunkTiles - kMwSerialTiles, s, cdf, r, item0, desc0);
+  }
+  return found;
+}
+
 // Chunks per wave of mw_first_kernel: two, so that the launch has B * NC / 2
 // waves (4032 at C2) and every wave is resident from the start -- with one
 // chunk per wave (8064 waves, against about 7 resident per SIMD) the last
@@ -1169,8 +1269,13 @@ constexpr int kMwChunksPerWG = (kMwNT / 64) * kMwCPW;
 // chunk sums of t (the CDF pass of a plain draw, or of the fallback, starts
 // from them); a residual job also stores those of max(0, t - d), finds its
 // chunks' entry values by look-back (both chunks' own sums published first),
-// and writes the sum pass's records (mw_records_chunk).
+// and writes the sum pass's records (mw_records_chunk).  The wave holding
+// chunk 0 then walks it (the walk's slowest chunk: its small running value
+// crosses a binade every few elements) and stores the exact running value
+// after it, so the sum pass's walk starts at chunk 1.
 __global__ __launch_bounds__(kMwNT) void mw_first_kernel(Args a, int decide) {
+  __shared__ __align__(16) float xs0[kMwChunk];  // chunk 0's values and tile records
+  __shared__ MwRec tr0[kMwChunkTiles];
   const int b = blockIdx.y, lane = threadIdx.x & 63;
   const int c0 = kMwCPW * (blockIdx.x * (kMwNT / 64) + (threadIdx.x >> 6));
   MwJob j;
@@ -1232,11 +1337,19 @@ __global__ __launch_bounds__(kMwNT) void mw_first_kernel(Args a, int decide) {
   unsigned long long *fl = a.flags + (long long)b * a.NC;
   if (two && lane == 0) lb_store(fl + c0 + 1, kLbAgg | f2u(sx[1]));  // before c0's look-back
   const float E0 = mw_lookback(a, b, c0, sx[0]);
-  mw_records_chunk(a, b, c0, kPassSum, j, E0, x[0]);
-  if (!two) return;
-  const float E1 = E0 + sx[0];
-  if (lane == 0) lb_store(fl + c0 + 1, kLbIncl | f2u(E1 + sx[1]));
-  mw_records_chunk(a, b, c0 + 1, kPassSum, j, E1, x[1]);
+  const bool walk0 = c0 == 0;  // wave-uniform
+  mw_records_chunk(a, b, c0, kPassSum, j, E0, x[0], walk0 ? tr0 : nullptr, walk0 ? xs0 : nullptr);
+  if (two) {
+    const float E1 = E0 + sx[0];
+    if (lane == 0) lb_store(fl + c0 + 1, kLbIncl | f2u(E1 + sx[1]));
+    mw_records_chunk(a, b, c0 + 1, kPassSum, j, E1, x[1]);
+  }
+  if (walk0) {
+    wave_sync();
+    float s0;
+    mw_walk_chunk0(xs0, tr0, false, 0.0f, s0);
+    if (lane == 0) a.s0[b] = s0;
+  }
 }
 
 constexpr int kMwWin = 256;  // chunk records staged in LDS at a time
@@ -1267,13 +1380,6 @@ struct MwWalkLds {
   alignas(16) float xs[kMwChunk];
 };
 
-// Orders one wave's LDS accesses (a wave's LDS operations complete in issue
-// order, so this only keeps the compiler from moving accesses across it).
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // The exact walk of job b's row for one pass, by the calling wave alone: it
 // synchronises only itself, so the other waves of its work-group can wait at
@@ -1281,9 +1387,11 @@ __device__ __forceinline__ void wave_sync() {
 // fallback flag; CDF pass: the drawn index, and the outputs in cpp mode) and
 // returns the final running value.  use_cache = false ignores the cached
 // serial tiles (another work-group may still be filling a slot); the walk
-// then reads those tiles' values from the row.
+// then reads those tiles' values from the row.  pre0: chunk 0 was already
+// walked (mw_walk_chunk0), ending at running value s0 with hit found0.
 __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const MwJob &j,
-                                         const MwElem &e, MwWalkLds &L, bool use_cache = true) {
+                                         const MwElem &e, MwWalkLds &L, bool use_cache = true,
+                                         bool pre0 = false, float s0 = 0.0f, long long found0 = -1) {
   using namespace seq;
   MwChunk *cr = L.cr;
   MwRec *tr = L.tr;
@@ -1296,10 +1404,10 @@ __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const M
   const MwRec *trec = a.trec + rowrec * a.NC * kMwChunkTiles;
 
   // One round of loads before the first wait: chunk 0's values and tile
-  // records, the first window of chunk records, every cache slot (all
-  // written by the records for active jobs; in-bounds, unused otherwise) and
-  // the cache count.
-  {
+  // records (unless chunk 0 was walked already), the first window of chunk
+  // records, every cache slot (all written by the records for active jobs;
+  // in-bounds, unused otherwise) and the cache count.
+  if (!pre0) {
     const float4 *src = reinterpret_cast<const float4 *>(a.x0 + rowrec * kMwChunk + lane * kMwTile);
     float4 *dst = reinterpret_cast<float4 *>(xs + lane * kMwTile);
 #pragma unroll
@@ -1337,32 +1445,8 @@ __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const M
     dma16(trec + (long long)cp * kMwChunkTiles + lane, (CFA_LDS void *)pft[p]);
   }
 
-  // Serial replay of a tile's 16 values from s (CDF: first hit index).  The
-  // running value never decreases (x >= 0), so the first i with r <= s_i is
-  // searched only in a tile whose last partial sum reaches r.
   auto replay16 = [&](const float *x, long long i0, float &s) -> long long {
-    float ps[kMwTile];
-    float acc = s;
-#pragma unroll
-    for (int k = 0; k < kMwTile; ++k) {
-      acc = acc + x[k];
-      ps[k] = acc;
-    }
-    if (cdf && r <= acc) {
-      // static indices only: a dynamically indexed ps[] would live in scratch
-      int k = kMwTile - 1;
-      float sk = ps[kMwTile - 1];
-#pragma unroll
-      for (int q = kMwTile - 2; q >= 0; --q) {
-        const bool h = r <= ps[q];
-        k = h ? q : k;
-        sk = h ? ps[q] : sk;
-      }
-      s = sk;
-      return i0 + k;
-    }
-    s = acc;
-    return -1;
+    return mw_replay16(x, i0, s, cdf, r);
   };
   // values of tile `tile`: the cache when the records stored them
   auto serial = [&](long long tile, float &s) -> long long {
@@ -1379,49 +1463,10 @@ __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const M
     return replay16(x, tile * kMwTile, s);
   };
 
-  // chunk 0: its first kMwSerialTiles tiles replayed serially (the small
-  // running value doubles every few elements there: 1, 2, 4, ... 32 for a
-  // flat row), then runs of tiles applied from their records, the tiles
-  // straddling a binade replayed serially from LDS
-  float s = 0.0f;
-  long long found = -1;
-  {
-    const float4 *h4 = reinterpret_cast<const float4 *>(xs);
-    float xh[kMwSerialTiles * kMwTile];
-#pragma unroll
-    for (int k = 0; k < kMwSerialTiles * kMwTile / 4; ++k) {
-      const float4 q = h4[k];
-      xh[4 * k] = q.x;
-      xh[4 * k + 1] = q.y;
-      xh[4 * k + 2] = q.z;
-      xh[4 * k + 3] = q.w;
-    }
-#pragma unroll
-    for (int t = 0; t < kMwSerialTiles; ++t)
-      if (found < 0) found = replay16(xh + t * kMwTile, (long long)t * kMwTile, s);
-  }
-  if (found < 0) {
-    auto item0 = [&](int i, int &reg) -> Inc {
-      const MwRec q = tr[kMwSerialTiles + i];
-      reg = q.reg;
-      return q.pad ? Inc{kBad, kBad} : Inc{q.e, q.o};
-    };
-    auto desc0 = [&](int i0, float &s2) -> long long {
-      const int i = kMwSerialTiles + i0;
-      const float4 *x4 = reinterpret_cast<const float4 *>(xs + i * kMwTile);
-      float x[kMwTile];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float4 q = x4[k];
-        x[4 * k] = q.x;
-        x[4 * k + 1] = q.y;
-        x[4 * k + 2] = q.z;
-        x[4 * k + 3] = q.w;
-      }
-      return replay16(x, (long long)i * kMwTile, s2);
-    };
-    found = walk(kMwChunkTiles - kMwSerialTiles, s, cdf, r, item0, desc0);
-  }
+  // chunk 0, unless it was walked already
+  float s = s0;
+  long long found = found0;
+  if (!pre0) found = mw_walk_chunk0(xs, tr, cdf, r, s);
   wait_vmcnt<0>();
   wave_sync();
 
@@ -1554,6 +1599,7 @@ __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const M
 constexpr int kMwTailNT = 1024;
 constexpr int kMwTailWaves = kMwTailNT / 64;
 constexpr int kMwTailWGs = 4;
+constexpr int kMwTailWorkers = kMwTailWGs * kMwTailWaves - 1;  // every wave but the walker
 constexpr long kMwTailSpins = 1l << 15;  // s_sleep(2) polls: about 2 ms
 constexpr unsigned long long kTsyncSet = 1ull << 63;  // a.tsync[2 b]: S is there
 
@@ -1600,7 +1646,8 @@ __global__ __launch_bounds__(kMwTailNT) void mw_tail_kernel(Args a) {
   if (resid) {
     if (part == 0) {
       if (wave == 0) {
-        const float S = mw_walk(a, b, kPassSum, j, mw_elem(a, b, j, kPassSum), L);
+        // chunk 0 was walked by the first pass (a.s0)
+        const float S = mw_walk(a, b, kPassSum, j, mw_elem(a, b, j, kPassSum), L, true, true, a.s0[b]);
         if (lane == 0) {
           sS = S;
           __hip_atomic_store(ts, kTsyncSet | f2u(S), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -1627,25 +1674,39 @@ __global__ __launch_bounds__(kMwTailNT) void mw_tail_kernel(Args a) {
   const MwElem e = mw_elem_r(a, b, j, kPassCdf, r);
   // approximate entry value of chunk c on the CDF pass's scale (a residual
   // job whose sum fell to the fallback draws from t: t's own chunk sums)
-  auto entry = [&](int c) -> float {
+  auto entry = [&](int c) __attribute__((always_inline)) -> float {
     if (resid && e.fn == 2) return mw_entry_prefix(a.csum_t + (long long)b * a.NC, c);
     return (e.fn == 1) ? Es[c] / e.S : Es[c];
   };
-  // part p's share: chunks 16 p + wave, then every 16 kMwTailWGs further; a
-  // chunk surely past u gets a "skipped" record and no loads
-  auto share = [&](int p) {
-    for (int c = p * kMwTailWaves + wave; c < a.NC; c += kMwTailWGs * kMwTailWaves) {
-      const float E0 = entry(c);
-      if (mw_skip(kPassCdf, j, E0)) {
-        mw_write_skipped(a, (long long)kPassCdf * a.B + b, c);
-        continue;
-      }
-      float x[kMwTile];
-      mw_tile_values(a, e, (long long)c * kMwChunkTiles + lane, x);
-      mw_records_chunk(a, b, c, kPassCdf, j, E0, x);
+  // records of chunk c; a chunk surely past u gets a "skipped" record and no
+  // loads.  Chunk 0 (never skipped: its entry value is 0) also goes to the
+  // walker's LDS.
+  auto records = [&](int c) __attribute__((always_inline)) {
+    const float E0 = entry(c);
+    if (mw_skip(kPassCdf, j, E0)) {
+      mw_write_skipped(a, (long long)kPassCdf * a.B + b, c);
+      return;
     }
+    float x[kMwTile];
+    mw_tile_values(a, e, (long long)c * kMwChunkTiles + lane, x);
+    mw_records_chunk(a, b, c, kPassCdf, j, E0, x, c == 0 ? L.tr : nullptr, c == 0 ? L.xs : nullptr);
   };
-  share(part);
+  // worker gw = 16 part + wave (1 .. 16 kMwTailWGs - 1) writes chunks gw,
+  // gw + kMwTailWorkers, ...; the walker (gw = 0) writes chunk 0 and walks it
+  // at once, while the workers write the rest
+  auto share_of = [&](int gw) __attribute__((always_inline)) {
+    for (int c = gw; c < a.NC; c += kMwTailWorkers) records(c);
+  };
+  const int gw = part * kMwTailWaves + wave;
+  float s0 = 0.0f;
+  long long found0 = -1;
+  if (gw == 0) {
+    records(0);
+    wave_sync();
+    found0 = mw_walk_chunk0(L.xs, L.tr, true, j.u, s0);
+  } else {
+    share_of(gw);
+  }
   if (part != 0) {
     // every wave's record stores complete, then one release for the part
     wait_vmcnt<0>();
@@ -1670,10 +1731,10 @@ __global__ __launch_bounds__(kMwTailNT) void mw_tail_kernel(Args a) {
   __syncthreads();
   const bool all_in = sok != 0;
   if (!all_in) {
-    for (int p = 1; p < kMwTailWGs; ++p) share(p);
+    for (int p = 1; p < kMwTailWGs; ++p) share_of(p * kMwTailWaves + wave);
     __syncthreads();
   }
-  if (wave == 0) mw_walk(a, b, kPassCdf, j, e, L, all_in);
+  if (wave == 0) mw_walk(a, b, kPassCdf, j, e, L, all_in, true, s0, found0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1913,7 +1974,7 @@ constexpr int kHeadPositions = 3;
 // Workspace layout (each region 256-byte aligned).
 struct WsLayout {
   size_t part, apart, rawtok, dec, ufin, jobs, res, csum_x, csum_t, crec, trec, badcnt, bad, x0, flags,
-      tsync, total;
+      tsync, s0, total;
 };
 
 static WsLayout ws_layout(int B, int K, int V, int mode) {
@@ -1945,6 +2006,7 @@ static WsLayout ws_layout(int B, int K, int V, int mode) {
   L.x0 = take(mw ? 2 * (size_t)B * kMwChunk * sizeof(float) : 0);
   L.flags = take(mw ? (size_t)B * NC * sizeof(unsigned long long) : 0);
   L.tsync = take(2 * (size_t)B * sizeof(unsigned long long));
+  L.s0 = take((size_t)B * sizeof(float));
   L.total = o;
   return L;
 }
@@ -2063,6 +2125,7 @@ static int run_pipeline(Args &a, bool vec, void *workspace, hipStream_t st, floa
   a.x0 = (float *)(ws + L.x0);
   a.flags = (unsigned long long *)(ws + L.flags);
   a.tsync = (unsigned long long *)(ws + L.tsync);
+  a.s0 = (float *)(ws + L.s0);
   // the first statistics pass zeroes the look-back words, cache counters and
   // tail synchronisation words; without one (probabilities input) a small
   // kernel does
