@@ -1574,12 +1574,14 @@ __device__ __forceinline__ float mw_walk(const Args &a, int b, int pass, const M
 
 // Everything after the first exact pass, kMwTailWGs work-groups ("parts")
 // of kMwTailNT threads per job:
-//   1. part 0's wave 0 walks the sum pass (residual draws) and publishes S;
-//   2. every part writes its share of the CDF pass's records (chunk c goes
-//      to part (c / 16) % kMwTailWGs, wave c % 16), from entry values that
-//      one wave per part scans from the stored chunk sums once;
-//   3. the other parts report their shares done, and part 0's wave 0 walks
-//      the CDF pass.
+//   1. part 0's wave 0 (the walker) walks the sum pass (residual draws)
+//      from chunk 1 on (the first pass walked chunk 0) and publishes S;
+//   2. the walker writes the CDF pass's records of chunk 0 and walks it;
+//      meanwhile the other waves of the job write the records of chunks
+//      1 .. NC - 1 (chunk c to wave (c - 1) % 63 + 1 of the job's 64), from
+//      entry values that one wave per part scans from the stored chunk sums;
+//   3. the other parts report their shares done, and the walker walks the
+//      rest of the CDF pass.
 // A job's stages follow each other directly instead of in three launches
 // (walk, records, walk), each of which waited for the slowest job of the
 // previous one.
