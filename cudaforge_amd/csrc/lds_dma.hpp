@@ -27,6 +27,13 @@ __device__ __forceinline__ void dma16(const void *src, CFA_LDS void *lds) {
                : "memory");
 }
 
+// The same with a wave-uniform 64-bit base in SGPRs and a per-lane 32-bit
+// byte offset: no 64-bit address arithmetic per transfer on the vector unit.
+__device__ __forceinline__ void dma16_s(const void *sbase, uint32_t voff, CFA_LDS void *lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory");
+}
+
 // Work-group barrier without the release/acquire fences of __syncthreads
 // (those would wait for every outstanding transfer); the empty asm statements
 // keep the compiler from moving memory accesses across it.

@@ -199,14 +199,6 @@ __device__ __forceinline__ void issue_tile(const Args &a, const long long *gtab,
   }
 }
 
-// One 16-byte-per-lane transfer with a wave-uniform 64-bit base (SGPRs) and
-// a per-lane 32-bit byte offset: no per-transfer address arithmetic on the
-// vector unit.
-__device__ __forceinline__ void dma16_s(const void *sbase, uint32_t voff, CFA_LDS void *lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
-               : "memory");
-}
-
 // Per-lane byte offsets, within their 16-key group, of this lane's K and V
 // transfers (issue_tile's rows and chunks) for a tile that lies wholly below
 // nkeys, where no position is clamped: the same for every such tile.

@@ -107,16 +107,26 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 // low halves of the bytes of w & 0x0f0f0f0f and odd ones of
 // (w >> 4) & 0x0f0f0f0f, so each converts with one byte-to-float
 // instruction; each pair packs with one conversion.
+//
+// Byte P of v as a float: v_cvt_f32_ubyte<P>, written out because the
+// compiler otherwise extracts each masked nibble with a bitfield extract
+// before converting byte 0 (12 more vector instructions per slice).
+template <int P>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) {
+  float r;
+  asm("v_cvt_f32_ubyte%2 %0, %1" : "=v"(r) : "v"(v), "i"(P));
+  return r;
+}
+template <int P>
+__device__ __forceinline__ uint32_t dequant_pair(uint32_t lo, uint32_t hi, float s, float c) {
+  const float f0 = __builtin_fmaf(ubyte_f32<P>(lo), s, c);
+  const float f1 = __builtin_fmaf(ubyte_f32<P>(hi), s, c);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{f0, f1}, bf16x2));
+}
 __device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float c) {
   const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-  uint32_t o[4];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const float f0 = __builtin_fmaf((float)((lo >> (8 * p)) & 0xffu), s, c);
-    const float f1 = __builtin_fmaf((float)((hi >> (8 * p)) & 0xffu), s, c);
-    o[p] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{f0, f1}, bf16x2));
-  }
-  return make_uint4(o[0], o[1], o[2], o[3]);
+  return make_uint4(dequant_pair<0>(lo, hi, s, c), dequant_pair<1>(lo, hi, s, c),
+                    dequant_pair<2>(lo, hi, s, c), dequant_pair<3>(lo, hi, s, c));
 }
 
 // vmcnt(N) lgkmcnt(0)
@@ -177,7 +187,7 @@ __global__ __launch_bounds__(kNT, 1) void w4mm_kernel(Args a) {
     for (int jj = 0; jj < kAX; ++jj) {
       const int j = 2 * h + jj;
       const uint32_t off = aoffs[j] + (((ahi >> j) & 1u) ? k1 : k0);
-      dma16(a.A + off, (CFA_LDS void *)(dst + 1024 * (wave * kAXS + j)));
+      dma16_s(a.A, 2u * off, (CFA_LDS void *)(dst + 1024 * (wave * kAXS + j)));  // M * K < 2^31
     }
   };
   // the word-ring transfer of each wave: waves 0-3 packed row w of the slice
@@ -186,13 +196,13 @@ __global__ __launch_bounds__(kNT, 1) void w4mm_kernel(Args a) {
   // same bytes to the same place), so that every wave issues one word-ring
   // transfer and then kAX A transfers per iteration
   const int ww = wave >= 5 ? 0 : wave;
-  const uint32_t *qsrc = a.q + (long long)(ww & 3) * a.N + n0 + 4 * lane;
+  const uint32_t qoff = 4u * (uint32_t)((ww & 3) * a.N + n0 + 4 * lane);  // bytes from the slice's row 0
   const __half *ssrc = (lane >= 32 && a.z ? a.z : a.s) + n0 + 8 * (lane & 31);
   auto issue_w = [&](int r) {
     uint8_t *dst = wring + (((r % kWSlots) + kWSlots) % kWSlots) * kWSlot;
     const int k0 = abs_slice(r) * kSK;
     if (ww < 4)
-      dma16(qsrc + (long long)(k0 / 8) * a.N, (CFA_LDS void *)(dst + 1024 * ww));
+      dma16_s(a.q + (long long)(k0 / 8) * a.N, qoff, (CFA_LDS void *)(dst + 1024 * ww));
     else
       dma16(ssrc + (long long)(k0 / a.group) * a.N, (CFA_LDS void *)(dst + kQBytes));
   };
