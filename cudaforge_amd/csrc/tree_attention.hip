@@ -406,6 +406,13 @@ __device__ __forceinline__ void mfma_phase(const Lane<D> &ln, const uint8_t *Kne
   f32x4 negb[kQT];
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt) negb[qt] = f32x4{-b[qt], -b[qt], -b[qt], -b[qt]};
+  // the column sums first: they read no LDS, so they cover the latency of
+  // the phase's first operand reads (about 1.5%)
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt)
+      lacc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, P.p[qt][blk], lacc[qt], 0, 0, 0);
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
@@ -419,11 +426,6 @@ __device__ __forceinline__ void mfma_phase(const Lane<D> &ln, const uint8_t *Kne
         o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, P.p[qt][blk], o[qt][dt], 0, 0, 0);
     }
   }
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt)
-      lacc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, P.p[qt][blk], lacc[qt], 0, 0, 0);
 #pragma unroll
   for (int kk = 0; kk < D / 32; ++kk)
 #pragma unroll
