@@ -264,6 +264,23 @@ def _time_launches(fn, reps, names):
     return out
 
 
+def _warm_up(fn, seconds=0.3, min_calls=40):
+    """Call fn() in rounds of 20 until at least min_calls calls and `seconds`
+    of wall time have passed: a leg's first calls run up to 20% slower than
+    its later ones (tree attention: 97 against 81 us per call after 40
+    warm-up calls in a fresh process)."""
+    import torch
+
+    torch.cuda.synchronize()
+    t_end = time.perf_counter() + seconds
+    n = 0
+    while n < min_calls or time.perf_counter() < t_end:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        n += 20
+
+
 def tree_attention_leg(dev, reps=20):
     """B=16, 63-node binary tree, 32 q / 8 KV heads,
     head_dim 128, context 4096, page 16, random page table, bf16 N(0,1)."""
@@ -294,17 +311,7 @@ def tree_attention_leg(dev, reps=20):
     def run():
         tree_attention(q, kp, vp, bt, ctx, mt, max_keys=C + N, out=out, workspace=ws)
 
-    # steady state: a leg's first calls run up to 20% slower than its later
-    # ones (97 against 81 us per call after 40 warm-up calls in a fresh
-    # process); warm up for at least 0.3 s of calls
-    torch.cuda.synchronize()
-    t_end = time.perf_counter() + 0.3
-    n = 0
-    while n < 40 or time.perf_counter() < t_end:
-        for _ in range(20):
-            run()
-        torch.cuda.synchronize()
-        n += 20
+    _warm_up(run)
     ms = _time_launches(run, reps, ("tree_attn", "tree_attn_merge"))
     t = (ms["tree_attn"] + ms["tree_attn_merge"]) * 1e-3
     # the whole call on its stream, back to back (adds the dispatch gap
@@ -437,8 +444,7 @@ def w4a16_gemm_leg(dev, reps=20):
                      ("fused_then_silu_mul_us", fused_then_silu_mul)]
         row = {}
         for label, fn in legs:
-            for _ in range(3):
-                fn()
+            _warm_up(fn, seconds=0.2, min_calls=20)
             stream = torch.cuda.current_stream(dev)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
