@@ -592,9 +592,13 @@ __global__ __launch_bounds__(kNT) void tree_attn_kernel(Args a) {
       } else {
         block_barrier();
       }
+      // the SIMD's other wave is in its VALU phase meanwhile: the MFMA
+      // phase's issue goes first, its VALU work fills the MFMAs' shadow
+      __builtin_amdgcn_s_setprio(1);
       if (busy)
         mfma_phase(ln, kring + ((t + 1 - t0) % kKStages) * kTileBytes,
                  vring + ((t - t0) % kVStages) * kTileBytes, sm.b, P, S, o, lacc);
+      __builtin_amdgcn_s_setprio(0);
     }
     if (!lag) block_barrier();
   }
